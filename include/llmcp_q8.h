@@ -1,0 +1,263 @@
+/*
+ * llmcp_q8.h -- C ABI of the MI355X (gfx950) Q8_0 quantized linear path.
+ *
+ * This library replaces the loop nests that llmcp's matmul lowering hook
+ * emits for `weight_format = "q8_0_p4"`:
+ *
+ *   emitQ8PackedDecodeMatmul / emitQ8PackedMatmul / emitQ8PackedScalarMatmul
+ *     include/llmcp/Dialect/LLMCP/Transforms/MatmulLoweringInternal.h:22-37
+ *   dispatched by lowerMatmulInternal
+ *     lib/Dialect/LLMCP/Transforms/MatmulLoweringCommon.cpp:492-508
+ *
+ * The hook would emit `func.call @llmcp_q8_*` with llvm.emit_c_interface, so
+ * generated code calls the `_mlir_ciface_llmcp_q8_*` symbols below with
+ * memref descriptors laid out as the runtime's MemRef<T,N>
+ * (include/llmcp/Runtime/AotRuntime.h:52-58).  Everything is plain C: no
+ * torch, no HIP types in signatures (streams travel as `void *`).
+ *
+ * Conventions
+ *  - Every entry returns an int status (LLMCP_Q8_OK == 0).  The reference
+ *    hook "declines" by returning a null Value (LowerToLinalg.cpp:161-166,
+ *    :745-750); here that is LLMCP_Q8_DECLINED and the caller falls back.
+ *    llmcp_q8_last_error() gives a thread-local message for the last failure.
+ *    No C++ exception crosses this boundary.
+ *  - Activation and output descriptors point to device memory (HBM).  Weight
+ *    descriptors may point either into a host arena that was uploaded with
+ *    llmcp_q8_upload_arena / llmcp_q8_upload_p4, or at a device p4 buffer
+ *    registered with llmcp_q8_register_device_p4; the library translates the
+ *    address to its device-resident copy (registry filled at upload).
+ *  - Calls are asynchronous on the context's stream.  One host thread drives
+ *    one context; calls on one context must not overlap (shared workspace).
+ */
+#ifndef LLMCP_Q8_H
+#define LLMCP_Q8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Version of this C ABI.  The model ABI of the AOT library
+ * (llmcp_model_abi_version() == 2, include/llmcp/Support/AotAbi.h:12) is not
+ * changed by this library. */
+#define LLMCP_Q8_ABI_VERSION 1
+
+enum llmcp_q8_status {
+  LLMCP_Q8_OK = 0,
+  LLMCP_Q8_DECLINED = 1,  /* unsupported shape/format: caller falls back */
+  LLMCP_Q8_EINVAL = 2,    /* bad argument (null, inconsistent sizes) */
+  LLMCP_Q8_ENOTFOUND = 3, /* weight address not in any uploaded tensor */
+  LLMCP_Q8_EHIP = 4,      /* HIP runtime error */
+  LLMCP_Q8_EFORMAT = 5,   /* packed-weights header or manifest invalid */
+  LLMCP_Q8_EIO = 6,       /* file open/map failure */
+  LLMCP_Q8_ENOMEM = 7     /* device allocation failed */
+};
+
+enum llmcp_q8_activation { LLMCP_Q8_ACT_NONE = 0, LLMCP_Q8_ACT_SILU = 1 };
+
+/* llmcp.execution_mode (LowerToLinalg.cpp:40-52). */
+enum llmcp_q8_mode { LLMCP_Q8_PREFILL = 0, LLMCP_Q8_DECODE = 1 };
+
+/* MemRef<T,N> of include/llmcp/Runtime/AotRuntime.h:52-58. */
+typedef struct {
+  float *base;
+  float *data;
+  int64_t offset;
+  int64_t sizes[2];
+  int64_t strides[2];
+} llmcp_memref_f32_2d;
+
+typedef struct {
+  int8_t *base;
+  int8_t *data;
+  int64_t offset;
+  int64_t sizes[1];
+  int64_t strides[1];
+} llmcp_memref_i8_1d;
+
+typedef struct {
+  int64_t *base;
+  int64_t *data;
+  int64_t offset;
+  int64_t sizes[1];
+  int64_t strides[1];
+} llmcp_memref_i64_1d;
+
+typedef struct llmcp_q8_ctx llmcp_q8_ctx;
+
+/* ---------------------------------------------------------------- core -- */
+
+int32_t llmcp_q8_abi_version(void);
+const char *llmcp_q8_last_error(void);
+
+/* Creates a context on HIP device `device` with its own non-blocking stream
+ * (default priority).  Replaces the runtime's per-process state of
+ * AotRuntime::init (lib/Runtime/AotRuntime.cpp:39-66). */
+int llmcp_q8_ctx_create(int device, llmcp_q8_ctx **out);
+int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx);
+/* Use a caller-owned hipStream_t (NULL restores the context's own stream). */
+int llmcp_q8_ctx_set_stream(llmcp_q8_ctx *ctx, void *hip_stream);
+void *llmcp_q8_ctx_stream(llmcp_q8_ctx *ctx);
+int llmcp_q8_ctx_synchronize(llmcp_q8_ctx *ctx);
+/* Context used by the _mlir_ciface_* entries (set by the AOT runtime). */
+int llmcp_q8_set_default_ctx(llmcp_q8_ctx *ctx);
+
+/* ------------------------------------------------------------- weights -- */
+
+/* Uploads one q8_0_p4 tensor [rows, cols] whose packed bytes live in host
+ * memory (e.g. inside a mmapped arena) and repacks it once on the device.
+ * Later weight descriptors whose data lies inside [host_p4, host_p4+bytes)
+ * resolve to this copy.  Shape rule isQ8PackedShape
+ * (include/llmcp/Support/Q8PackedLayout.h:38-42): rows % 8 == 0,
+ * cols % 32 == 0.  `repack_ms` (nullable) receives the device repack time. */
+int llmcp_q8_upload_p4(llmcp_q8_ctx *ctx, const void *host_p4, int64_t rows,
+                       int64_t cols, float *repack_ms);
+
+/* Same for a p4 tensor already in device memory (e.g. written by
+ * llmcp_q8_synthesize_p4).  The device buffer is registered under its own
+ * address and may be freed by the caller after this call returns. */
+int llmcp_q8_register_device_p4(llmcp_q8_ctx *ctx, const void *dev_p4,
+                                int64_t rows, int64_t cols, float *repack_ms);
+
+/* Drops the device copy registered under `key` (host or device address). */
+int llmcp_q8_release(llmcp_q8_ctx *ctx, const void *key);
+
+/* Validates a mapped LLMCPWGT file (include/llmcp/Support/PackedWeights.h,
+ * lib/Runtime/WeightArena.cpp:27-131 rules) and uploads every Q8_0 tensor.
+ * `file` is the whole mapping, header first.  Returns the number of Q8_0
+ * tensors uploaded through `num_q8` (nullable). */
+int llmcp_q8_upload_arena(llmcp_q8_ctx *ctx, const void *file,
+                          uint64_t file_bytes, int64_t *num_q8);
+
+/* Host-only validation of a mapped LLMCPWGT file with the same rules; no
+ * device is touched.  Counts all tensors and the Q8_0 ones (nullable). */
+int llmcp_q8_arena_inspect(const void *file, uint64_t file_bytes,
+                           int64_t *num_tensors, int64_t *num_q8);
+
+/* ------------------------------------------------------------ ops ------- */
+
+/* llmcp.linear with weight_format q8_0_p4 (LowerToLinalg.cpp:143-209):
+ * y[M,N] = act(x[M,K] . W[N,K]^T), x quantized per call to Q8_1 blocks.
+ * execution_mode DECODE requires M == 1 and runs the GEMV; PREFILL runs the
+ * int8-MFMA GEMM for any M.  activation: NONE or SILU
+ * (applyMatmulActivation, MatmulLoweringCommon.cpp:78-103). */
+int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                    const llmcp_memref_i8_1d *weight,
+                    llmcp_memref_f32_2d *output, int32_t activation,
+                    int32_t execution_mode);
+
+/* Fused SwiGLU hidden: h = silu(x . Wg^T) * (x . Wu^T), the pair
+ * `linear{activation=silu}` + `mul` that FuseSiluMul produces
+ * (FuseLinearActivations.cpp:27-43, LowerToLinalg.cpp:377-393). */
+int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                    const llmcp_memref_i8_1d *w_gate,
+                    const llmcp_memref_i8_1d *w_up,
+                    llmcp_memref_f32_2d *output, int32_t execution_mode);
+
+/* llmcp.lm_head (LowerToLinalg.cpp:729-765): f32 logits [M,V] over the tied
+ * table, plus the first-maximum index of the last row written to
+ * `argmax_dev` (device int64, nullable) -- the host std::max_element of
+ * llmcp-benchmark.cpp:51-54 fused into the kernel. */
+int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
+                     const llmcp_memref_i8_1d *table,
+                     llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
+                     int32_t execution_mode);
+
+/* llmcp.embedding with weight_format q8_0_p4 (emitQ8PackedEmbedding,
+ * LowerToLinalg.cpp:435-531): out[t, c] = f32(q(token_t, c)) * f32(d).
+ * Tokens outside [0, rows) produce a zero row and set the context's
+ * error flag (llmcp_q8_ctx_check). */
+int llmcp_q8_embedding(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
+                       const llmcp_memref_i8_1d *table,
+                       llmcp_memref_f32_2d *output);
+
+/* Activation quantizer Q8_1 (Q8Decode.cpp:83-120): qa_dev int8 [M,K] and
+ * sa_dev f32 [M,K/32], both dense row-major device buffers. */
+int llmcp_q8_quantize_activations(llmcp_q8_ctx *ctx,
+                                  const llmcp_memref_f32_2d *input,
+                                  int8_t *qa_dev, float *sa_dev);
+
+/* Per-block int32 dot products I[m][n][b] (Q8Decode.cpp:166-191) of the
+ * Q8_1-quantized input against the registered weight, into out_dev
+ * (device int32 [M,N,K/32]).  Exposes the exact integer stage. */
+int llmcp_q8_block_dots(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                        const llmcp_memref_i8_1d *weight, int32_t *out_dev);
+
+/* Reads and clears the device error flag (1 = an embedding token was out of
+ * range since the last check).  Synchronizes the stream. */
+int llmcp_q8_ctx_check(llmcp_q8_ctx *ctx, int32_t *flag);
+
+/* ---------------------------------------------------- offline packing -- */
+
+/* quantizeTensorQ8_0Packed (lib/Model/Quantization.cpp:165-214) on the host:
+ * [rows, cols] f32 -> rows*cols*34/32 bytes.  OpenMP over lane groups. */
+int llmcp_q8_pack_p4_host(const float *w, int64_t rows, int64_t cols,
+                          uint8_t *out);
+
+/* Same quantizer on the device for synthetic weights: w[r][c] =
+ * stddev * N(0,1) drawn from a counter-based generator keyed by (seed, r*cols+c)
+ * and written f32 to w_dev (nullable), then packed into p4_dev. */
+int llmcp_q8_synthesize_p4(llmcp_q8_ctx *ctx, uint64_t seed, int64_t rows,
+                           int64_t cols, float stddev, float *w_dev,
+                           void *p4_dev);
+
+/* Writes a single-file arena (PackedWeights.h layout, manifest of
+ * WeightPacker.cpp:126-160) holding the given q8_0_p4 tensors. */
+int llmcp_q8_write_arena(const char *path, int32_t count,
+                         const char *const *names, const int64_t *rows,
+                         const int64_t *cols, const void *const *p4);
+
+/* -------------------------------------------------- MLIR C interface ---- */
+
+/* What the edited lowering hook calls (func.call + llvm.emit_c_interface),
+ * on the default context.  Status as above. */
+int32_t _mlir_ciface_llmcp_q8_linear(llmcp_memref_f32_2d *input,
+                                     llmcp_memref_i8_1d *weight,
+                                     llmcp_memref_f32_2d *output,
+                                     int32_t activation,
+                                     int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
+                                     llmcp_memref_i8_1d *w_gate,
+                                     llmcp_memref_i8_1d *w_up,
+                                     llmcp_memref_f32_2d *output,
+                                     int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_lm_head(llmcp_memref_f32_2d *hidden,
+                                      llmcp_memref_i8_1d *table,
+                                      llmcp_memref_f32_2d *logits,
+                                      llmcp_memref_i64_1d *argmax,
+                                      int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_embedding(llmcp_memref_i64_1d *tokens,
+                                        llmcp_memref_i8_1d *table,
+                                        llmcp_memref_f32_2d *output);
+
+/* ------------------------------------------- device plumbing (host use) -- */
+/* Small helpers so hosts without a HIP toolchain (ctypes, cgo) can move data
+ * and time work on the context's stream. */
+
+int llmcp_q8_dev_alloc(llmcp_q8_ctx *ctx, uint64_t bytes, void **out);
+int llmcp_q8_dev_free(llmcp_q8_ctx *ctx, void *ptr);
+int llmcp_q8_memcpy_h2d(llmcp_q8_ctx *ctx, void *dst, const void *src,
+                        uint64_t bytes);
+int llmcp_q8_memcpy_d2h(llmcp_q8_ctx *ctx, void *dst, const void *src,
+                        uint64_t bytes);
+int llmcp_q8_memcpy_d2d(llmcp_q8_ctx *ctx, void *dst, const void *src,
+                        uint64_t bytes);
+int llmcp_q8_event_create(void **event);
+int llmcp_q8_event_destroy(void *event);
+int llmcp_q8_event_record(llmcp_q8_ctx *ctx, void *event);
+int llmcp_q8_event_elapsed_ms(void *start, void *stop, float *ms);
+/* Stream capture into a HIP graph and replay (launch-bound loops). */
+int llmcp_q8_graph_begin(llmcp_q8_ctx *ctx);
+int llmcp_q8_graph_end(llmcp_q8_ctx *ctx, void **graph_exec);
+int llmcp_q8_graph_launch(llmcp_q8_ctx *ctx, void *graph_exec);
+int llmcp_q8_graph_destroy(void *graph_exec);
+/* Bytes the device copy of a registered weight occupies (0 if unknown). */
+uint64_t llmcp_q8_device_bytes(llmcp_q8_ctx *ctx, const void *key);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLMCP_Q8_H */

@@ -1,0 +1,55 @@
+// q8_kernels.h -- host-side launchers of the gfx950 kernels (internal; the
+// public C ABI is include/llmcp_q8.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "q8_common.h"
+
+namespace llmcp_q8 {
+
+// p4 arena bytes (device) -> pass layout (device), once per tensor.
+hipError_t launch_repack(const uint8_t *p4, uint8_t *out, int64_t rows,
+                         int64_t cols, hipStream_t s);
+
+// Synthetic N(0, stddev^2) weights from a counter-based generator.
+hipError_t launch_synth(uint64_t seed, int64_t rows, int64_t cols,
+                        float stddev, float *w, hipStream_t s);
+
+// Device llmcp-pack: f32 [rows, cols] -> p4 bytes (Quantization.cpp:92-214).
+hipError_t launch_pack_p4(const float *w, int64_t rows, int64_t cols,
+                          uint8_t *p4, hipStream_t s);
+
+// Q8_1 activation quantizer: x [m, cols] (row stride ldx floats) ->
+// qa [m, ldq] int8 and sa [m, lds] f32, zero-filled up to blocks_pad blocks.
+hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
+                           int64_t cols, int8_t *qa, int64_t ldq, float *sa,
+                           int64_t lds, int64_t blocks_pad, hipStream_t s);
+
+struct GemvLaunch {
+  const float *x = nullptr;      // f32 input row (quantized in the prologue)
+  const int8_t *qa = nullptr;    // or: pre-quantized input (padded)
+  const float *sa = nullptr;
+  const uint8_t *w[2] = {nullptr, nullptr};  // pass-layout weights
+  float *y = nullptr;            // f32 output [rows]
+  int64_t rows = 0;              // N
+  int64_t cols = 0;              // K
+  int nmat = 1;                  // 2 = fused SwiGLU (gate, up)
+  int activation = 0;            // 0 none, 1 silu (nmat == 1 only)
+  ArgmaxState *argmax = nullptr; // non-null: fused argmax
+  int64_t *argmax_out = nullptr;
+};
+
+hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s);
+
+hipError_t launch_embedding(const int64_t *tokens, int64_t count,
+                            const uint8_t *table, int64_t rows, int64_t cols,
+                            float *out, int64_t ldo, int32_t *err_flag,
+                            hipStream_t s);
+
+hipError_t launch_block_dots(const int8_t *qa, int64_t ldq, int64_t m,
+                             const uint8_t *w, int64_t rows, int64_t cols,
+                             int32_t *out, hipStream_t s);
+
+}  // namespace llmcp_q8

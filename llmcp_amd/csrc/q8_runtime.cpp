@@ -1,0 +1,957 @@
+// q8_runtime.cpp -- host side of the MI355X Q8_0 linear path: context,
+// weight registry (host/device address -> device-resident repacked tensor),
+// LLMCPWGT arena loader, host packer and the C ABI of include/llmcp_q8.h.
+//
+// Reference interfaces replaced here:
+//   lowering hook      MatmulLoweringInternal.h:22-37, MatmulLoweringCommon.cpp:492-508
+//   arena loader       lib/Runtime/WeightArena.cpp:27-131, include/llmcp/Support/PackedWeights.h
+//   arena writer       lib/Model/WeightPacker.cpp:126-160, :164-274
+//   packer             lib/Model/Quantization.cpp:92-116, :165-214
+#include <hip/hip_runtime.h>
+#include <omp.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <mutex>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/llmcp_q8.h"
+#include "json_min.h"
+#include "q8_kernels.h"
+
+using namespace llmcp_q8;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(LLMCP_Q8_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                              \
+  do {                                             \
+    hipError_t e_ = (expr);                        \
+    if (e_ != hipSuccess) return hip_fail(e_, #expr); \
+  } while (0)
+
+struct Tensor {
+  uintptr_t key = 0;       // address callers pass in weight descriptors
+  uint64_t key_bytes = 0;  // p4 size: rows * cols * 34 / 32
+  uint8_t *dev = nullptr;  // pass layout, device
+  uint64_t dev_bytes = 0;
+  int64_t rows = 0;
+  int64_t cols = 0;
+};
+
+}  // namespace
+
+struct llmcp_q8_ctx {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  std::map<uintptr_t, Tensor> registry;  // by key
+  ArgmaxState *argmax = nullptr;
+  int32_t *err_flag = nullptr;
+  int8_t *qa = nullptr;  // activation scratch (quantized input)
+  float *sa = nullptr;
+  uint64_t qa_bytes = 0;
+  uint64_t sa_bytes = 0;
+  hipGraph_t capture = nullptr;
+};
+
+namespace {
+
+llmcp_q8_ctx *g_default_ctx = nullptr;
+
+int set_device(llmcp_q8_ctx *ctx) {
+  HIP_TRY(hipSetDevice(ctx->device));
+  return LLMCP_Q8_OK;
+}
+
+const Tensor *find_tensor(llmcp_q8_ctx *ctx, const void *addr) {
+  auto it = ctx->registry.find((uintptr_t)addr);
+  if (it == ctx->registry.end()) return nullptr;
+  return &it->second;
+}
+
+// Weight descriptor -> registered tensor, with the verifier's size rule
+// (LLMCPOps.cpp:57-65: size == N * (K + K/16)).
+int resolve_weight(llmcp_q8_ctx *ctx, const llmcp_memref_i8_1d *w,
+                   const Tensor **out) {
+  if (!w || !w->data) return fail(LLMCP_Q8_EINVAL, "null weight descriptor");
+  const void *addr = w->data + w->offset;
+  const Tensor *t = find_tensor(ctx, addr);
+  if (!t)
+    return fail(LLMCP_Q8_ENOTFOUND,
+                "weight %p is not an uploaded q8_0_p4 tensor", addr);
+  if (w->strides[0] != 1 || (uint64_t)w->sizes[0] != t->key_bytes)
+    return fail(LLMCP_Q8_DECLINED,
+                "q8_0_p4 weight size must be N * (K + (K/32)*2)");
+  *out = t;
+  return LLMCP_Q8_OK;
+}
+
+bool dense_rows(const llmcp_memref_f32_2d *d) {
+  return d && d->data && d->strides[1] == 1 && d->sizes[0] >= 0 &&
+         d->sizes[1] > 0 && (d->sizes[0] <= 1 || d->strides[0] >= d->sizes[1]);
+}
+
+int ensure_scratch(llmcp_q8_ctx *ctx, uint64_t qa_bytes, uint64_t sa_bytes) {
+  if (qa_bytes > ctx->qa_bytes) {
+    if (ctx->qa) HIP_TRY(hipFree(ctx->qa));
+    ctx->qa = nullptr;
+    ctx->qa_bytes = 0;
+    if (hipMalloc(&ctx->qa, qa_bytes) != hipSuccess)
+      return fail(LLMCP_Q8_ENOMEM, "activation scratch of %llu bytes",
+                  (unsigned long long)qa_bytes);
+    ctx->qa_bytes = qa_bytes;
+  }
+  if (sa_bytes > ctx->sa_bytes) {
+    if (ctx->sa) HIP_TRY(hipFree(ctx->sa));
+    ctx->sa = nullptr;
+    ctx->sa_bytes = 0;
+    if (hipMalloc(&ctx->sa, sa_bytes) != hipSuccess)
+      return fail(LLMCP_Q8_ENOMEM, "scale scratch of %llu bytes",
+                  (unsigned long long)sa_bytes);
+    ctx->sa_bytes = sa_bytes;
+  }
+  return LLMCP_Q8_OK;
+}
+
+// Repacks device p4 bytes into a new registry entry under `key`.
+int register_from_device_p4(llmcp_q8_ctx *ctx, const void *key,
+                            const uint8_t *dev_p4, int64_t rows, int64_t cols,
+                            float *repack_ms) {
+  Tensor t;
+  t.key = (uintptr_t)key;
+  t.rows = rows;
+  t.cols = cols;
+  t.key_bytes = (uint64_t)rows * (uint64_t)(cols / kBlock) * 34u;
+  t.dev_bytes = (uint64_t)device_bytes_for(rows, cols);
+  if (hipMalloc(&t.dev, t.dev_bytes) != hipSuccess)
+    return fail(LLMCP_Q8_ENOMEM, "device weight of %llu bytes",
+                (unsigned long long)t.dev_bytes);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (repack_ms) {
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    HIP_TRY(hipEventRecord(e0, ctx->stream));
+  }
+  hipError_t err = launch_repack(dev_p4, t.dev, rows, cols, ctx->stream);
+  if (err != hipSuccess) {
+    (void)hipFree(t.dev);
+    return hip_fail(err, "repack");
+  }
+  if (repack_ms) {
+    HIP_TRY(hipEventRecord(e1, ctx->stream));
+    HIP_TRY(hipEventSynchronize(e1));
+    HIP_TRY(hipEventElapsedTime(repack_ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+  auto old = ctx->registry.find(t.key);
+  if (old != ctx->registry.end()) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    (void)hipFree(old->second.dev);
+    ctx->registry.erase(old);
+  }
+  ctx->registry[t.key] = t;
+  return LLMCP_Q8_OK;
+}
+
+bool packable(int64_t rows, int64_t cols) {
+  // isQ8PackedShape (Q8PackedLayout.h:38-42).
+  return rows > 0 && cols > 0 && rows % 8 == 0 && cols % kBlock == 0;
+}
+
+uint32_t rd32(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+         ((uint32_t)p[3] << 24);
+}
+uint64_t rd64(const uint8_t *p) {
+  return (uint64_t)rd32(p) | ((uint64_t)rd32(p + 4) << 32);
+}
+void wr32(uint8_t *p, uint32_t v) {
+  for (int i = 0; i < 4; ++i) p[i] = (uint8_t)(v >> (8 * i));
+}
+void wr64(uint8_t *p, uint64_t v) {
+  for (int i = 0; i < 8; ++i) p[i] = (uint8_t)(v >> (8 * i));
+}
+
+// ---------------------------------------------------- host f16 and pack --
+
+uint16_t host_f32_to_f16(float value) {
+  uint32_t x;
+  std::memcpy(&x, &value, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t exp = (x >> 23) & 0xffu;
+  const uint32_t man = x & 0x7fffffu;
+  if (exp == 0xffu)
+    return (uint16_t)(sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u));
+  const int32_t e = (int32_t)exp - 112;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (exp == 0) return (uint16_t)sign;
+    const uint32_t full = man | 0x800000u;
+    const int shift = 14 - e;
+    if (shift > 24) return (uint16_t)sign;
+    uint32_t m = full >> shift;
+    const uint32_t rem = full & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (m & 1u))) ++m;
+    return (uint16_t)(sign | m);
+  }
+  uint32_t h = ((uint32_t)e << 10) | (man >> 13);
+  const uint32_t rem = man & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+  return (uint16_t)(sign | h);
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" {
+
+int32_t llmcp_q8_abi_version(void) { return LLMCP_Q8_ABI_VERSION; }
+
+const char *llmcp_q8_last_error(void) { return g_last_error.c_str(); }
+
+int llmcp_q8_ctx_create(int device, llmcp_q8_ctx **out) {
+  if (!out) return fail(LLMCP_Q8_EINVAL, "null output pointer");
+  *out = nullptr;
+  int count = 0;
+  HIP_TRY(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count)
+    return fail(LLMCP_Q8_EINVAL, "device %d out of range (%d devices)", device,
+                count);
+  auto *ctx = new llmcp_q8_ctx();
+  ctx->device = device;
+  int rc = set_device(ctx);
+  if (rc) {
+    delete ctx;
+    return rc;
+  }
+  hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return hip_fail(e, "hipStreamCreateWithFlags");
+  }
+  ctx->stream = ctx->own_stream;
+  if (hipMalloc(&ctx->argmax, sizeof(ArgmaxState)) != hipSuccess ||
+      hipMalloc(&ctx->err_flag, sizeof(int32_t)) != hipSuccess) {
+    llmcp_q8_ctx_destroy(ctx);
+    return fail(LLMCP_Q8_ENOMEM, "context workspace");
+  }
+  if (hipMemset(ctx->argmax, 0, sizeof(ArgmaxState)) != hipSuccess ||
+      hipMemset(ctx->err_flag, 0, sizeof(int32_t)) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess) {
+    llmcp_q8_ctx_destroy(ctx);
+    return fail(LLMCP_Q8_EHIP, "context workspace init");
+  }
+  *out = ctx;
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx) {
+  if (!ctx) return LLMCP_Q8_OK;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
+  if (ctx->stream && ctx->stream != ctx->own_stream)
+    (void)hipStreamSynchronize(ctx->stream);
+  for (auto &kv : ctx->registry) (void)hipFree(kv.second.dev);
+  if (ctx->argmax) (void)hipFree(ctx->argmax);
+  if (ctx->err_flag) (void)hipFree(ctx->err_flag);
+  if (ctx->qa) (void)hipFree(ctx->qa);
+  if (ctx->sa) (void)hipFree(ctx->sa);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+  if (g_default_ctx == ctx) g_default_ctx = nullptr;
+  delete ctx;
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_ctx_set_stream(llmcp_q8_ctx *ctx, void *hip_stream) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own_stream;
+  return LLMCP_Q8_OK;
+}
+
+void *llmcp_q8_ctx_stream(llmcp_q8_ctx *ctx) {
+  return ctx ? (void *)ctx->stream : nullptr;
+}
+
+int llmcp_q8_ctx_synchronize(llmcp_q8_ctx *ctx) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_set_default_ctx(llmcp_q8_ctx *ctx) {
+  g_default_ctx = ctx;
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_ctx_check(llmcp_q8_ctx *ctx, int32_t *flag) {
+  if (!ctx || !flag) return fail(LLMCP_Q8_EINVAL, "null argument");
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipMemcpyAsync(flag, ctx->err_flag, sizeof(int32_t),
+                         hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipMemsetAsync(ctx->err_flag, 0, sizeof(int32_t), ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+// ------------------------------------------------------------- weights --
+
+int llmcp_q8_upload_p4(llmcp_q8_ctx *ctx, const void *host_p4, int64_t rows,
+                       int64_t cols, float *repack_ms) {
+  if (!ctx || !host_p4) return fail(LLMCP_Q8_EINVAL, "null argument");
+  if (!packable(rows, cols))
+    return fail(LLMCP_Q8_DECLINED,
+                "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  const uint64_t bytes = (uint64_t)rows * (uint64_t)(cols / kBlock) * 34u;
+  uint8_t *staging = nullptr;
+  if (hipMalloc(&staging, bytes) != hipSuccess)
+    return fail(LLMCP_Q8_ENOMEM, "staging of %llu bytes",
+                (unsigned long long)bytes);
+  hipError_t e = hipMemcpyAsync(staging, host_p4, bytes, hipMemcpyHostToDevice,
+                                ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(staging);
+    return hip_fail(e, "upload");
+  }
+  rc = register_from_device_p4(ctx, host_p4, staging, rows, cols, repack_ms);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipFree(staging);
+  return rc;
+}
+
+int llmcp_q8_register_device_p4(llmcp_q8_ctx *ctx, const void *dev_p4,
+                                int64_t rows, int64_t cols, float *repack_ms) {
+  if (!ctx || !dev_p4) return fail(LLMCP_Q8_EINVAL, "null argument");
+  if (!packable(rows, cols))
+    return fail(LLMCP_Q8_DECLINED,
+                "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  rc = register_from_device_p4(ctx, dev_p4, (const uint8_t *)dev_p4, rows,
+                               cols, repack_ms);
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_release(llmcp_q8_ctx *ctx, const void *key) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  auto it = ctx->registry.find((uintptr_t)key);
+  if (it == ctx->registry.end())
+    return fail(LLMCP_Q8_ENOTFOUND, "no tensor registered at %p", key);
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  HIP_TRY(hipFree(it->second.dev));
+  ctx->registry.erase(it);
+  return LLMCP_Q8_OK;
+}
+
+uint64_t llmcp_q8_device_bytes(llmcp_q8_ctx *ctx, const void *key) {
+  if (!ctx) return 0;
+  const Tensor *t = find_tensor(ctx, key);
+  return t ? t->dev_bytes : 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+struct ArenaTensor {
+  std::string name;
+  std::string dtype;
+  const uint8_t *data;
+  std::vector<int64_t> shape;
+};
+
+// Arena validation follows PackedWeightsHeader::read (PackedWeights.h:36-56)
+// and Arena::load (WeightArena.cpp:27-131) rule for rule.
+int parse_arena(const void *file, uint64_t file_bytes,
+                std::vector<ArenaTensor> &out) {
+  if (!file) return fail(LLMCP_Q8_EINVAL, "null argument");
+  const uint8_t *f = (const uint8_t *)file;
+  if (file_bytes < 64 || std::memcmp(f, "LLMCPWGT", 8) != 0)
+    return fail(LLMCP_Q8_EFORMAT,
+                "invalid packed weights header; repack weights with llmcp-pack");
+  if (rd32(f + 8) != 1 || rd32(f + 12) != 64)
+    return fail(LLMCP_Q8_EFORMAT,
+                "unsupported packed weights format version or header size");
+  const uint64_t arena = rd64(f + 16), moff = rd64(f + 24), mbytes = rd64(f + 32);
+  if (arena < 64 || moff != arena || moff > file_bytes || mbytes == 0 ||
+      mbytes != file_bytes - moff)
+    return fail(LLMCP_Q8_EFORMAT, "invalid packed weights arena or manifest bounds");
+  json::Value root;
+  json::Parser parser((const char *)f + moff, (size_t)mbytes);
+  if (!parser.parse(root) || root.kind != json::Value::Object)
+    return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+  const json::Value *total = root.get("total_bytes");
+  const json::Value *header = root.get("header_bytes");
+  const json::Value *mode = root.get("quantization");
+  const json::Value *tensors = root.get("tensors");
+  if (!total || !total->is_int() || total->i < 0 || (uint64_t)total->i != arena ||
+      !header || !header->is_int() || header->i != 64 || !mode ||
+      !mode->is_string() || (mode->s != "none" && mode->s != "q8_0") ||
+      !tensors || tensors->kind != json::Value::Array || tensors->arr.empty())
+    return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+  if (mode->s == "q8_0") {
+    const json::Value *bs = root.get("block_size");
+    const json::Value *ql = root.get("quant_layout");
+    if (!bs || !bs->is_int() || bs->i != 32 || !ql || !ql->is_string() ||
+        ql->s != "q8_0_p4")
+      return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+  }
+  std::set<std::string> names;
+  std::vector<ArenaTensor> result;
+  for (const json::Value &e : tensors->arr) {
+    const json::Value *name = e.get("name");
+    const json::Value *offset = e.get("offset");
+    const json::Value *size = e.get("size");
+    const json::Value *dtype = e.get("dtype");
+    const json::Value *shape = e.get("shape");
+    if (e.kind != json::Value::Object || !name || !name->is_string() ||
+        name->s.empty() || !offset || !offset->is_int() || offset->i < 64 ||
+        offset->i % 64 || !size || !size->is_int() || size->i <= 0 || !dtype ||
+        !dtype->is_string() || !shape || shape->kind != json::Value::Array ||
+        shape->arr.empty())
+      return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+    const uint64_t begin = (uint64_t)offset->i, length = (uint64_t)size->i;
+    if (begin > arena || length > arena - begin)
+      return fail(LLMCP_Q8_EFORMAT, "tensor outside arena: %s", name->s.c_str());
+    uint64_t elements = 1;
+    std::vector<int64_t> dims;
+    for (const json::Value &d : shape->arr) {
+      if (!d.is_int() || d.i <= 0 ||
+          elements > std::numeric_limits<uint64_t>::max() / (uint64_t)d.i)
+        return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+      elements *= (uint64_t)d.i;
+      dims.push_back(d.i);
+    }
+    uint64_t unit;
+    if (dtype->s == "Q8_0") {
+      if (mode->s != "q8_0" || dims.size() != 2 || dims[1] % 32)
+        return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+      elements /= 32;
+      unit = 34;
+    } else if (dtype->s == "BF16") {
+      unit = 2;
+    } else if (dtype->s == "F32") {
+      unit = 4;
+    } else {
+      return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+    }
+    if (elements > std::numeric_limits<uint64_t>::max() / unit ||
+        elements * unit != length)
+      return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+    if (!names.insert(name->s).second)
+      return fail(LLMCP_Q8_EFORMAT, "invalid embedded weight manifest");
+    if (dtype->s == "Q8_0" && !packable(dims[0], dims[1]))
+      return fail(LLMCP_Q8_EFORMAT, "Q8_0 tensor %s is not a packed shape",
+                  name->s.c_str());
+    result.push_back({name->s, dtype->s, f + begin, dims});
+  }
+  out.swap(result);
+  return LLMCP_Q8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmcp_q8_arena_inspect(const void *file, uint64_t file_bytes,
+                           int64_t *num_tensors, int64_t *num_q8) {
+  std::vector<ArenaTensor> tensors;
+  int rc = parse_arena(file, file_bytes, tensors);
+  if (rc) return rc;
+  int64_t q8 = 0;
+  for (const ArenaTensor &t : tensors) q8 += t.dtype == "Q8_0";
+  if (num_tensors) *num_tensors = (int64_t)tensors.size();
+  if (num_q8) *num_q8 = q8;
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_upload_arena(llmcp_q8_ctx *ctx, const void *file,
+                          uint64_t file_bytes, int64_t *num_q8) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  std::vector<ArenaTensor> tensors;
+  int rc = parse_arena(file, file_bytes, tensors);
+  if (rc) return rc;
+  // Validation passed: upload.  A failure part-way leaves earlier tensors
+  // registered and reports the error.
+  int64_t n = 0;
+  for (const ArenaTensor &t : tensors) {
+    if (t.dtype != "Q8_0") continue;
+    rc = llmcp_q8_upload_p4(ctx, t.data, t.shape[0], t.shape[1], nullptr);
+    if (rc) return rc;
+    ++n;
+  }
+  if (num_q8) *num_q8 = n;
+  return LLMCP_Q8_OK;
+}
+
+// ------------------------------------------------------------------ ops --
+
+static int gemv_common(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                       const Tensor *w0, const Tensor *w1,
+                       llmcp_memref_f32_2d *output, int activation,
+                       int64_t *argmax_dev) {
+  GemvLaunch l;
+  l.x = input->data + input->offset;
+  l.w[0] = w0->dev;
+  l.w[1] = w1 ? w1->dev : nullptr;
+  l.y = output->data + output->offset;
+  l.rows = w0->rows;
+  l.cols = w0->cols;
+  l.nmat = w1 ? 2 : 1;
+  l.activation = activation;
+  if (argmax_dev) {
+    l.argmax = ctx->argmax;
+    l.argmax_out = argmax_dev;
+  }
+  hipError_t e = launch_gemv(l, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "gemv launch");
+  return LLMCP_Q8_OK;
+}
+
+static int check_linear_shapes(const llmcp_memref_f32_2d *input,
+                               const Tensor *w, llmcp_memref_f32_2d *output) {
+  if (!dense_rows(input) || !dense_rows(output))
+    return fail(LLMCP_Q8_DECLINED, "activations must be row-major f32 memrefs");
+  if (input->sizes[1] != w->cols)
+    return fail(LLMCP_Q8_DECLINED, "input K %lld != weight K %lld",
+                (long long)input->sizes[1], (long long)w->cols);
+  if (output->sizes[1] != w->rows)
+    return fail(LLMCP_Q8_DECLINED, "output N %lld != weight N %lld",
+                (long long)output->sizes[1], (long long)w->rows);
+  if (output->sizes[0] != input->sizes[0])
+    return fail(LLMCP_Q8_DECLINED, "output outer dimension must match input");
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                    const llmcp_memref_i8_1d *weight,
+                    llmcp_memref_f32_2d *output, int32_t activation,
+                    int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  const Tensor *w = nullptr;
+  int rc = resolve_weight(ctx, weight, &w);
+  if (rc) return rc;
+  rc = check_linear_shapes(input, w, output);
+  if (rc) return rc;
+  if (activation != LLMCP_Q8_ACT_NONE && activation != LLMCP_Q8_ACT_SILU)
+    return fail(LLMCP_Q8_DECLINED, "unsupported activation %d", activation);
+  const int64_t m = input->sizes[0];
+  if (m == 0) return LLMCP_Q8_OK;
+  if ((rc = set_device(ctx))) return rc;
+  if (execution_mode == LLMCP_Q8_DECODE) {
+    if (m != 1)
+      return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
+                  (long long)m);
+    return gemv_common(ctx, input, w, nullptr, output, activation, nullptr);
+  }
+  if (execution_mode != LLMCP_Q8_PREFILL)
+    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
+  if (m == 1)
+    return gemv_common(ctx, input, w, nullptr, output, activation, nullptr);
+  return fail(LLMCP_Q8_DECLINED, "prefill GEMM for M > 1 not available");
+}
+
+int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                    const llmcp_memref_i8_1d *w_gate,
+                    const llmcp_memref_i8_1d *w_up,
+                    llmcp_memref_f32_2d *output, int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  const Tensor *wg = nullptr, *wu = nullptr;
+  int rc = resolve_weight(ctx, w_gate, &wg);
+  if (rc) return rc;
+  if ((rc = resolve_weight(ctx, w_up, &wu))) return rc;
+  if (wg->rows != wu->rows || wg->cols != wu->cols)
+    return fail(LLMCP_Q8_DECLINED, "gate and up weights differ in shape");
+  if ((rc = check_linear_shapes(input, wg, output))) return rc;
+  const int64_t m = input->sizes[0];
+  if (m == 0) return LLMCP_Q8_OK;
+  if ((rc = set_device(ctx))) return rc;
+  if (execution_mode != LLMCP_Q8_DECODE && execution_mode != LLMCP_Q8_PREFILL)
+    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
+  if (m != 1)
+    return fail(LLMCP_Q8_DECLINED, "fused SwiGLU for M > 1 not available");
+  return gemv_common(ctx, input, wg, wu, output, LLMCP_Q8_ACT_NONE, nullptr);
+}
+
+int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
+                     const llmcp_memref_i8_1d *table,
+                     llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
+                     int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  const Tensor *w = nullptr;
+  int rc = resolve_weight(ctx, table, &w);
+  if (rc) return rc;
+  if ((rc = check_linear_shapes(hidden, w, logits))) return rc;
+  const int64_t m = hidden->sizes[0];
+  if (m == 0) return LLMCP_Q8_OK;
+  if ((rc = set_device(ctx))) return rc;
+  if (execution_mode != LLMCP_Q8_DECODE && execution_mode != LLMCP_Q8_PREFILL)
+    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
+  if (m != 1)
+    return fail(LLMCP_Q8_DECLINED, "lm_head for M > 1 not available");
+  return gemv_common(ctx, hidden, w, nullptr, logits, LLMCP_Q8_ACT_NONE,
+                     argmax_dev);
+}
+
+int llmcp_q8_embedding(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
+                       const llmcp_memref_i8_1d *table,
+                       llmcp_memref_f32_2d *output) {
+  if (!ctx || !tokens || !output) return fail(LLMCP_Q8_EINVAL, "null argument");
+  const Tensor *w = nullptr;
+  int rc = resolve_weight(ctx, table, &w);
+  if (rc) return rc;
+  if (tokens->strides[0] != 1 && tokens->sizes[0] > 1)
+    return fail(LLMCP_Q8_DECLINED, "tokens must be contiguous");
+  if (!dense_rows(output) || output->sizes[1] != w->cols ||
+      output->sizes[0] != tokens->sizes[0])
+    return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
+  if (tokens->sizes[0] > 65535)
+    return fail(LLMCP_Q8_DECLINED, "at most 65535 tokens per call");
+  if ((rc = set_device(ctx))) return rc;
+  hipError_t e = launch_embedding(tokens->data + tokens->offset,
+                                  tokens->sizes[0], w->dev, w->rows, w->cols,
+                                  output->data + output->offset,
+                                  output->strides[0], ctx->err_flag,
+                                  ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "embedding launch");
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_quantize_activations(llmcp_q8_ctx *ctx,
+                                  const llmcp_memref_f32_2d *input,
+                                  int8_t *qa_dev, float *sa_dev) {
+  if (!ctx || !qa_dev || !sa_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
+  if (!dense_rows(input) || input->sizes[1] % kBlock)
+    return fail(LLMCP_Q8_DECLINED, "input must be row-major with K %% 32 == 0");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  const int64_t m = input->sizes[0], k = input->sizes[1];
+  if (m == 0) return LLMCP_Q8_OK;
+  hipError_t e = launch_quantize(input->data + input->offset, m,
+                                 input->strides[0], k, qa_dev, k, sa_dev,
+                                 k / kBlock, k / kBlock, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_block_dots(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                        const llmcp_memref_i8_1d *weight, int32_t *out_dev) {
+  if (!ctx || !out_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
+  const Tensor *w = nullptr;
+  int rc = resolve_weight(ctx, weight, &w);
+  if (rc) return rc;
+  if (!dense_rows(input) || input->sizes[1] != w->cols)
+    return fail(LLMCP_Q8_DECLINED, "input must be row-major [M, K]");
+  if ((rc = set_device(ctx))) return rc;
+  const int64_t m = input->sizes[0], k = input->sizes[1], b = k / kBlock;
+  if (m == 0) return LLMCP_Q8_OK;
+  if ((rc = ensure_scratch(ctx, (uint64_t)(m * k), (uint64_t)(m * b * 4))))
+    return rc;
+  hipError_t e = launch_quantize(input->data + input->offset, m,
+                                 input->strides[0], k, ctx->qa, k, ctx->sa, b,
+                                 b, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  e = launch_block_dots(ctx->qa, k, m, w->dev, w->rows, w->cols, out_dev,
+                        ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "block dots launch");
+  return LLMCP_Q8_OK;
+}
+
+// ------------------------------------------------------ offline packing --
+
+int llmcp_q8_pack_p4_host(const float *w, int64_t rows, int64_t cols,
+                          uint8_t *out) {
+  if (!w || !out) return fail(LLMCP_Q8_EINVAL, "null argument");
+  if (!packable(rows, cols))
+    return fail(LLMCP_Q8_DECLINED,
+                "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
+  const int64_t blocks = cols / kBlock, groups = rows / kLanes;
+#pragma omp parallel for schedule(static)
+  for (int64_t g = 0; g < groups; ++g) {
+    for (int64_t b = 0; b < blocks; ++b) {
+      uint8_t *rec = out + (g * blocks + b) * kRecord;
+      for (int r = 0; r < kLanes; ++r) {
+        const float *v = w + (g * kLanes + r) * cols + b * kBlock;
+        float amax = 0.0f;
+        for (int i = 0; i < kBlock; ++i) amax = std::max(amax, std::fabs(v[i]));
+        uint16_t d = 0;
+        int8_t q[kBlock] = {0};
+        if (amax != 0.0f) {
+          const float scale = amax / 127.0f;
+          d = host_f32_to_f16(scale);
+          for (int i = 0; i < kBlock; ++i) {
+            long x = std::lround(v[i] / scale);
+            q[i] = (int8_t)std::min(127L, std::max(-127L, x));
+          }
+        }
+        rec[2 * r] = (uint8_t)(d & 0xff);
+        rec[2 * r + 1] = (uint8_t)(d >> 8);
+        for (int c = 0; c < 8; ++c)
+          std::memcpy(rec + 8 + 16 * c + 4 * r, q + 4 * c, 4);
+      }
+    }
+  }
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_synthesize_p4(llmcp_q8_ctx *ctx, uint64_t seed, int64_t rows,
+                           int64_t cols, float stddev, float *w_dev,
+                           void *p4_dev) {
+  if (!ctx || !p4_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
+  if (!packable(rows, cols))
+    return fail(LLMCP_Q8_DECLINED,
+                "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  float *w = w_dev;
+  if (!w && hipMalloc(&w, (size_t)rows * (size_t)cols * 4) != hipSuccess)
+    return fail(LLMCP_Q8_ENOMEM, "synthetic weight staging");
+  hipError_t e = launch_synth(seed, rows, cols, stddev, w, ctx->stream);
+  if (e == hipSuccess)
+    e = launch_pack_p4(w, rows, cols, (uint8_t *)p4_dev, ctx->stream);
+  if (!w_dev) {
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(w);
+  }
+  if (e != hipSuccess) return hip_fail(e, "synthesize");
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_write_arena(const char *path, int32_t count,
+                         const char *const *names, const int64_t *rows,
+                         const int64_t *cols, const void *const *p4) {
+  if (!path || count <= 0 || !names || !rows || !cols || !p4)
+    return fail(LLMCP_Q8_EINVAL, "bad arena writer arguments");
+  std::vector<uint64_t> offsets(count), sizes(count);
+  uint64_t cursor = 64;
+  for (int32_t i = 0; i < count; ++i) {
+    if (!names[i] || !names[i][0] || !packable(rows[i], cols[i]))
+      return fail(LLMCP_Q8_EINVAL, "tensor %d: bad name or shape", i);
+    cursor = (cursor + 63) / 64 * 64;
+    offsets[i] = cursor;
+    sizes[i] = (uint64_t)rows[i] * (uint64_t)(cols[i] / 32) * 34u;
+    cursor += sizes[i];
+  }
+  const uint64_t arena = (cursor + 63) / 64 * 64;
+  std::string m = "{\"model\":\"synthetic\",\"total_bytes\":" +
+                  std::to_string(arena) +
+                  ",\"header_bytes\":64,\"group_stride\":0,\"num_groups\":0,"
+                  "\"alignment\":64,\"quantization\":\"q8_0\",\"block_size\":32,"
+                  "\"quant_layout\":\"q8_0_p4\",\"tensors\":[";
+  for (int32_t i = 0; i < count; ++i) {
+    std::string name;
+    for (const char *c = names[i]; *c; ++c) {
+      if (*c == '"' || *c == '\\') name += '\\';
+      name += *c;
+    }
+    m += (i ? "," : "");
+    m += "{\"name\":\"" + name + "\",\"offset\":" + std::to_string(offsets[i]) +
+         ",\"size\":" + std::to_string(sizes[i]) +
+         ",\"dtype\":\"Q8_0\",\"source_size\":" +
+         std::to_string((uint64_t)rows[i] * (uint64_t)cols[i] * 4u) +
+         ",\"shape\":[" + std::to_string(rows[i]) + "," +
+         std::to_string(cols[i]) + "]}";
+  }
+  m += "]}\n";
+  FILE *fp = std::fopen(path, "wb");
+  if (!fp) return fail(LLMCP_Q8_EIO, "cannot open %s", path);
+  std::vector<uint8_t> header(64, 0);
+  bool ok = std::fwrite(header.data(), 1, 64, fp) == 64;
+  uint64_t pos = 64;
+  std::vector<uint8_t> zeros(64, 0);
+  for (int32_t i = 0; i < count && ok; ++i) {
+    while (ok && pos < offsets[i]) {
+      const uint64_t n = std::min<uint64_t>(64, offsets[i] - pos);
+      ok = std::fwrite(zeros.data(), 1, n, fp) == n;
+      pos += n;
+    }
+    ok = ok && std::fwrite(p4[i], 1, sizes[i], fp) == sizes[i];
+    pos += sizes[i];
+  }
+  while (ok && pos < arena) {
+    const uint64_t n = std::min<uint64_t>(64, arena - pos);
+    ok = std::fwrite(zeros.data(), 1, n, fp) == n;
+    pos += n;
+  }
+  ok = ok && std::fwrite(m.data(), 1, m.size(), fp) == m.size();
+  // Publish the header last (WeightPacker.cpp:269-272).
+  std::memcpy(header.data(), "LLMCPWGT", 8);
+  wr32(header.data() + 8, 1);
+  wr32(header.data() + 12, 64);
+  wr64(header.data() + 16, arena);
+  wr64(header.data() + 24, arena);
+  wr64(header.data() + 32, m.size());
+  ok = ok && std::fflush(fp) == 0 && std::fseek(fp, 0, SEEK_SET) == 0 &&
+       std::fwrite(header.data(), 1, 64, fp) == 64;
+  ok = (std::fclose(fp) == 0) && ok;
+  if (!ok) return fail(LLMCP_Q8_EIO, "short write to %s", path);
+  return LLMCP_Q8_OK;
+}
+
+// ---------------------------------------------------- MLIR C interface --
+
+int32_t _mlir_ciface_llmcp_q8_linear(llmcp_memref_f32_2d *input,
+                                     llmcp_memref_i8_1d *weight,
+                                     llmcp_memref_f32_2d *output,
+                                     int32_t activation,
+                                     int32_t execution_mode) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  return llmcp_q8_linear(g_default_ctx, input, weight, output, activation,
+                         execution_mode);
+}
+
+int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
+                                     llmcp_memref_i8_1d *w_gate,
+                                     llmcp_memref_i8_1d *w_up,
+                                     llmcp_memref_f32_2d *output,
+                                     int32_t execution_mode) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  return llmcp_q8_swiglu(g_default_ctx, input, w_gate, w_up, output,
+                         execution_mode);
+}
+
+int32_t _mlir_ciface_llmcp_q8_lm_head(llmcp_memref_f32_2d *hidden,
+                                      llmcp_memref_i8_1d *table,
+                                      llmcp_memref_f32_2d *logits,
+                                      llmcp_memref_i64_1d *argmax,
+                                      int32_t execution_mode) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  int64_t *am = argmax ? argmax->data + argmax->offset : nullptr;
+  return llmcp_q8_lm_head(g_default_ctx, hidden, table, logits, am,
+                          execution_mode);
+}
+
+int32_t _mlir_ciface_llmcp_q8_embedding(llmcp_memref_i64_1d *tokens,
+                                        llmcp_memref_i8_1d *table,
+                                        llmcp_memref_f32_2d *output) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  return llmcp_q8_embedding(g_default_ctx, tokens, table, output);
+}
+
+// --------------------------------------------------- device plumbing --
+
+int llmcp_q8_dev_alloc(llmcp_q8_ctx *ctx, uint64_t bytes, void **out) {
+  if (!ctx || !out) return fail(LLMCP_Q8_EINVAL, "null argument");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess)
+    return fail(LLMCP_Q8_ENOMEM, "hipMalloc of %llu bytes",
+                (unsigned long long)bytes);
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_dev_free(llmcp_q8_ctx *ctx, void *ptr) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  if (!ptr) return LLMCP_Q8_OK;
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  HIP_TRY(hipFree(ptr));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_memcpy_h2d(llmcp_q8_ctx *ctx, void *dst, const void *src,
+                        uint64_t bytes) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_memcpy_d2h(llmcp_q8_ctx *ctx, void *dst, const void *src,
+                        uint64_t bytes) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_memcpy_d2d(llmcp_q8_ctx *ctx, void *dst, const void *src,
+                        uint64_t bytes) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_event_create(void **event) {
+  if (!event) return fail(LLMCP_Q8_EINVAL, "null argument");
+  hipEvent_t e;
+  HIP_TRY(hipEventCreate(&e));
+  *event = (void *)e;
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_event_destroy(void *event) {
+  if (event) HIP_TRY(hipEventDestroy((hipEvent_t)event));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_event_record(llmcp_q8_ctx *ctx, void *event) {
+  if (!ctx || !event) return fail(LLMCP_Q8_EINVAL, "null argument");
+  HIP_TRY(hipEventRecord((hipEvent_t)event, ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_event_elapsed_ms(void *start, void *stop, float *ms) {
+  if (!start || !stop || !ms) return fail(LLMCP_Q8_EINVAL, "null argument");
+  HIP_TRY(hipEventSynchronize((hipEvent_t)stop));
+  HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_graph_begin(llmcp_q8_ctx *ctx) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_graph_end(llmcp_q8_ctx *ctx, void **graph_exec) {
+  if (!ctx || !graph_exec) return fail(LLMCP_Q8_EINVAL, "null argument");
+  hipGraph_t g = nullptr;
+  HIP_TRY(hipStreamEndCapture(ctx->stream, &g));
+  hipGraphExec_t ex = nullptr;
+  hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *graph_exec = (void *)ex;
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_graph_launch(llmcp_q8_ctx *ctx, void *graph_exec) {
+  if (!ctx || !graph_exec) return fail(LLMCP_Q8_EINVAL, "null argument");
+  HIP_TRY(hipGraphLaunch((hipGraphExec_t)graph_exec, ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_graph_destroy(void *graph_exec) {
+  if (graph_exec) HIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+  return LLMCP_Q8_OK;
+}
+
+}  // extern "C"

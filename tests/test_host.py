@@ -1,0 +1,134 @@
+"""CPU-side tests of the C-ABI library: it loads, exports every symbol that
+include/llmcp_q8.h declares, its host packer (llmcp-pack's
+quantizeTensorQ8_0Packed) matches the oracle byte for byte, and its arena
+loader applies the reference's validation rules (PackedWeightsTest.cpp:186-223,
+WeightArena.cpp:27-131).  No device is touched.
+"""
+import ctypes
+import json
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "llmcp_q8.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:llmcp_q8|_mlir_ciface_llmcp_q8)_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(q8):
+    names = declared_functions()
+    assert len(names) >= 30
+    L = q8.lib()
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(names) == set(q8.EXPORTS)
+
+
+def test_abi_version(q8):
+    assert q8.lib().llmcp_q8_abi_version() == 1
+
+
+def test_host_packer_matches_oracle(q8, oracle):
+    rng = np.random.default_rng(21)
+    for n, k in [(8, 32), (40, 320), (64, 2560)]:
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        w[3, 32:64] = 0.0  # zero block -> d = 0
+        assert np.array_equal(q8.pack_p4_host(w), oracle.pack_q8_0_p4(w))
+
+
+def test_host_packer_rejects_unpackable(q8):
+    with pytest.raises(q8.Declined):
+        q8.pack_p4_host(np.zeros((12, 64), np.float32))
+
+
+def _arena(tmp_path, q8, tensors):
+    path = str(tmp_path / "w.bin")
+    q8.write_arena(path, tensors)
+    return np.fromfile(path, dtype=np.uint8)
+
+
+def test_arena_round_trip(q8, oracle, tmp_path):
+    rng = np.random.default_rng(22)
+    a = oracle.pack_q8_0_p4((rng.standard_normal((16, 64)) * 0.02).astype(np.float32))
+    b = oracle.pack_q8_0_p4((rng.standard_normal((8, 96)) * 0.02).astype(np.float32))
+    f = _arena(tmp_path, q8, [("model.a.weight", 16, 64, a), ("model.b.weight", 8, 96, b)])
+    assert bytes(f[:8]) == b"LLMCPWGT"
+    version, hdr = struct.unpack_from("<II", f, 8)
+    arena, moff, mbytes = struct.unpack_from("<QQQ", f, 16)
+    assert (version, hdr) == (1, 64) and moff == arena and mbytes == f.size - arena
+    manifest = json.loads(bytes(f[moff:]).decode())
+    assert manifest["quantization"] == "q8_0" and manifest["quant_layout"] == "q8_0_p4"
+    for entry, data in zip(manifest["tensors"], [a, b]):
+        assert entry["offset"] % 64 == 0
+        assert np.array_equal(f[entry["offset"]:entry["offset"] + entry["size"]], data)
+    assert q8.arena_inspect(f) == (2, 2)
+
+
+def _rewrite_manifest(f, edit):
+    arena = struct.unpack_from("<Q", f, 16)[0]
+    m = json.loads(bytes(f[arena:]).decode())
+    edit(m)
+    body = json.dumps(m).encode()
+    out = np.concatenate([f[:arena], np.frombuffer(body, np.uint8)])
+    struct.pack_into("<Q", out, 32, len(body))
+    return out
+
+
+@pytest.mark.parametrize("corruption", [
+    "magic", "version", "header_size", "manifest_bounds", "json", "total",
+    "block_size", "layout", "offset_align", "outside", "size", "dtype",
+    "duplicate", "shape_rank",
+])
+def test_arena_rejects_corruption(q8, oracle, tmp_path, corruption):
+    a = oracle.pack_q8_0_p4(np.ones((8, 64), np.float32))
+    f = _arena(tmp_path, q8, [("t", 8, 64, a)]).copy()
+    if corruption == "magic":
+        f[0] = ord("X")
+    elif corruption == "version":
+        struct.pack_into("<I", f, 8, 2)
+    elif corruption == "header_size":
+        struct.pack_into("<I", f, 12, 32)
+    elif corruption == "manifest_bounds":
+        struct.pack_into("<Q", f, 32, 5)
+    elif corruption == "json":
+        arena = struct.unpack_from("<Q", f, 16)[0]
+        f[arena] = ord("[")
+    elif corruption == "total":
+        f = _rewrite_manifest(f, lambda m: m.update(total_bytes=m["total_bytes"] + 64))
+    elif corruption == "block_size":
+        f = _rewrite_manifest(f, lambda m: m.update(block_size=16))
+    elif corruption == "layout":
+        f = _rewrite_manifest(f, lambda m: m.update(quant_layout="q8_0"))
+    elif corruption == "offset_align":
+        f = _rewrite_manifest(f, lambda m: m["tensors"][0].update(offset=96))
+    elif corruption == "outside":
+        f = _rewrite_manifest(f, lambda m: m["tensors"][0].update(offset=m["total_bytes"]))
+    elif corruption == "size":
+        f = _rewrite_manifest(f, lambda m: m["tensors"][0].update(size=m["tensors"][0]["size"] - 34))
+    elif corruption == "dtype":
+        f = _rewrite_manifest(f, lambda m: m["tensors"][0].update(dtype="Q4_0"))
+    elif corruption == "duplicate":
+        f = _rewrite_manifest(f, lambda m: m["tensors"].append(dict(m["tensors"][0])))
+    elif corruption == "shape_rank":
+        f = _rewrite_manifest(f, lambda m: m["tensors"][0].update(shape=[8 * 64]))
+    with pytest.raises(q8.Q8Error) as e:
+        q8.arena_inspect(f)
+    assert e.value.code == q8.EFORMAT
+
+
+def test_arena_accepts_mixed_dtypes(q8, tmp_path, oracle):
+    a = oracle.pack_q8_0_p4(np.ones((8, 64), np.float32))
+    f = _arena(tmp_path, q8, [("t", 8, 64, a)])
+
+    def add_f32(m):
+        m["tensors"].append({"name": "norm", "offset": 64, "size": 16,
+                             "dtype": "F32", "shape": [4]})
+    f2 = _rewrite_manifest(f, add_f32)
+    assert q8.arena_inspect(f2) == (2, 1)
