@@ -90,8 +90,7 @@ def bench_decode_mlp(ctx, q8, steps, warmup, hidden=2560, ffn=9216):
 
     def one_rotation():
         for mats in pool:
-            ctx.swiglu(xd, mats[0][0], mats[1][0], hd, 1)
-            ctx.linear(hd, mats[2][0], yd, 1)
+            ctx.mlp(xd, mats[0][0], mats[1][0], mats[2][0], yd, h=hd)
 
     def gateup_rotation():
         for mats in pool:
@@ -268,7 +267,8 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": None,
-                     "kernel": "gemv_kernel<NMAT=2> (fused gate/up SwiGLU)",
+                     "kernel": "gemv_kernel<NMAT=2,QIN> (fused gate/up SwiGLU, "
+                               "timed alone via llmcp_q8_swiglu)",
                      "launch_us": round(res["gu_launch_us"], 3),
                      "algorithmic_bytes": res["gu_bytes"]},
         "cpu_baseline": None if cpu is None else {

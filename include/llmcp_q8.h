@@ -156,6 +156,17 @@ int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                     const llmcp_memref_i8_1d *w_up,
                     llmcp_memref_f32_2d *output, int32_t execution_mode);
 
+/* Decode MLP of one layer, ModelBuilder.cpp:205-216 with FuseSiluMul:
+ * h = silu(x . Wg^T) * (x . Wu^T), y = h . Wd^T.  Two kernels: the fused
+ * gate/up GEMV also quantizes h (Q8_1, as the down linear's quantizer
+ * would), so the down GEMV reads it directly.  `hidden` (nullable) receives
+ * h in f32.  Results equal llmcp_q8_swiglu followed by llmcp_q8_linear. */
+int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                 const llmcp_memref_i8_1d *w_gate,
+                 const llmcp_memref_i8_1d *w_up,
+                 const llmcp_memref_i8_1d *w_down, llmcp_memref_f32_2d *hidden,
+                 llmcp_memref_f32_2d *output, int32_t execution_mode);
+
 /* llmcp.lm_head (LowerToLinalg.cpp:729-765): f32 logits [M,V] over the tied
  * table, plus the first-maximum index of the last row written to
  * `argmax_dev` (device int64, nullable) -- the host std::max_element of

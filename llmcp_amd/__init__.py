@@ -57,7 +57,7 @@ EXPORTS = [
     "llmcp_q8_ctx_synchronize", "llmcp_q8_set_default_ctx",
     "llmcp_q8_upload_p4", "llmcp_q8_register_device_p4", "llmcp_q8_release",
     "llmcp_q8_upload_arena", "llmcp_q8_arena_inspect", "llmcp_q8_linear", "llmcp_q8_swiglu",
-    "llmcp_q8_lm_head", "llmcp_q8_embedding", "llmcp_q8_quantize_activations",
+    "llmcp_q8_lm_head", "llmcp_q8_mlp", "llmcp_q8_embedding", "llmcp_q8_quantize_activations",
     "llmcp_q8_block_dots", "llmcp_q8_ctx_check", "llmcp_q8_pack_p4_host",
     "llmcp_q8_synthesize_p4", "llmcp_q8_write_arena",
     "_mlir_ciface_llmcp_q8_linear", "_mlir_ciface_llmcp_q8_swiglu",
@@ -101,6 +101,7 @@ def lib():
         "llmcp_q8_linear": (I, [P, P, P, P, I32, I32]),
         "llmcp_q8_swiglu": (I, [P, P, P, P, P, I32]),
         "llmcp_q8_lm_head": (I, [P, P, P, P, P, I32]),
+        "llmcp_q8_mlp": (I, [P, P, P, P, P, P, P, I32]),
         "llmcp_q8_embedding": (I, [P, P, P, P]),
         "llmcp_q8_quantize_activations": (I, [P, P, P, P]),
         "llmcp_q8_block_dots": (I, [P, P, P, P]),
@@ -308,6 +309,16 @@ class Context:
                                     ctypes.byref(wg.memref()),
                                     ctypes.byref(wu.memref()), ctypes.byref(ho),
                                     MODE[mode]))
+
+    def mlp(self, x, wg, wu, wd, y, h=None, m=1, mode="decode"):
+        xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, wg.cols)
+        yo = f32_memref(y.ptr if hasattr(y, "ptr") else y, m, wd.rows)
+        ho = f32_memref(h.ptr if hasattr(h, "ptr") else h, m, wg.rows) if h is not None else None
+        check(lib().llmcp_q8_mlp(self.handle, ctypes.byref(xi),
+                                 ctypes.byref(wg.memref()), ctypes.byref(wu.memref()),
+                                 ctypes.byref(wd.memref()),
+                                 ctypes.byref(ho) if ho is not None else None,
+                                 ctypes.byref(yo), MODE[mode]))
 
     def lm_head(self, x, w, logits, m, argmax=None, mode="decode"):
         xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, w.cols)

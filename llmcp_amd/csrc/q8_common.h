@@ -39,12 +39,4 @@ inline int64_t device_bytes_for(int64_t rows, int64_t cols) {
   return rows / kLanes * passes_for(cols) * kPassBytes;
 }
 
-// Argmax accumulator in device memory, zeroed at context creation and reset
-// by the last workgroup of every lm_head launch.
-struct ArgmaxState {
-  unsigned long long key;
-  unsigned int ticket;
-  unsigned int pad;
-};
-
 }  // namespace llmcp_q8

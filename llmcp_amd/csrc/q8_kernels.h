@@ -28,20 +28,29 @@ hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
                            int64_t lds, int64_t blocks_pad, hipStream_t s);
 
 struct GemvLaunch {
-  const float *x = nullptr;      // f32 input row (quantized in the prologue)
-  const int8_t *qa = nullptr;    // or: pre-quantized input (padded)
-  const float *sa = nullptr;
+  const float *x = nullptr;      // f32 input row, quantized in the pass loop
+  const int8_t *qa = nullptr;    // or: Q8_1 input row, padded to passes*16
+  const float *sa = nullptr;     //     blocks (used when x is null)
   const uint8_t *w[2] = {nullptr, nullptr};  // pass-layout weights
   float *y = nullptr;            // f32 output [rows]
   int64_t rows = 0;              // N
   int64_t cols = 0;              // K
   int nmat = 1;                  // 2 = fused SwiGLU (gate, up)
   int activation = 0;            // 0 none, 1 silu (nmat == 1 only)
-  ArgmaxState *argmax = nullptr; // non-null: fused argmax
-  int64_t *argmax_out = nullptr;
+  unsigned long long *keys = nullptr;  // non-null: fused argmax partials,
+  int64_t *argmax_out = nullptr;       // gemv_workgroups(rows) entries
+  int8_t *qout = nullptr;        // non-null: also emit Q8_1 of y
+  float *sout = nullptr;         // (rows % 32 == 0, f32 input x required)
 };
 
+// One-matrix GEMVs with at most this many lane groups quantize the input
+// row inside the kernel; wider ones (every wave would re-read the row) take
+// a pre-quantized row.  Two-matrix (SwiGLU) GEMVs always quantize inside.
+constexpr int64_t kInLoopQuantMaxGroups = 4096;
+bool gemv_quantizes_input(int64_t rows, int nmat);
+
 hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s);
+int64_t gemv_workgroups(int64_t rows);
 
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             const uint8_t *table, int64_t rows, int64_t cols,

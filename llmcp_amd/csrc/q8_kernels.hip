@@ -218,20 +218,30 @@ __global__ void quantize_kernel(const float *__restrict__ x, int64_t m,
 // --------------------------------------------------------------- GEMV -- //
 
 struct GemvArgs {
-  const float *x;
-  const int8_t *qa;
+  const float *x;    // IN_WAVE / IN_WG: f32 input row, 16 B aligned
+  const int8_t *qa;  // IN_PRE: Q8_1 input, padded to passes * 16 blocks
   const float *sa;
   const uint8_t *w0;
   const uint8_t *w1;
   float *y;
-  ArgmaxState *am;
-  int64_t *am_out;
+  unsigned long long *keys;  // ARGMAX: one (value, index) key per workgroup
+  int8_t *qout;              // QOUT: Q8_1 of y, [rows] bytes + [rows/32] scales
+  float *sout;
   int64_t groups;
   int32_t blocks;
   int32_t passes;
-  int32_t x_aligned;
 };
 
+// Where the GEMV's input row comes from.
+enum InputMode {
+  IN_PRE = 0,   // pre-quantized Q8_1 row in global memory
+  IN_WAVE = 1,  // f32 row, each wave quantizes its blocks in the pass loop
+  IN_WG = 2     // f32 row, each workgroup quantizes it once into LDS
+};
+
+// Total order on (logit, index) whose maximum is the first maximum:
+// order-preserving float bits (with -0 folded into +0, which compare equal)
+// in the high word, the complemented index in the low word.
 __device__ __forceinline__ unsigned long long argmax_key(float v,
                                                          int64_t idx) {
   uint32_t bits = __builtin_bit_cast(uint32_t, v == 0.0f ? 0.0f : v);
@@ -240,32 +250,80 @@ __device__ __forceinline__ unsigned long long argmax_key(float v,
          (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d,
+                                          float inv) {
+  const int q0 = (int)rintf(a * inv), q1 = (int)rintf(b * inv);
+  const int q2 = (int)rintf(c * inv), q3 = (int)rintf(d * inv);
+  return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+         ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+}
+
+// Q8_1 of one 32-value block spread over the four lanes j, j+16, j+32, j+48
+// (lane 16r + j holds values 8r..8r+7): the same arithmetic as
+// Q8Decode.cpp:83-120, then every lane gathers the block's 8 words.
+__device__ __forceinline__ void quantize_shared_block(const uint4 &b0,
+                                                      const uint4 &b1, int j,
+                                                      uint4 &a0, uint4 &a1,
+                                                      float &s_out) {
+  const float4 v0 = __builtin_bit_cast(float4, b0);
+  const float4 v1 = __builtin_bit_cast(float4, b1);
+  float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)),
+                        fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                  fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)),
+                        fmaxf(fabsf(v1.z), fabsf(v1.w))));
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
+  const float s = m / 127.0f;
+  const float inv = m == 0.0f ? 0.0f : 1.0f / s;
+  const uint32_t lo = pack4(v0.x, v0.y, v0.z, v0.w, inv);
+  const uint32_t hi = pack4(v1.x, v1.y, v1.z, v1.w, inv);
+  a0.x = (uint32_t)__shfl((int)lo, j);
+  a0.y = (uint32_t)__shfl((int)hi, j);
+  a0.z = (uint32_t)__shfl((int)lo, j + 16);
+  a0.w = (uint32_t)__shfl((int)hi, j + 16);
+  a1.x = (uint32_t)__shfl((int)lo, j + 32);
+  a1.y = (uint32_t)__shfl((int)hi, j + 32);
+  a1.z = (uint32_t)__shfl((int)lo, j + 48);
+  a1.w = (uint32_t)__shfl((int)hi, j + 48);
+  s_out = s;
+}
+
 // One wave per lane group (4 rows); lane L = 16r + j owns row 4g+r and the
-// blocks 16p + j of every pass p.  D passes are kept in flight per wave.
-// PC > 0: the pass count is a compile-time constant and the pass sequence is
-// fully unrolled, so every wait on the weight ring is exact; PC == 0 handles
-// any pass count with a runtime loop.
-template <int NMAT, int ACT, bool ARGMAX, int D, bool PREQ, int PC>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  extern __shared__ __align__(16) unsigned char lds[];
+// blocks 16p + j of every pass p.  Each lane streams its weights (and, for
+// IN_PRE / IN_WAVE, its activation block) through a ring of D passes in
+// flight.
+//   IN    where the input row comes from (InputMode).
+//   QOUT  y is also quantized to Q8_1 for the next GEMV.  Needs 8 waves per
+//         workgroup: the workgroup owns one 32-row output block and
+//         quantizes it through LDS.
+//   PC>0  the pass count is a compile-time constant and the pass sequence
+//         is fully unrolled, so every wait on the ring is exact.
+template <int NMAT, int ACT, bool ARGMAX, int IN, bool QOUT, int D, int PC>
+__global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char lds[];  // IN_WG input row
+  __shared__ unsigned long long key_l[8];
+  __shared__ float y_l[kBlock];
+  __shared__ unsigned count_l;
+  if (QOUT && threadIdx.x == 0) count_l = 0;
   const int passes = PC > 0 ? PC : a.passes;
   const int nblk = passes * kPassBlocks;
-  int8_t *qa_l = (int8_t *)lds;
-  float *sa_l = (float *)(lds + nblk * kBlock);
-  unsigned long long *key_l =
-      (unsigned long long *)(lds + nblk * kBlock + nblk * 4);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int waves = blockDim.x >> 6;
   const int64_t g = (int64_t)blockIdx.x * waves + wave;
   const bool active = g < a.groups;
+  const int j = lane & 15;
+  const int r = lane >> 4;
+  int8_t *qa_l = (int8_t *)lds;
+  float *sa_l = (float *)(lds + nblk * kBlock);
 
   const unsigned char *base[NMAT];
   base[0] = a.w0 + g * passes * kPassBytes;
   if (NMAT == 2) base[NMAT - 1] = a.w1 + g * passes * kPassBytes;
 
-  uint4 q0[NMAT][D], q1[NMAT][D];
+  uint4 q0[NMAT][D], q1[NMAT][D], x0[D], x1[D];
   uint32_t sc[NMAT][D];
+  float xs[D];
   auto issue = [&](int slot, int p) {
     const int pc = p < passes ? p : passes - 1;
 #pragma unroll
@@ -275,48 +333,47 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       q1[mm][slot] = *(const uint4 *)(pb + 1024 + lane * 16);
       sc[mm][slot] = *(const uint16_t *)(pb + kPassQs + lane * 2);
     }
-  };
-  // Weight loads go out before the activation prologue so both overlap.
-  if (active) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) issue(d, d);
-  }
-
-  if (PREQ) {
-    const uint4 *src = (const uint4 *)a.qa;
-    for (int i = threadIdx.x; i < nblk * 2; i += blockDim.x)
-      ((uint4 *)qa_l)[i] = src[i];
-    for (int i = threadIdx.x; i < nblk; i += blockDim.x) sa_l[i] = a.sa[i];
-  } else {
-    for (int b0 = wave * 8; b0 < nblk; b0 += waves * 8) {
-      const int blk = b0 + (lane >> 3);
-      const bool valid = blk < a.blocks;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (valid)
-        v = load_float4(a.x + blk * kBlock + (lane & 7) * 4, a.x_aligned);
-      int32_t q;
-      float s = 0.0f;
-      quantize_block8(v, valid, lane, &q, &s);
-      ((int32_t *)qa_l)[blk * 8 + (lane & 7)] = q;
-      if ((lane & 7) == 0) sa_l[blk] = s;
+    // Raw loads only: any use of the loaded values here (even a select)
+    // would make the wave wait for them and drain the ring.  Padded blocks
+    // (blk >= blocks) are masked in consume().
+    const int blk = pc * kPassBlocks + j;
+    if (IN == IN_WAVE) {
+      const float *xp = a.x + (blk < a.blocks ? blk * kBlock + 8 * r : 0);
+      x0[slot] = *(const uint4 *)xp;
+      x1[slot] = *(const uint4 *)(xp + 4);
+    } else if (IN == IN_PRE) {
+      x0[slot] = *(const uint4 *)(a.qa + blk * kBlock);
+      x1[slot] = *(const uint4 *)(a.qa + blk * kBlock + 16);
+      xs[slot] = a.sa[blk];
     }
-  }
-  __syncthreads();
+  };
 
   float acc[NMAT];
 #pragma unroll
   for (int mm = 0; mm < NMAT; ++mm) acc[mm] = 0.0f;
 
-  const int j = lane & 15;
   // Pass p in ring slot d: exact block dots, scale, then the serial chain
   // over the pass's 16 blocks in block order -- after step t, lane t of each
   // row holds the running sum through block 16p + t; lane 15 carries it
   // into the next pass.
   auto consume = [&](int d, int p) {
+    uint4 a0, a1;
+    float s_a;
     const int blk = p * kPassBlocks + j;
-    const uint4 a0 = *(const uint4 *)(qa_l + blk * kBlock);
-    const uint4 a1 = *(const uint4 *)(qa_l + blk * kBlock + 16);
-    const float s_a = sa_l[blk];
+    const bool valid = blk < a.blocks;  // padded blocks: zero input
+    if (IN == IN_WAVE) {
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      quantize_shared_block(valid ? x0[d] : z, valid ? x1[d] : z, j, a0, a1,
+                            s_a);
+    } else if (IN == IN_PRE) {
+      a0 = x0[d];
+      a1 = x1[d];
+      s_a = valid ? xs[d] : 0.0f;
+    } else {
+      a0 = *(const uint4 *)(qa_l + blk * kBlock);
+      a1 = *(const uint4 *)(qa_l + blk * kBlock + 16);
+      s_a = sa_l[blk];
+    }
     float contrib[NMAT];
 #pragma unroll
     for (int mm = 0; mm < NMAT; ++mm) {
@@ -333,36 +390,101 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
   };
 
+  // sched_barrier(0) pins each refill right after the pass that frees its
+  // slot; without it the scheduler sinks the loads toward their uses and
+  // only about one pass stays in flight.
+  if (active) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, d);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (IN == IN_WG) {
+    // Quantize the whole input row into LDS once per workgroup, 8 lanes per
+    // block, four blocks' loads in flight per lane (the weight ring above
+    // is already on its way).
+    constexpr int U = 4;
+    const int tasks = nblk * 8;
+    for (int t0 = 0; t0 < tasks; t0 += (int)blockDim.x * U) {
+      float4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int t = t0 + u * (int)blockDim.x + (int)threadIdx.x;
+        const int blk = t >> 3;
+        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (blk < a.blocks) v[u] = *(const float4 *)(a.x + blk * kBlock + (t & 7) * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int t = t0 + u * (int)blockDim.x + (int)threadIdx.x;
+        const int blk = t >> 3;
+        int32_t q;
+        float sq = 0.0f;
+        quantize_block8(v[u], blk < a.blocks, lane, &q, &sq);
+        if (blk < nblk) {
+          ((int32_t *)qa_l)[t] = q;
+          if ((t & 7) == 0) sa_l[blk] = sq;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
   if (active) {
     if constexpr (PC > 0) {
 #pragma unroll
       for (int p = 0; p < PC; ++p) {
         consume(p % D, p);
+        __builtin_amdgcn_sched_barrier(0);
         if (p + D < PC) issue(p % D, p + D);
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else {
       for (int p0 = 0; p0 < passes; p0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-          const int p = p0 + d;
-          if (p < passes) {
-            consume(d, p);
-            issue(d, p + D);
+          if (p0 + d < passes) {
+            consume(d, p0 + d);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(d, p0 + d + D);
+            __builtin_amdgcn_sched_barrier(0);
           }
         }
       }
     }
   }
 
-  const int r = lane >> 4;
   const int64_t row = g * kLanes + r;
   float y;
   if (NMAT == 2)
     y = silu(acc[0]) * acc[NMAT - 1];
   else
     y = ACT == 1 ? silu(acc[0]) : acc[0];
-  const bool owner = active && (lane & 15) == 15;
+  const bool owner = active && j == 15;
   if (owner) a.y[row] = y;
+
+  if (QOUT) {
+    // The workgroup's 8 waves produced output rows 32*blockIdx.x .. +31.
+    // The last wave to finish (LDS arrival count, no barrier, so finished
+    // waves leave at once) quantizes that block (Q8Decode.cpp:83-120).
+    if (owner) y_l[wave * kLanes + r] = y;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    unsigned arrived = 0;
+    if (lane == 0) arrived = atomicAdd(&count_l, 1u);
+    arrived = (unsigned)__shfl((int)arrived, 0);
+    if (arrived == (unsigned)waves - 1) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      const float v = lane < kBlock ? y_l[lane] : 0.0f;
+      float m = fabsf(v);
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+      const float sq = m / 127.0f;
+      const float inv = m == 0.0f ? 0.0f : 1.0f / sq;
+      if (lane < kBlock)
+        a.qout[(int64_t)blockIdx.x * kBlock + lane] = (int8_t)(int)rintf(v * inv);
+      if (lane == 0) a.sout[blockIdx.x] = sq;
+    }
+  }
 
   if (ARGMAX) {
     unsigned long long key = owner ? argmax_key(y, row) : 0ull;
@@ -376,17 +498,39 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     if (threadIdx.x == 0) {
       unsigned long long best = key_l[0];
       for (int w = 1; w < waves; ++w) best = key_l[w] > best ? key_l[w] : best;
-      atomicMax(&a.am->key, best);
-      __threadfence();
-      const unsigned int ticket = atomicAdd(&a.am->ticket, 1u);
-      if (ticket == gridDim.x - 1) {
-        __threadfence();
-        const unsigned long long k = atomicAdd(&a.am->key, 0ull);
-        *a.am_out = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
-        atomicExch(&a.am->key, 0ull);
-        atomicExch(&a.am->ticket, 0u);
-      }
+      a.keys[blockIdx.x] = best;
     }
+  }
+}
+
+// Second stage of the fused argmax: one workgroup reduces the per-workgroup
+// keys and writes the index of the first maximum.  Loads are issued 16 deep
+// per thread so the pass costs one memory latency.
+__global__ __launch_bounds__(1024) void argmax_reduce_kernel(
+    const unsigned long long *__restrict__ keys, int64_t n, int64_t *out) {
+  __shared__ unsigned long long part[16];
+  unsigned long long best = 0ull;
+  for (int64_t i0 = 0; i0 < n; i0 += 16 * 1024) {
+    unsigned long long k[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int64_t i = i0 + u * 1024 + threadIdx.x;
+      k[u] = i < n ? keys[i] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) best = k[u] > best ? k[u] : best;
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned long long other = __shfl_xor(best, off);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+      best = part[w] > best ? part[w] : best;
+    *out = (int64_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
   }
 }
 
@@ -462,32 +606,30 @@ inline unsigned grid_for(int64_t threads, int block) {
   return (unsigned)((threads + block - 1) / block);
 }
 
-template <int NMAT, int ACT, bool ARGMAX, bool PREQ, int PC>
-hipError_t launch_gemv_p(const GemvArgs &args, int waves, size_t lds_bytes,
-                         hipStream_t s) {
-  constexpr int D = PC > 0 ? (PC < (NMAT == 2 ? 6 : 12) ? PC : (NMAT == 2 ? 6 : 12))
-                           : (NMAT == 2 ? 4 : 8);
+template <int NMAT, int ACT, bool ARGMAX, int IN, bool QOUT, int PC>
+hipError_t launch_gemv_p(const GemvArgs &args, int waves, hipStream_t s) {
+  constexpr int DMAX = NMAT == 2 ? 4 : 12;
+  constexpr int D = PC > 0 ? (PC < DMAX ? PC : DMAX) : (NMAT == 2 ? 4 : 8);
   const unsigned grid = (unsigned)((args.groups + waves - 1) / waves);
-  hipLaunchKernelGGL((gemv_kernel<NMAT, ACT, ARGMAX, D, PREQ, PC>), dim3(grid),
-                     dim3(64 * waves), lds_bytes, s, args);
+  const size_t lds = IN == IN_WG ? (size_t)args.passes * kPassBlocks * (kBlock + 4) : 0;
+  hipLaunchKernelGGL((gemv_kernel<NMAT, ACT, ARGMAX, IN, QOUT, D, PC>),
+                     dim3(grid), dim3(64 * waves), lds, s, args);
   return hipGetLastError();
 }
 
-// Pass counts with a fully unrolled kernel: K = 512..4096 step 512, and
-// K = 9216 (the MLP down projection).  Others take the runtime loop.
-template <int NMAT, int ACT, bool ARGMAX, bool PREQ>
-hipError_t launch_gemv_t(const GemvArgs &args, int waves, size_t lds_bytes,
-                         hipStream_t s) {
+// Pass counts with a fully unrolled kernel: K = 512, 1024, 1536, 2560
+// (hidden size), 4096 and 9216 (the MLP down projection).  Others take the
+// runtime loop.
+template <int NMAT, int ACT, bool ARGMAX, int IN, bool QOUT>
+hipError_t launch_gemv_t(const GemvArgs &args, int waves, hipStream_t s) {
   switch (args.passes) {
-    case 1: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 1>(args, waves, lds_bytes, s);
-    case 2: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 2>(args, waves, lds_bytes, s);
-    case 3: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 3>(args, waves, lds_bytes, s);
-    case 4: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 4>(args, waves, lds_bytes, s);
-    case 5: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 5>(args, waves, lds_bytes, s);
-    case 6: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 6>(args, waves, lds_bytes, s);
-    case 8: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 8>(args, waves, lds_bytes, s);
-    case 18: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 18>(args, waves, lds_bytes, s);
-    default: return launch_gemv_p<NMAT, ACT, ARGMAX, PREQ, 0>(args, waves, lds_bytes, s);
+    case 1: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 1>(args, waves, s);
+    case 2: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 2>(args, waves, s);
+    case 3: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 3>(args, waves, s);
+    case 5: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 5>(args, waves, s);
+    case 8: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 8>(args, waves, s);
+    case 18: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 18>(args, waves, s);
+    default: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 0>(args, waves, s);
   }
 }
 
@@ -532,6 +674,47 @@ hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
   return hipGetLastError();
 }
 
+// Launch shape of a one-row GEMV over `rows` outputs.
+//   fused MLP gate/up (quantized output)   8 waves, input quantized per WG
+//   wide SwiGLU (>= 2048 groups)           8 waves, input quantized per WG
+//   <= kInLoopQuantMaxGroups groups        1 wave,  input quantized per wave
+//   wider (lm_head)                        4 waves, pre-quantized input
+struct GemvShape {
+  int waves;
+  int in;
+};
+
+static GemvShape gemv_shape(int64_t rows, int nmat, bool qout, bool have_x) {
+  const int64_t groups = rows / kLanes;
+  if (have_x && (qout || (nmat == 2 && groups >= 2048))) return {8, IN_WG};
+  if (have_x) return {1, IN_WAVE};
+  return {groups >= 8192 ? 4 : 1, IN_PRE};
+}
+
+bool gemv_quantizes_input(int64_t rows, int nmat) {
+  return nmat == 2 || rows / kLanes <= kInLoopQuantMaxGroups;
+}
+
+int64_t gemv_workgroups(int64_t rows) {
+  // Argmax partials are only used by one-matrix GEMVs without QOUT.
+  const int64_t groups = rows / kLanes;
+  const int w = gemv_quantizes_input(rows, 1) ? 1 : (groups >= 8192 ? 4 : 1);
+  return (groups + w - 1) / w;
+}
+
+template <int IN>
+static hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
+                                 int waves, hipStream_t s) {
+  if (l.nmat == 2) {
+    if (IN == IN_WG && l.qout) return launch_gemv_t<2, 0, false, IN, true>(a, waves, s);
+    return launch_gemv_t<2, 0, false, IN, false>(a, waves, s);
+  }
+  if (IN == IN_WG) return hipErrorInvalidValue;  // one-matrix GEMVs use WAVE/PRE
+  if (l.keys) return launch_gemv_t<1, 0, true, IN, false>(a, waves, s);
+  if (l.activation == 1) return launch_gemv_t<1, 1, false, IN, false>(a, waves, s);
+  return launch_gemv_t<1, 0, false, IN, false>(a, waves, s);
+}
+
 hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
   GemvArgs a;
   a.x = l.x;
@@ -540,28 +723,26 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
   a.w0 = l.w[0];
   a.w1 = l.w[1] ? l.w[1] : l.w[0];
   a.y = l.y;
-  a.am = l.argmax;
-  a.am_out = l.argmax_out;
+  a.keys = l.keys;
+  a.qout = l.qout;
+  a.sout = l.sout;
   a.groups = l.rows / kLanes;
   a.blocks = (int32_t)(l.cols / kBlock);
   a.passes = (int32_t)passes_for(l.cols);
-  a.x_aligned = l.x && ((uintptr_t)l.x % 16 == 0) ? 1 : 0;
-  const int64_t nblk = (int64_t)a.passes * kPassBlocks;
-  const size_t lds_bytes = (size_t)(nblk * kBlock + nblk * 4 + 8 * 8);
-  const bool preq = l.qa != nullptr;
-  // Few groups (small N) -> one wave per workgroup and deep prefetch so
-  // every CU gets work and enough bytes are in flight.
-  const int waves = a.groups >= 8192 ? 4 : 1;
-  if (preq) {
-    if (l.nmat == 2) return launch_gemv_t<2, 0, false, true>(a, waves, lds_bytes, s);
-    if (l.argmax) return launch_gemv_t<1, 0, true, true>(a, waves, lds_bytes, s);
-    if (l.activation == 1) return launch_gemv_t<1, 1, false, true>(a, waves, lds_bytes, s);
-    return launch_gemv_t<1, 0, false, true>(a, waves, lds_bytes, s);
-  }
-  if (l.nmat == 2) return launch_gemv_t<2, 0, false, false>(a, waves, lds_bytes, s);
-  if (l.argmax) return launch_gemv_t<1, 0, true, false>(a, waves, lds_bytes, s);
-  if (l.activation == 1) return launch_gemv_t<1, 1, false, false>(a, waves, lds_bytes, s);
-  return launch_gemv_t<1, 0, false, false>(a, waves, lds_bytes, s);
+  const GemvShape sh = gemv_shape(l.rows, l.nmat, l.qout != nullptr, l.x != nullptr);
+  if (l.qout && (sh.in != IN_WG || l.rows % kBlock)) return hipErrorInvalidValue;
+  hipError_t e;
+  if (sh.in == IN_WG)
+    e = launch_gemv_in<IN_WG>(a, l, sh.waves, s);
+  else if (sh.in == IN_WAVE)
+    e = launch_gemv_in<IN_WAVE>(a, l, sh.waves, s);
+  else
+    e = launch_gemv_in<IN_PRE>(a, l, sh.waves, s);
+  if (e != hipSuccess || !l.keys) return e;
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(1024), 0, s,
+                     (const unsigned long long *)l.keys,
+                     (a.groups + sh.waves - 1) / sh.waves, l.argmax_out);
+  return hipGetLastError();
 }
 
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,

@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <map>
@@ -67,12 +68,24 @@ struct llmcp_q8_ctx {
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   std::map<uintptr_t, Tensor> registry;  // by key
-  ArgmaxState *argmax = nullptr;
   int32_t *err_flag = nullptr;
-  int8_t *qa = nullptr;  // activation scratch (quantized input)
+  // Workspace, sized when weights are registered so that decode-time calls
+  // (and graph capture) never allocate: the quantized input row, its scales
+  // and the per-workgroup argmax keys of the lm_head.
+  int8_t *qa = nullptr;
   float *sa = nullptr;
+  unsigned long long *keys = nullptr;
   uint64_t qa_bytes = 0;
   uint64_t sa_bytes = 0;
+  uint64_t keys_bytes = 0;
+  // Fused MLP: Q8_1 of the SwiGLU output for the down projection and an f32
+  // spill of h.
+  int8_t *hq = nullptr;
+  float *hs = nullptr;
+  float *hf = nullptr;
+  uint64_t hq_bytes = 0;
+  uint64_t hs_bytes = 0;
+  uint64_t hf_bytes = 0;
   hipGraph_t capture = nullptr;
 };
 
@@ -113,26 +126,43 @@ bool dense_rows(const llmcp_memref_f32_2d *d) {
          d->sizes[1] > 0 && (d->sizes[0] <= 1 || d->strides[0] >= d->sizes[1]);
 }
 
-int ensure_scratch(llmcp_q8_ctx *ctx, uint64_t qa_bytes, uint64_t sa_bytes) {
-  if (qa_bytes > ctx->qa_bytes) {
-    if (ctx->qa) HIP_TRY(hipFree(ctx->qa));
-    ctx->qa = nullptr;
-    ctx->qa_bytes = 0;
-    if (hipMalloc(&ctx->qa, qa_bytes) != hipSuccess)
-      return fail(LLMCP_Q8_ENOMEM, "activation scratch of %llu bytes",
-                  (unsigned long long)qa_bytes);
-    ctx->qa_bytes = qa_bytes;
+template <typename T>
+int grow(llmcp_q8_ctx *ctx, T *&ptr, uint64_t &have, uint64_t need,
+         const char *what) {
+  if (need <= have) return LLMCP_Q8_OK;
+  if (ptr) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipFree(ptr));
   }
-  if (sa_bytes > ctx->sa_bytes) {
-    if (ctx->sa) HIP_TRY(hipFree(ctx->sa));
-    ctx->sa = nullptr;
-    ctx->sa_bytes = 0;
-    if (hipMalloc(&ctx->sa, sa_bytes) != hipSuccess)
-      return fail(LLMCP_Q8_ENOMEM, "scale scratch of %llu bytes",
-                  (unsigned long long)sa_bytes);
-    ctx->sa_bytes = sa_bytes;
-  }
+  ptr = nullptr;
+  have = 0;
+  if (hipMalloc((void **)&ptr, need) != hipSuccess)
+    return fail(LLMCP_Q8_ENOMEM, "%s of %llu bytes", what,
+                (unsigned long long)need);
+  have = need;
   return LLMCP_Q8_OK;
+}
+
+int ensure_scratch(llmcp_q8_ctx *ctx, uint64_t qa_bytes, uint64_t sa_bytes,
+                   uint64_t keys_bytes = 0) {
+  int rc = grow(ctx, ctx->qa, ctx->qa_bytes, qa_bytes, "activation scratch");
+  if (!rc) rc = grow(ctx, ctx->sa, ctx->sa_bytes, sa_bytes, "scale scratch");
+  if (!rc) rc = grow(ctx, ctx->keys, ctx->keys_bytes, keys_bytes, "argmax keys");
+  return rc;
+}
+
+// Workspace a one-row call against a [rows, cols] weight needs, including
+// the quantized-output buffers should its output feed another GEMV.
+int ensure_decode_scratch(llmcp_q8_ctx *ctx, int64_t rows, int64_t cols) {
+  const uint64_t nblk = (uint64_t)passes_for(cols) * kPassBlocks;
+  int rc = ensure_scratch(ctx, nblk * kBlock, nblk * 4,
+                          (uint64_t)gemv_workgroups(rows) * 8u);
+  if (rc || rows % kBlock) return rc;
+  const uint64_t oblk = (uint64_t)passes_for(rows) * kPassBlocks;
+  rc = grow(ctx, ctx->hq, ctx->hq_bytes, oblk * kBlock, "output quant scratch");
+  if (!rc) rc = grow(ctx, ctx->hs, ctx->hs_bytes, oblk * 4, "output scales");
+  if (!rc) rc = grow(ctx, ctx->hf, ctx->hf_bytes, (uint64_t)rows * 4, "mlp hidden");
+  return rc;
 }
 
 // Repacks device p4 bytes into a new registry entry under `key`.
@@ -165,6 +195,11 @@ int register_from_device_p4(llmcp_q8_ctx *ctx, const void *key,
     HIP_TRY(hipEventElapsedTime(repack_ms, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+  }
+  int rc = ensure_decode_scratch(ctx, rows, cols);
+  if (rc) {
+    (void)hipFree(t.dev);
+    return rc;
   }
   auto old = ctx->registry.find(t.key);
   if (old != ctx->registry.end()) {
@@ -255,13 +290,11 @@ int llmcp_q8_ctx_create(int device, llmcp_q8_ctx **out) {
     return hip_fail(e, "hipStreamCreateWithFlags");
   }
   ctx->stream = ctx->own_stream;
-  if (hipMalloc(&ctx->argmax, sizeof(ArgmaxState)) != hipSuccess ||
-      hipMalloc(&ctx->err_flag, sizeof(int32_t)) != hipSuccess) {
+  if (hipMalloc(&ctx->err_flag, sizeof(int32_t)) != hipSuccess) {
     llmcp_q8_ctx_destroy(ctx);
     return fail(LLMCP_Q8_ENOMEM, "context workspace");
   }
-  if (hipMemset(ctx->argmax, 0, sizeof(ArgmaxState)) != hipSuccess ||
-      hipMemset(ctx->err_flag, 0, sizeof(int32_t)) != hipSuccess ||
+  if (hipMemset(ctx->err_flag, 0, sizeof(int32_t)) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {
     llmcp_q8_ctx_destroy(ctx);
     return fail(LLMCP_Q8_EHIP, "context workspace init");
@@ -277,10 +310,13 @@ int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx) {
   if (ctx->stream && ctx->stream != ctx->own_stream)
     (void)hipStreamSynchronize(ctx->stream);
   for (auto &kv : ctx->registry) (void)hipFree(kv.second.dev);
-  if (ctx->argmax) (void)hipFree(ctx->argmax);
   if (ctx->err_flag) (void)hipFree(ctx->err_flag);
   if (ctx->qa) (void)hipFree(ctx->qa);
   if (ctx->sa) (void)hipFree(ctx->sa);
+  if (ctx->keys) (void)hipFree(ctx->keys);
+  if (ctx->hq) (void)hipFree(ctx->hq);
+  if (ctx->hs) (void)hipFree(ctx->hs);
+  if (ctx->hf) (void)hipFree(ctx->hf);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   if (g_default_ctx == ctx) g_default_ctx = nullptr;
   delete ctx;
@@ -514,22 +550,43 @@ int llmcp_q8_upload_arena(llmcp_q8_ctx *ctx, const void *file,
 
 // ------------------------------------------------------------------ ops --
 
-static int gemv_common(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
-                       const Tensor *w0, const Tensor *w1,
-                       llmcp_memref_f32_2d *output, int activation,
-                       int64_t *argmax_dev) {
+// One-row GEMV (decode, or prefill with M == 1).  Narrow outputs quantize
+// the input inside the GEMV; wide ones (lm_head) quantize it once first.
+static int gemv_common(llmcp_q8_ctx *ctx, const float *x, const Tensor *w0,
+                       const Tensor *w1, float *y, int activation,
+                       int64_t *argmax_dev, bool quantize_out) {
+  int rc = ensure_decode_scratch(ctx, w0->rows, w0->cols);
+  if (rc) return rc;
   GemvLaunch l;
-  l.x = input->data + input->offset;
+  const bool in_loop = gemv_quantizes_input(w0->rows, w1 ? 2 : 1) &&
+                       (uintptr_t)x % 16 == 0;
+  if (quantize_out && !in_loop)
+    return fail(LLMCP_Q8_DECLINED, "fused MLP needs a 16-byte aligned input");
+  if (in_loop) {
+    l.x = x;
+  } else {
+    const int64_t nblk = passes_for(w0->cols) * kPassBlocks;
+    hipError_t e = launch_quantize(x, 1, w0->cols, w0->cols, ctx->qa,
+                                   nblk * kBlock, ctx->sa, nblk, nblk,
+                                   ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+    l.qa = ctx->qa;
+    l.sa = ctx->sa;
+  }
   l.w[0] = w0->dev;
   l.w[1] = w1 ? w1->dev : nullptr;
-  l.y = output->data + output->offset;
+  l.y = y;
   l.rows = w0->rows;
   l.cols = w0->cols;
   l.nmat = w1 ? 2 : 1;
   l.activation = activation;
   if (argmax_dev) {
-    l.argmax = ctx->argmax;
+    l.keys = ctx->keys;
     l.argmax_out = argmax_dev;
+  }
+  if (quantize_out) {
+    l.qout = ctx->hq;
+    l.sout = ctx->hs;
   }
   hipError_t e = launch_gemv(l, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "gemv launch");
@@ -570,12 +627,16 @@ int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
     if (m != 1)
       return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
                   (long long)m);
-    return gemv_common(ctx, input, w, nullptr, output, activation, nullptr);
+    return gemv_common(ctx, input->data + input->offset, w, nullptr,
+                       output->data + output->offset, activation, nullptr,
+                       false);
   }
   if (execution_mode != LLMCP_Q8_PREFILL)
     return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
   if (m == 1)
-    return gemv_common(ctx, input, w, nullptr, output, activation, nullptr);
+    return gemv_common(ctx, input->data + input->offset, w, nullptr,
+                       output->data + output->offset, activation, nullptr,
+                       false);
   return fail(LLMCP_Q8_DECLINED, "prefill GEMM for M > 1 not available");
 }
 
@@ -598,7 +659,9 @@ int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
     return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
   if (m != 1)
     return fail(LLMCP_Q8_DECLINED, "fused SwiGLU for M > 1 not available");
-  return gemv_common(ctx, input, wg, wu, output, LLMCP_Q8_ACT_NONE, nullptr);
+  return gemv_common(ctx, input->data + input->offset, wg, wu,
+                     output->data + output->offset, LLMCP_Q8_ACT_NONE, nullptr,
+                     false);
 }
 
 int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
@@ -617,8 +680,66 @@ int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
     return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
   if (m != 1)
     return fail(LLMCP_Q8_DECLINED, "lm_head for M > 1 not available");
-  return gemv_common(ctx, hidden, w, nullptr, logits, LLMCP_Q8_ACT_NONE,
-                     argmax_dev);
+  return gemv_common(ctx, hidden->data + hidden->offset, w, nullptr,
+                     logits->data + logits->offset, LLMCP_Q8_ACT_NONE,
+                     argmax_dev, false);
+}
+
+int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                 const llmcp_memref_i8_1d *w_gate,
+                 const llmcp_memref_i8_1d *w_up,
+                 const llmcp_memref_i8_1d *w_down, llmcp_memref_f32_2d *hidden,
+                 llmcp_memref_f32_2d *output, int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  const Tensor *wg = nullptr, *wu = nullptr, *wd = nullptr;
+  int rc = resolve_weight(ctx, w_gate, &wg);
+  if (!rc) rc = resolve_weight(ctx, w_up, &wu);
+  if (!rc) rc = resolve_weight(ctx, w_down, &wd);
+  if (rc) return rc;
+  if (wg->rows != wu->rows || wg->cols != wu->cols || wd->cols != wg->rows ||
+      wd->rows != wg->cols)
+    return fail(LLMCP_Q8_DECLINED, "gate/up [F,H] and down [H,F] shapes differ");
+  if (wg->rows % kBlock)
+    return fail(LLMCP_Q8_DECLINED, "MLP width must be a multiple of 32");
+  if (!dense_rows(input) || !dense_rows(output) || input->sizes[1] != wg->cols ||
+      output->sizes[1] != wd->rows || output->sizes[0] != input->sizes[0])
+    return fail(LLMCP_Q8_DECLINED, "MLP input/output must be [M, H] row-major");
+  if (hidden && (!dense_rows(hidden) || hidden->sizes[1] != wg->rows ||
+                 hidden->sizes[0] != input->sizes[0]))
+    return fail(LLMCP_Q8_DECLINED, "MLP hidden must be [M, F] row-major");
+  if (execution_mode != LLMCP_Q8_DECODE && execution_mode != LLMCP_Q8_PREFILL)
+    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
+  const int64_t m = input->sizes[0];
+  if (m == 0) return LLMCP_Q8_OK;
+  if (m != 1) return fail(LLMCP_Q8_DECLINED, "fused MLP needs M == 1");
+  if ((rc = set_device(ctx))) return rc;
+  if ((rc = ensure_decode_scratch(ctx, wg->rows, wg->cols))) return rc;
+  float *h = hidden ? hidden->data + hidden->offset : ctx->hf;
+  static const int down_in_loop = [] {
+    const char *v = std::getenv("LLMCP_Q8_MLP_DOWN_IN");
+    return v && std::strcmp(v, "wave") == 0 ? 1 : 0;
+  }();
+  if (down_in_loop) {
+    rc = gemv_common(ctx, input->data + input->offset, wg, wu, h,
+                     LLMCP_Q8_ACT_NONE, nullptr, false);
+    if (!rc)
+      rc = gemv_common(ctx, h, wd, nullptr, output->data + output->offset,
+                       LLMCP_Q8_ACT_NONE, nullptr, false);
+    return rc;
+  }
+  rc = gemv_common(ctx, input->data + input->offset, wg, wu, h,
+                   LLMCP_Q8_ACT_NONE, nullptr, true);
+  if (rc) return rc;
+  GemvLaunch l;
+  l.qa = ctx->hq;
+  l.sa = ctx->hs;
+  l.w[0] = wd->dev;
+  l.y = output->data + output->offset;
+  l.rows = wd->rows;
+  l.cols = wd->cols;
+  hipError_t e = launch_gemv(l, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "down gemv launch");
+  return LLMCP_Q8_OK;
 }
 
 int llmcp_q8_embedding(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,

@@ -164,6 +164,53 @@ def test_decode_mlp_end_to_end(ctx, oracle):
         ctx.release(t)
 
 
+def test_fused_mlp_matches_separate_ops(ctx, oracle):
+    # llmcp_q8_mlp: gate/up GEMV quantizes h for the down GEMV in its own
+    # epilogue (ticketed); the result must equal swiglu -> linear bit for bit,
+    # over repeated calls (tickets reset) and for a width that leaves a
+    # partial last pass (ffn = 1056 -> 33 blocks).
+    rng = np.random.default_rng(21)
+    for hidden, ffn in ((2560, 9216), (512, 1056)):
+        wg, wu, wd = weights(rng, ffn, hidden), weights(rng, ffn, hidden), weights(rng, hidden, ffn)
+        pg, pu, pd = (oracle.pack_q8_0_p4(w) for w in (wg, wu, wd))
+        tg, tu, td = ctx.upload_p4(pg, ffn, hidden), ctx.upload_p4(pu, ffn, hidden), ctx.upload_p4(pd, hidden, ffn)
+        for trial in range(3):
+            x = rng.standard_normal((1, hidden)).astype(np.float32)
+            xd, hd, yd = ctx.to_device(x), ctx.alloc(ffn * 4), ctx.alloc(hidden * 4)
+            ctx.mlp(xd, tg, tu, td, yd, h=hd)
+            h = ctx.to_host(hd, (1, ffn), np.float32)
+            y = ctx.to_host(yd, (1, hidden), np.float32)
+            h_ref = oracle.swiglu(x, pg, pu, ffn, colpar=True)
+            y_ref = oracle.linear(h_ref, pd, hidden, colpar=True)
+            assert bits_equal(h, h_ref)
+            assert bits_equal(y, y_ref), (hidden, ffn, trial)
+            y2d = ctx.alloc(hidden * 4)
+            ctx.mlp(xd, tg, tu, td, y2d)  # internal h buffer
+            assert bits_equal(ctx.to_host(y2d, (1, hidden), np.float32), y_ref)
+        for t in (tg, tu, td):
+            ctx.release(t)
+
+
+def test_wide_output_uses_prequantized_input(ctx, oracle, q8):
+    # N > 16384 quantizes the row once before the GEMV; a misaligned input
+    # row takes the same path.  Both must match the reference bit for bit.
+    rng = np.random.default_rng(22)
+    n, k = 16416, 512
+    w = weights(rng, n, k)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    y, p4 = run_linear(ctx, oracle, w, x)
+    assert bits_equal(y, oracle.linear(x, p4, n))
+    n2 = 264
+    w2 = weights(rng, n2, k)
+    p42 = oracle.pack_q8_0_p4(w2)
+    t = ctx.upload_p4(p42, n2, k)
+    xd = ctx.to_device(np.concatenate([[0.0], x.ravel()]).astype(np.float32))
+    yd = ctx.alloc(n2 * 4)
+    ctx.linear(xd.ptr + 4, t, yd, 1)
+    assert bits_equal(ctx.to_host(yd, (1, n2), np.float32), oracle.linear(x, p42, n2))
+    ctx.release(t)
+
+
 def test_lm_head_argmax_and_ties(ctx, oracle):
     rng = np.random.default_rng(12)
     v, k = 4096, 2560
