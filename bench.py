@@ -180,6 +180,108 @@ def bench_lm_head(ctx, v=248320, k=2560, iters=20):
                 gather_us=us2, gather_gb_s=gather_bytes / (us2 * 1e-6) / 1e9)
 
 
+def bench_gemm(ctx, m, n=9216, k=2560, iters=30):
+    """Config 4: prefill GEMM, activation quantization included ("op") and
+    the quantize kernel alone, over a rotating pool of weight copies."""
+    per = p4_bytes(n, k)
+    copies = max(2, -(-int(1.6 * MALL_BYTES) // per)) if m <= 256 else 2
+    ws = []
+    for c in range(copies):
+        p4d, _ = ctx.synthesize_p4(seed=7000 + c, rows=n, cols=k)
+        ws.append((ctx.register_device_p4(p4d, n, k), p4d))
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    xd, yd = ctx.to_device(x), ctx.alloc(m * n * 4)
+    qd, sd = ctx.alloc(m * k), ctx.alloc(m * k // 32 * 4)
+    ctx.linear(xd, ws[0][0], yd, m, mode="prefill")  # first call sizes scratch
+    ctx.sync()
+
+    def rot():
+        for w, _ in ws:
+            ctx.linear(xd, w, yd, m, mode="prefill")
+
+    def qrot():
+        for _ in ws:
+            ctx.quantize(xd, m, k, qd, sd)
+
+    timer = Timer(ctx)
+    g, gq = graph_of(ctx, rot), graph_of(ctx, qrot)
+    rounds = max(1, iters // copies)
+    run_graph(ctx, timer, g, 1)
+    us = run_graph(ctx, timer, g, rounds) * 1e3 / (rounds * copies)
+    run_graph(ctx, timer, gq, 1)
+    q_us = run_graph(ctx, timer, gq, rounds) * 1e3 / (rounds * copies)
+    for w, p4d in ws:
+        ctx.release(w)
+        p4d.free()
+    ops = 2.0 * m * n * k
+    kern = max(us - q_us, 1e-3)
+    return {"op_us": round(us, 2), "quantize_us": round(q_us, 2),
+            "gemm_us": round(kern, 2),
+            "op_TOPS": round(ops / (us * 1e-6) / 1e12, 1),
+            "gemm_TOPS": round(ops / (kern * 1e-6) / 1e12, 1),
+            "frac_int8_peak": round(ops / (kern * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+            "bytes": per + m * k * 4 + m * n * 4}
+
+
+def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320):
+    """Config 5: every Q8_0 linear of a 32-layer 4B-class model plus the tied
+    lm_head, all resident in HBM, at M=1 (decode) and M=1024 (prefill)."""
+    shapes = [("gate", ffn, hidden), ("up", ffn, hidden), ("down", hidden, ffn),
+              ("qkv", qkv, hidden), ("o", hidden, hidden), ("a", hidden, hidden),
+              ("b", hidden, hidden)]
+    layer = []
+    total = 0
+    for li in range(layers):
+        ws = {}
+        for j, (name, n, k) in enumerate(shapes):
+            p4d, _ = ctx.synthesize_p4(seed=100000 + 16 * li + j, rows=n, cols=k)
+            ws[name] = (ctx.register_device_p4(p4d, n, k), p4d)
+            total += p4_bytes(n, k)
+        layer.append(ws)
+    p4d, _ = ctx.synthesize_p4(seed=99, rows=vocab, cols=hidden)
+    head = (ctx.register_device_p4(p4d, vocab, hidden), p4d)
+    total += p4_bytes(vocab, hidden)
+    rng = np.random.default_rng(5)
+    out = {"weight_bytes": total, "linears": layers * len(shapes) + 1}
+    timer = Timer(ctx)
+    for m, mode in ((1, "decode"), (1024, "prefill")):
+        x = ctx.to_device(rng.standard_normal((m, hidden)).astype(np.float32))
+        h = ctx.to_device(rng.standard_normal((m, ffn)).astype(np.float32))
+        yq, yh = ctx.alloc(m * qkv * 4), ctx.alloc(m * ffn * 4)
+        y = ctx.alloc(m * hidden * 4)
+        logits, am = ctx.alloc(vocab * 4), ctx.alloc(8)
+
+        def step():
+            for ws in layer:
+                ctx.linear(x, ws["qkv"][0], yq, m, mode=mode)
+                for nm in ("o", "a", "b"):
+                    ctx.linear(x, ws[nm][0], y, m, mode=mode)
+                if m == 1:
+                    ctx.mlp(x, ws["gate"][0], ws["up"][0], ws["down"][0], y, h=yh)
+                else:
+                    ctx.swiglu(x, ws["gate"][0], ws["up"][0], yh, m, mode=mode)
+                    ctx.linear(h, ws["down"][0], y, m, mode=mode)
+            ctx.lm_head(x, head[0], logits, 1, argmax=am, mode=mode)
+
+        step()  # sizes scratch outside capture
+        ctx.sync()
+        g = graph_of(ctx, step)
+        run_graph(ctx, timer, g, 1)
+        reps = 10 if m == 1 else 3
+        us = run_graph(ctx, timer, g, reps) * 1e3 / reps
+        ops = 2.0 * m * (total - p4_bytes(vocab, hidden)) * 32 / 34 + 2.0 * vocab * hidden
+        key = "m%d" % m
+        out[key] = {"us": round(us, 1), "GB/s": round(total / (us * 1e-6) / 1e9, 1),
+                    "TOPS": round(ops / (us * 1e-6) / 1e12, 2)}
+    for ws in layer:
+        for w, p4d in ws.values():
+            ctx.release(w)
+            p4d.free()
+    ctx.release(head[0])
+    head[1].free()
+    return out
+
+
 def cpu_baseline(res, budget_s=12.0):
     """Reference x86 scalar Q8 path (oracle restatement) on the host cores."""
     from oracle import q8_oracle as o
@@ -242,6 +344,9 @@ def main():
             "frac_hbm": round(c3["gb_s"] / HBM_PEAK_GBS, 4)}
         extra["embedding_gather_1024"] = {"us": round(c3["gather_us"], 2),
                                           "GB/s": round(c3["gather_gb_s"], 1)}
+        for m in (64, 256, 1024):
+            extra["gemm_m%d_n9216_k2560" % m] = bench_gemm(ctx, m)
+        extra["sequence_32_layers"] = bench_sequence(ctx)
     cpu = None if args.no_cpu else cpu_baseline(res)
     line = {
         "metric": "Q8_0 linear: M=1 GEMV HBM GB/s (% peak); M=1024 GEMM int8 TOPS (% peak)",

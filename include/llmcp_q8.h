@@ -57,6 +57,12 @@ enum llmcp_q8_status {
 
 enum llmcp_q8_activation { LLMCP_Q8_ACT_NONE = 0, LLMCP_Q8_ACT_SILU = 1 };
 
+/* Per-block epilogue of the prefill GEMM.  Both are the reference's math:
+ * FMA    acc = fma(f32(I), sa*dw, acc)  -- the SDOT GEMM, Q8Matmul.cpp:204-223
+ * SCALAR acc = acc + f32(I)*(sa*dw)     -- the x86 scalar path, Q8Scalar.cpp:192-199
+ * The decode GEMV always computes the SCALAR form. */
+enum llmcp_q8_epilogue { LLMCP_Q8_EPI_SCALAR = 0, LLMCP_Q8_EPI_FMA = 1 };
+
 /* llmcp.execution_mode (LowerToLinalg.cpp:40-52). */
 enum llmcp_q8_mode { LLMCP_Q8_PREFILL = 0, LLMCP_Q8_DECODE = 1 };
 
@@ -101,6 +107,8 @@ int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx);
 int llmcp_q8_ctx_set_stream(llmcp_q8_ctx *ctx, void *hip_stream);
 void *llmcp_q8_ctx_stream(llmcp_q8_ctx *ctx);
 int llmcp_q8_ctx_synchronize(llmcp_q8_ctx *ctx);
+/* Selects the prefill GEMM epilogue (default LLMCP_Q8_EPI_FMA). */
+int llmcp_q8_set_gemm_epilogue(llmcp_q8_ctx *ctx, int32_t variant);
 /* Context used by the _mlir_ciface_* entries (set by the AOT runtime). */
 int llmcp_q8_set_default_ctx(llmcp_q8_ctx *ctx);
 
@@ -141,7 +149,7 @@ int llmcp_q8_arena_inspect(const void *file, uint64_t file_bytes,
 /* llmcp.linear with weight_format q8_0_p4 (LowerToLinalg.cpp:143-209):
  * y[M,N] = act(x[M,K] . W[N,K]^T), x quantized per call to Q8_1 blocks.
  * execution_mode DECODE requires M == 1 and runs the GEMV; PREFILL runs the
- * int8-MFMA GEMM for any M.  activation: NONE or SILU
+ * int8-MFMA GEMM for any M (its epilogue: llmcp_q8_set_gemm_epilogue).  activation: NONE or SILU
  * (applyMatmulActivation, MatmulLoweringCommon.cpp:78-103). */
 int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                     const llmcp_memref_i8_1d *weight,

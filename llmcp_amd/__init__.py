@@ -55,6 +55,7 @@ EXPORTS = [
     "llmcp_q8_abi_version", "llmcp_q8_last_error", "llmcp_q8_ctx_create",
     "llmcp_q8_ctx_destroy", "llmcp_q8_ctx_set_stream", "llmcp_q8_ctx_stream",
     "llmcp_q8_ctx_synchronize", "llmcp_q8_set_default_ctx",
+    "llmcp_q8_set_gemm_epilogue",
     "llmcp_q8_upload_p4", "llmcp_q8_register_device_p4", "llmcp_q8_release",
     "llmcp_q8_upload_arena", "llmcp_q8_arena_inspect", "llmcp_q8_linear", "llmcp_q8_swiglu",
     "llmcp_q8_lm_head", "llmcp_q8_mlp", "llmcp_q8_embedding", "llmcp_q8_quantize_activations",
@@ -92,6 +93,7 @@ def lib():
         "llmcp_q8_ctx_stream": (P, [P]),
         "llmcp_q8_ctx_synchronize": (I, [P]),
         "llmcp_q8_set_default_ctx": (I, [P]),
+        "llmcp_q8_set_gemm_epilogue": (I, [P, I32]),
         "llmcp_q8_upload_p4": (I, [P, P, I64, I64, F]),
         "llmcp_q8_register_device_p4": (I, [P, P, I64, I64, F]),
         "llmcp_q8_release": (I, [P, P]),
@@ -234,6 +236,10 @@ class Context:
 
     def __exit__(self, *exc):
         self.close()
+
+    def set_gemm_epilogue(self, variant):
+        """'fma' (SDOT GEMM, Q8Matmul.cpp) or 'scalar' (x86 path, Q8Scalar.cpp)."""
+        check(lib().llmcp_q8_set_gemm_epilogue(self.handle, {"scalar": 0, "fma": 1}[variant]))
 
     def sync(self):
         check(lib().llmcp_q8_ctx_synchronize(self.handle))

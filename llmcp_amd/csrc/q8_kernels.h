@@ -52,6 +52,28 @@ bool gemv_quantizes_input(int64_t rows, int nmat);
 hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s);
 int64_t gemv_workgroups(int64_t rows);
 
+// Prefill GEMM on int8 MFMA.  qa/sa: Q8_1 activations [m, ldq] / [m, lds],
+// zero-padded to passes*16 blocks (launch_quantize with blocks_pad).
+struct GemmLaunch {
+  const int8_t *qa = nullptr;
+  int64_t ldq = 0;
+  const float *sa = nullptr;
+  int64_t lds = 0;
+  const uint8_t *w = nullptr;  // pass layout
+  int64_t rows = 0;            // N
+  int64_t cols = 0;            // K
+  int64_t m = 0;               // M
+  float *y = nullptr;
+  int64_t ldy = 0;
+  int activation = 0;
+  bool fma = true;             // epilogue: fma (SDOT GEMM) or mul+add (scalar)
+};
+
+hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);
+
+// h[i] = h[i] * u[i] (f32), the SwiGLU multiply of the prefill path.
+hipError_t launch_mul(float *h, const float *u, int64_t count, hipStream_t s);
+
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             const uint8_t *table, int64_t rows, int64_t cols,
                             float *out, int64_t ldo, int32_t *err_flag,

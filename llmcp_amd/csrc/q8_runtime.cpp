@@ -83,10 +83,13 @@ struct llmcp_q8_ctx {
   int8_t *hq = nullptr;
   float *hs = nullptr;
   float *hf = nullptr;
+  float *up = nullptr;  // prefill SwiGLU: the up projection
+  uint64_t up_bytes = 0;
   uint64_t hq_bytes = 0;
   uint64_t hs_bytes = 0;
   uint64_t hf_bytes = 0;
   hipGraph_t capture = nullptr;
+  bool gemm_fma = true;  // prefill GEMM epilogue variant
 };
 
 namespace {
@@ -317,6 +320,7 @@ int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx) {
   if (ctx->hq) (void)hipFree(ctx->hq);
   if (ctx->hs) (void)hipFree(ctx->hs);
   if (ctx->hf) (void)hipFree(ctx->hf);
+  if (ctx->up) (void)hipFree(ctx->up);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   if (g_default_ctx == ctx) g_default_ctx = nullptr;
   delete ctx;
@@ -341,6 +345,14 @@ int llmcp_q8_ctx_synchronize(llmcp_q8_ctx *ctx) {
 
 int llmcp_q8_set_default_ctx(llmcp_q8_ctx *ctx) {
   g_default_ctx = ctx;
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_set_gemm_epilogue(llmcp_q8_ctx *ctx, int32_t variant) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  if (variant != LLMCP_Q8_EPI_FMA && variant != LLMCP_Q8_EPI_SCALAR)
+    return fail(LLMCP_Q8_EINVAL, "unknown epilogue variant %d", variant);
+  ctx->gemm_fma = variant == LLMCP_Q8_EPI_FMA;
   return LLMCP_Q8_OK;
 }
 
@@ -593,6 +605,39 @@ static int gemv_common(llmcp_q8_ctx *ctx, const float *x, const Tensor *w0,
   return LLMCP_Q8_OK;
 }
 
+// Prefill: quantize all M rows once (zero-padded to whole passes), then the
+// int8-MFMA GEMM.  The activation scratch grows on first use for a larger M.
+static int gemm_common(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                       const Tensor *w, llmcp_memref_f32_2d *output,
+                       int activation) {
+  const int64_t m = input->sizes[0];
+  const int64_t nblk = passes_for(w->cols) * kPassBlocks;
+  int rc = ensure_scratch(ctx, (uint64_t)(m * nblk * kBlock),
+                          (uint64_t)(m * nblk * 4));
+  if (rc) return rc;
+  hipError_t e = launch_quantize(input->data + input->offset, m,
+                                 input->strides[0], w->cols, ctx->qa,
+                                 nblk * kBlock, ctx->sa, nblk, nblk,
+                                 ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  GemmLaunch g;
+  g.qa = ctx->qa;
+  g.ldq = nblk * kBlock;
+  g.sa = ctx->sa;
+  g.lds = nblk;
+  g.w = w->dev;
+  g.rows = w->rows;
+  g.cols = w->cols;
+  g.m = m;
+  g.y = output->data + output->offset;
+  g.ldy = output->strides[0];
+  g.activation = activation;
+  g.fma = ctx->gemm_fma;
+  e = launch_gemm(g, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "gemm launch");
+  return LLMCP_Q8_OK;
+}
+
 static int check_linear_shapes(const llmcp_memref_f32_2d *input,
                                const Tensor *w, llmcp_memref_f32_2d *output) {
   if (!dense_rows(input) || !dense_rows(output))
@@ -633,11 +678,11 @@ int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
   }
   if (execution_mode != LLMCP_Q8_PREFILL)
     return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
-  if (m == 1)
+  if (m == 1)  // one row: the GEMV (scalar epilogue) beats a 1/128-full tile
     return gemv_common(ctx, input->data + input->offset, w, nullptr,
                        output->data + output->offset, activation, nullptr,
                        false);
-  return fail(LLMCP_Q8_DECLINED, "prefill GEMM for M > 1 not available");
+  return gemm_common(ctx, input, w, output, activation);
 }
 
 int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
@@ -657,8 +702,26 @@ int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
   if ((rc = set_device(ctx))) return rc;
   if (execution_mode != LLMCP_Q8_DECODE && execution_mode != LLMCP_Q8_PREFILL)
     return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
-  if (m != 1)
-    return fail(LLMCP_Q8_DECLINED, "fused SwiGLU for M > 1 not available");
+  if (m != 1) {
+    // Prefill: gate GEMM with SiLU into the output, up GEMM into scratch,
+    // then h = gate * up (MulOpLowering, LowerToLinalg.cpp:377-393).
+    if (output->strides[0] != wg->rows)
+      return fail(LLMCP_Q8_DECLINED, "prefill SwiGLU output must be dense");
+    rc = grow(ctx, ctx->up, ctx->up_bytes, (uint64_t)(m * wg->rows * 4),
+              "prefill up scratch");
+    if (rc) return rc;
+    rc = gemm_common(ctx, input, wg, output, LLMCP_Q8_ACT_SILU);
+    if (rc) return rc;
+    llmcp_memref_f32_2d up = *output;
+    up.base = up.data = ctx->up;
+    up.offset = 0;
+    rc = gemm_common(ctx, input, wu, &up, LLMCP_Q8_ACT_NONE);
+    if (rc) return rc;
+    hipError_t e = launch_mul(output->data + output->offset, ctx->up,
+                              m * wg->rows, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "mul launch");
+    return LLMCP_Q8_OK;
+  }
   return gemv_common(ctx, input->data + input->offset, wg, wu,
                      output->data + output->offset, LLMCP_Q8_ACT_NONE, nullptr,
                      false);

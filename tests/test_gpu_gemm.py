@@ -1,0 +1,115 @@
+"""GPU parity of the prefill int8-MFMA GEMM (Q8Matmul.cpp / Q8Scalar.cpp
+semantics) against the CPU oracle.  Each output element sums its blocks in
+order with the selected epilogue, so results are compared bit for bit with
+the oracle's matching epilogue and within the north-star tolerance with the
+other one."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-4
+
+
+def bits_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32),
+                          np.asarray(b, np.float32).view(np.uint32))
+
+
+def close(a, b):
+    err = np.abs(a.astype(np.float64) - b.astype(np.float64))
+    return bool(np.all((err <= ATOL) | (err <= RTOL * np.abs(b.astype(np.float64)))))
+
+
+def gemm(ctx, p4, n, k, x, activation="none"):
+    m = x.shape[0]
+    t = ctx.upload_p4(p4, n, k)
+    xd, yd = ctx.to_device(x), ctx.alloc(m * n * 4)
+    ctx.linear(xd, t, yd, m, activation=activation, mode="prefill")
+    y = ctx.to_host(yd, (m, n), np.float32)
+    ctx.release(t)
+    return y
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 136, 288), (19, 136, 288), (64, 264, 512),
+                                   (130, 520, 1056), (256, 1024, 2560)])
+@pytest.mark.parametrize("epi", ["fma", "scalar"])
+def test_gemm_bitwise(ctx, oracle, m, n, k, epi):
+    rng = np.random.default_rng(m * 7 + n + k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[m // 2, 32:64] = 0.0
+    p4 = oracle.pack_q8_0_p4(w)
+    ctx.set_gemm_epilogue(epi)
+    try:
+        y = gemm(ctx, p4, n, k, x)
+    finally:
+        ctx.set_gemm_epilogue("fma")
+    assert bits_equal(y, oracle.linear(x, p4, n, epilogue=epi))
+    other = "scalar" if epi == "fma" else "fma"
+    assert close(y, oracle.linear(x, p4, n, epilogue=other))
+
+
+def test_gemm_exact_operand_boundaries(ctx, oracle):
+    # run_numeric.py:690-732 prefill case: M=19, N=136, K=288, exact operands,
+    # zero last block of row 0, against a float64 matmul at 1e-5 / 1e-6.
+    rng = np.random.default_rng(0)
+    m, n, k = 19, 136, 288
+
+    def exact(rows):
+        v = rng.integers(-63, 64, size=(rows, k // 32, 32)).astype(np.float64)
+        v[:, :, 0] = 127
+        e = rng.integers(-6, -4, size=(rows, k // 32, 1))
+        return np.ldexp(v, e).reshape(rows, k).astype(np.float32)
+
+    x, w = exact(m), exact(n)
+    x[0, -32:] = 0
+    y = gemm(ctx, oracle.pack_q8_0_p4(w), n, k, x)
+    np.testing.assert_allclose(y, x.astype(np.float64) @ w.astype(np.float64).T,
+                               rtol=1e-5, atol=1e-6)
+
+
+def test_gemm_silu(ctx, oracle):
+    rng = np.random.default_rng(3)
+    m, n, k = 33, 264, 1024
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    p4 = oracle.pack_q8_0_p4(w)
+    y = gemm(ctx, p4, n, k, x, activation="silu")
+    assert bits_equal(y, oracle.linear(x, p4, n, activation="silu", epilogue="fma"))
+
+
+@pytest.mark.parametrize("m", [64, 256, 1024])
+def test_gemm_config4_rows(ctx, oracle, m):
+    # Config 4 (K=2560 -> N=9216, M = 64 / 256 / 1024): full GEMM on the GPU,
+    # 24 sampled rows (first, last, random) recomputed by the oracle.
+    n, k = 9216, 2560
+    p4d, _ = ctx.synthesize_p4(seed=40 + m, rows=n, cols=k)
+    t = ctx.register_device_p4(p4d, n, k)
+    p4 = ctx.to_host(p4d, (p4d.nbytes,), np.uint8)
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    xd, yd = ctx.to_device(x), ctx.alloc(m * n * 4)
+    ctx.linear(xd, t, yd, m, mode="prefill")
+    y = ctx.to_host(yd, (m, n), np.float32)
+    rows = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, 22)]))
+    ref = oracle.linear(x[rows], p4, n, epilogue="fma")
+    assert bits_equal(y[rows], ref)
+    ctx.release(t)
+
+
+def test_prefill_swiglu(ctx, oracle):
+    # Prefill MLP hidden for M > 1: silu(gate GEMM) * up GEMM, SDOT epilogue.
+    rng = np.random.default_rng(5)
+    m, n, k = 40, 1056, 512
+    wg = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wu = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    pg, pu = oracle.pack_q8_0_p4(wg), oracle.pack_q8_0_p4(wu)
+    tg, tu = ctx.upload_p4(pg, n, k), ctx.upload_p4(pu, n, k)
+    xd, hd = ctx.to_device(x), ctx.alloc(m * n * 4)
+    ctx.swiglu(xd, tg, tu, hd, m, mode="prefill")
+    h = ctx.to_host(hd, (m, n), np.float32)
+    assert bits_equal(h, oracle.swiglu(x, pg, pu, n, epilogue="fma"))
+    ctx.release(tg)
+    ctx.release(tu)
