@@ -317,6 +317,30 @@ def cpu_baseline(res, budget_s=12.0):
                 colpar_ms_per_step=dt_col * 1e3)
 
 
+def copy_calibration(ctx, nbytes=256 << 20, reps=10):
+    """A plain device copy of known size (HIP's copy kernel), run under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE to scale the counters."""
+    a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    q8lib = __import__("llmcp_amd").lib()
+    for _ in range(reps):
+        q8lib.llmcp_q8_memcpy_d2d(ctx.handle, b.ptr, a.ptr, nbytes)
+    ctx.sync()
+    a.free()
+    b.free()
+    return {"copy_bytes": nbytes, "reps": reps}
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE, WRITE_SIZE, copy-calibrated)."""
+    path = os.path.join(ROOT, "profiles", "gemv_gateup_decode_mlp_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -324,6 +348,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the Q8_0 linear path runs on a single "
@@ -332,6 +358,8 @@ def main():
         sys.exit(2)
     import llmcp_amd as q8
     ctx = q8.Context(0)
+    if args.copy_calibration:
+        copy_calibration(ctx)
     res = bench_decode_mlp(ctx, q8, args.steps, args.warmup)
     extra = {}
     if not args.no_extra:
@@ -371,7 +399,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(res["gu_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": (load_traffic() or {}).get("hbm_bytes_per_launch"),
                      "kernel": "gemv_kernel<NMAT=2,QIN> (fused gate/up SwiGLU, "
                                "timed alone via llmcp_q8_swiglu)",
                      "launch_us": round(res["gu_launch_us"], 3),
