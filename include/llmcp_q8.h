@@ -208,6 +208,15 @@ int llmcp_q8_block_dots(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
  * range since the last check).  Synchronizes the stream. */
 int llmcp_q8_ctx_check(llmcp_q8_ctx *ctx, int32_t *flag);
 
+/* Device self-test of the two floating-point identities the activation
+ * quantizer uses in place of IEEE division (no counterpart in the
+ * reference; it pins the quantizer's exactness on the running GPU):
+ * RN(m/127) by reciprocal-multiply plus one FMA correction for every
+ * non-negative float m, and RN(1/s) by v_rcp_f32 plus one Newton step for
+ * every positive float s.  Writes the number of inputs where either differs
+ * from IEEE division (0 expected).  Synchronous; about 4e9 evaluations. */
+int llmcp_q8_selftest_quantizer(llmcp_q8_ctx *ctx, uint64_t *mismatches);
+
 /* ---------------------------------------------------- offline packing -- */
 
 /* quantizeTensorQ8_0Packed (lib/Model/Quantization.cpp:165-214) on the host:

@@ -68,7 +68,7 @@ EXPORTS = [
     "llmcp_q8_event_destroy", "llmcp_q8_event_record",
     "llmcp_q8_event_elapsed_ms", "llmcp_q8_graph_begin", "llmcp_q8_graph_end",
     "llmcp_q8_graph_launch", "llmcp_q8_graph_destroy",
-    "llmcp_q8_device_bytes",
+    "llmcp_q8_device_bytes", "llmcp_q8_selftest_quantizer",
 ]
 
 
@@ -129,6 +129,7 @@ def lib():
         "llmcp_q8_graph_launch": (I, [P, P]),
         "llmcp_q8_graph_destroy": (I, [P]),
         "llmcp_q8_device_bytes": (U64, [P, P]),
+        "llmcp_q8_selftest_quantizer": (I, [P, ctypes.POINTER(U64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -354,6 +355,12 @@ class Context:
         f = ctypes.c_int32(0)
         check(lib().llmcp_q8_ctx_check(self.handle, ctypes.byref(f)))
         return f.value
+
+    def selftest_quantizer(self):
+        """Mismatches of the quantizer's division identities (0 expected)."""
+        n = ctypes.c_uint64(0)
+        check(lib().llmcp_q8_selftest_quantizer(self.handle, ctypes.byref(n)))
+        return n.value
 
     # ---- timing
     def event(self):

@@ -27,8 +27,13 @@ hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
                            int64_t cols, int8_t *qa, int64_t ldq, float *sa,
                            int64_t lds, int64_t blocks_pad, hipStream_t s);
 
+// Exhaustive device check of the quantizer's division identities; adds the
+// number of mismatching inputs to *bad.
+hipError_t launch_selftest_quantizer(unsigned long long *bad, hipStream_t s);
+
 struct GemvLaunch {
-  const float *x = nullptr;      // f32 input row, quantized in the pass loop
+  const float *x = nullptr;      // f32 input row (16 B aligned), quantized
+                                 // once per workgroup into LDS
   const int8_t *qa = nullptr;    // or: Q8_1 input row, padded to passes*16
   const float *sa = nullptr;     //     blocks (used when x is null)
   const uint8_t *w[2] = {nullptr, nullptr};  // pass-layout weights
@@ -39,13 +44,12 @@ struct GemvLaunch {
   int activation = 0;            // 0 none, 1 silu (nmat == 1 only)
   unsigned long long *keys = nullptr;  // non-null: fused argmax partials,
   int64_t *argmax_out = nullptr;       // gemv_workgroups(rows) entries
-  int8_t *qout = nullptr;        // non-null: also emit Q8_1 of y
-  float *sout = nullptr;         // (rows % 32 == 0, f32 input x required)
 };
 
 // One-matrix GEMVs with at most this many lane groups quantize the input
-// row inside the kernel; wider ones (every wave would re-read the row) take
-// a pre-quantized row.  Two-matrix (SwiGLU) GEMVs always quantize inside.
+// row inside the kernel (once per workgroup); wider ones (every workgroup
+// would re-read the row) take a pre-quantized row.  Two-matrix (SwiGLU)
+// GEMVs always quantize inside.
 constexpr int64_t kInLoopQuantMaxGroups = 4096;
 bool gemv_quantizes_input(int64_t rows, int nmat);
 

@@ -37,12 +37,24 @@ __device__ __forceinline__ float silu(float v) {
   return v * sig;
 }
 
+__device__ __forceinline__ uint32_t word(const uint4 &v, int k) {
+  return k == 0 ? v.x : (k == 1 ? v.y : (k == 2 ? v.z : v.w));
+}
+
 __device__ __forceinline__ int dot8(const uint4 &w, const uint4 &a, int acc) {
   acc = __builtin_amdgcn_sdot4((int)w.x, (int)a.x, acc, false);
   acc = __builtin_amdgcn_sdot4((int)w.y, (int)a.y, acc, false);
   acc = __builtin_amdgcn_sdot4((int)w.z, (int)a.z, acc, false);
   acc = __builtin_amdgcn_sdot4((int)w.w, (int)a.w, acc, false);
   return acc;
+}
+
+// Lane permutation by DPP control word (quad_perm 0x00-0xFF, row ops above).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xf, 0xf, false));
 }
 
 // DPP row_ror:1 -- lane i of each 16-lane row receives lane (i-1) mod 16.
@@ -165,30 +177,78 @@ __global__ void pack_p4_kernel(const float *__restrict__ w, int64_t groups,
 
 // --------------------------------------------- activation quantizer ---- //
 
+// RN(m / 127) for m >= 0: m * RN(1/127) and one FMA correction.  The
+// identity holds for every finite non-negative float (checked exhaustively;
+// the device self-test repeats the check); +inf is passed through.
+__device__ __forceinline__ float div127(float m) {
+  constexpr float c = 1.0f / 127.0f;
+  const float q = m * c;
+  const float r = __builtin_fmaf(-q, 127.0f, m);
+  const float s = __builtin_fmaf(r, c, q);
+  return m == __builtin_inff() ? m : s;
+}
+
+// RN(1 / s).  For s in [2^-125, 2^126] v_rcp_f32 plus one Newton step with
+// FMA is exact (checked exhaustively over that range on gfx950 by the device
+// self-test); outside it -- where 1/s is subnormal or overflows -- the IEEE
+// division sequence runs instead.
+__device__ __forceinline__ float recip(float s) {
+  if (s >= 0x1p-125f && s <= 0x1p126f) {
+    const float y = __builtin_amdgcn_rcpf(s);
+    const float e = __builtin_fmaf(-s, y, 1.0f);
+    return __builtin_fmaf(e, y, y);
+  }
+  return 1.0f / s;
+}
+
 // Quantizes 8 blocks per wave instruction: 8 lanes x float4 per block.
 // Q8Decode.cpp:83-120: sa = max|x|/127; inv = max==0 ? 0 : 1/sa;
 // q = (int8)(int32)roundeven(x*inv).
 __device__ __forceinline__ void quantize_block8(float4 v, bool valid,
-                                                int lane, int32_t *q_out,
-                                                float *s_out) {
+                                                int32_t *q_out, float *s_out) {
   if (!valid) v = make_float4(0.f, 0.f, 0.f, 0.f);
   float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  m = fmaxf(m, __shfl_xor(m, 1));
-  m = fmaxf(m, __shfl_xor(m, 2));
-  m = fmaxf(m, __shfl_xor(m, 4));
-  const float s = m / 127.0f;
-  const float inv = m == 0.0f ? 0.0f : 1.0f / s;
+  // max over the 8 lanes of the block with DPP (no LDS round trips): swap
+  // neighbours, swap pairs, then mirror each half-row (lane i <-> 7 - i).
+  m = fmaxf(m, dpp_f32<0xB1>(m));
+  m = fmaxf(m, dpp_f32<0x4E>(m));
+  m = fmaxf(m, dpp_f32<0x141>(m));
+  const float s = div127(m);
+  const float inv = m == 0.0f ? 0.0f : recip(s);
   const int q0 = (int)rintf(v.x * inv), q1 = (int)rintf(v.y * inv);
   const int q2 = (int)rintf(v.z * inv), q3 = (int)rintf(v.w * inv);
   *q_out = (int32_t)((uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
                      ((uint32_t)(q2 & 0xff) << 16) |
                      ((uint32_t)(q3 & 0xff) << 24));
-  if ((lane & 7) == 0) *s_out = s;
+  *s_out = s;  // the same in all 8 lanes of the block
 }
 
 __device__ __forceinline__ float4 load_float4(const float *p, bool aligned) {
   if (aligned) return *(const float4 *)p;
   return make_float4(p[0], p[1], p[2], p[3]);
+}
+
+// Exhaustive check of div127 and recip against IEEE division over the
+// float bit patterns [lo, hi): one pattern per thread, mismatches counted
+// per wave.
+__global__ void selftest_quant_kernel(uint32_t lo, uint32_t hi,
+                                      unsigned long long *bad) {
+  const uint32_t i = lo + blockIdx.x * blockDim.x + threadIdx.x;
+  bool miss = false;
+  if (i < hi) {
+    const float v = __builtin_bit_cast(float, i);
+    const float d_ref = v / 127.0f;
+    miss = __builtin_bit_cast(uint32_t, div127(v)) !=
+           __builtin_bit_cast(uint32_t, d_ref);
+    if (v > 0.0f) {
+      const float r_ref = 1.0f / v;
+      miss |= __builtin_bit_cast(uint32_t, recip(v)) !=
+              __builtin_bit_cast(uint32_t, r_ref);
+    }
+  }
+  const unsigned long long mask = __ballot(miss);
+  if ((threadIdx.x & 63) == 0 && mask)
+    atomicAdd(bad, (unsigned long long)__popcll(mask));
 }
 
 // Grid: x covers (row, padded block) in units of 8 blocks per wave.
@@ -208,7 +268,7 @@ __global__ void quantize_kernel(const float *__restrict__ x, int64_t m,
     v = load_float4(x + row * ldx + blk * kBlock + (lane & 7) * 4, aligned);
   int32_t q;
   float s;
-  quantize_block8(v, valid, lane, &q, &s);
+  quantize_block8(v, valid, &q, &s);
   if (in_range) {
     *(int32_t *)(qa + row * ldq + blk * kBlock + (lane & 7) * 4) = q;
     if ((lane & 7) == 0) sa[row * lds + blk] = s;
@@ -218,15 +278,13 @@ __global__ void quantize_kernel(const float *__restrict__ x, int64_t m,
 // --------------------------------------------------------------- GEMV -- //
 
 struct GemvArgs {
-  const float *x;    // IN_WAVE / IN_WG: f32 input row, 16 B aligned
+  const float *x;    // IN_WG: f32 input row, 16 B aligned
   const int8_t *qa;  // IN_PRE: Q8_1 input, padded to passes * 16 blocks
   const float *sa;
   const uint8_t *w0;
   const uint8_t *w1;
   float *y;
   unsigned long long *keys;  // ARGMAX: one (value, index) key per workgroup
-  int8_t *qout;              // QOUT: Q8_1 of y, [rows] bytes + [rows/32] scales
-  float *sout;
   int64_t groups;
   int32_t blocks;
   int32_t passes;
@@ -234,9 +292,8 @@ struct GemvArgs {
 
 // Where the GEMV's input row comes from.
 enum InputMode {
-  IN_PRE = 0,   // pre-quantized Q8_1 row in global memory
-  IN_WAVE = 1,  // f32 row, each wave quantizes its blocks in the pass loop
-  IN_WG = 2     // f32 row, each workgroup quantizes it once into LDS
+  IN_PRE = 0,  // pre-quantized Q8_1 row in global memory
+  IN_WG = 1    // f32 row, each workgroup quantizes it once into LDS
 };
 
 // Total order on (logit, index) whose maximum is the first maximum:
@@ -250,76 +307,70 @@ __device__ __forceinline__ unsigned long long argmax_key(float v,
          (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
-__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d,
-                                          float inv) {
-  const int q0 = (int)rintf(a * inv), q1 = (int)rintf(b * inv);
-  const int q2 = (int)rintf(c * inv), q3 = (int)rintf(d * inv);
-  return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-         ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+// Waves per workgroup of an IN_WG GEMV with a compile-time pass count.  The
+// workgroup quantizes the input row once (pc * 16 blocks, 8 lanes per block,
+// row_rounds float4 loads per lane), so wider workgroups share that work.
+__host__ __device__ constexpr int wg_waves(int nmat, int pc) {
+  return nmat == 2 ? 3 : (pc <= 5 ? 2 : 4);
 }
-
-// Q8_1 of one 32-value block spread over the four lanes j, j+16, j+32, j+48
-// (lane 16r + j holds values 8r..8r+7): the same arithmetic as
-// Q8Decode.cpp:83-120, then every lane gathers the block's 8 words.
-__device__ __forceinline__ void quantize_shared_block(const uint4 &b0,
-                                                      const uint4 &b1, int j,
-                                                      uint4 &a0, uint4 &a1,
-                                                      float &s_out) {
-  const float4 v0 = __builtin_bit_cast(float4, b0);
-  const float4 v1 = __builtin_bit_cast(float4, b1);
-  float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)),
-                        fmaxf(fabsf(v0.z), fabsf(v0.w))),
-                  fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)),
-                        fmaxf(fabsf(v1.z), fabsf(v1.w))));
-  m = fmaxf(m, __shfl_xor(m, 16));
-  m = fmaxf(m, __shfl_xor(m, 32));
-  const float s = m / 127.0f;
-  const float inv = m == 0.0f ? 0.0f : 1.0f / s;
-  const uint32_t lo = pack4(v0.x, v0.y, v0.z, v0.w, inv);
-  const uint32_t hi = pack4(v1.x, v1.y, v1.z, v1.w, inv);
-  a0.x = (uint32_t)__shfl((int)lo, j);
-  a0.y = (uint32_t)__shfl((int)hi, j);
-  a0.z = (uint32_t)__shfl((int)lo, j + 16);
-  a0.w = (uint32_t)__shfl((int)hi, j + 16);
-  a1.x = (uint32_t)__shfl((int)lo, j + 32);
-  a1.y = (uint32_t)__shfl((int)hi, j + 32);
-  a1.z = (uint32_t)__shfl((int)lo, j + 48);
-  a1.w = (uint32_t)__shfl((int)hi, j + 48);
-  s_out = s;
+__host__ __device__ constexpr int row_rounds(int pc, int w) {
+  return (2 * pc + w - 1) / w;
+}
+// LDS bytes of the quantized row: int8 values + f32 scales per block slot.
+__host__ __device__ constexpr int row_slots(int pc, int w) {
+  return pc > 0 ? row_rounds(pc, w) * 8 * w : 0;
 }
 
 // One wave per lane group (4 rows); lane L = 16r + j owns row 4g+r and the
-// blocks 16p + j of every pass p.  Each lane streams its weights (and, for
-// IN_PRE / IN_WAVE, its activation block) through a ring of D passes in
-// flight.
-//   IN    where the input row comes from (InputMode).
-//   QOUT  y is also quantized to Q8_1 for the next GEMV.  Needs 8 waves per
-//         workgroup: the workgroup owns one 32-row output block and
-//         quantizes it through LDS.
+// blocks 16p + j of every pass p.  W waves per workgroup.  Each lane streams
+// its weights (and, for IN_PRE, its activation block) through a ring of D
+// passes in flight.
+//   IN    where the input row comes from (InputMode).  IN_WG with PC > 0
+//         issues the row's loads before the weight ring: loads complete in
+//         issue order, so the row is quantized while the ring is in flight.
 //   PC>0  the pass count is a compile-time constant and the pass sequence
 //         is fully unrolled, so every wait on the ring is exact.
-template <int NMAT, int ACT, bool ARGMAX, int IN, bool QOUT, int D, int PC>
-__global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
+// Per pass, prepare() forms the 16 blocks' contributions and chain() adds
+// them in block order; the next pass's prepare() is scheduled together with
+// the current chain(), so the dots overlap the serial DPP additions.
+template <int NMAT, int ACT, bool ARGMAX, int IN, int W, int D, int PC>
+__global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];  // IN_WG input row
-  __shared__ unsigned long long key_l[8];
-  __shared__ float y_l[kBlock];
-  __shared__ unsigned count_l;
-  if (QOUT && threadIdx.x == 0) count_l = 0;
+  __shared__ unsigned long long key_l[W];
   const int passes = PC > 0 ? PC : a.passes;
   const int nblk = passes * kPassBlocks;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int waves = blockDim.x >> 6;
-  const int64_t g = (int64_t)blockIdx.x * waves + wave;
+  const int64_t g = (int64_t)blockIdx.x * W + wave;
   const bool active = g < a.groups;
   const int j = lane & 15;
   const int r = lane >> 4;
+  // IN_WG, compile-time pass count: the row's float4 loads, 8 per block.
+  constexpr bool kRowFirst = IN == IN_WG && PC > 0;
+  constexpr int XR = kRowFirst ? row_rounds(PC, W) : 1;
+  // Block slots in LDS: every task of the unrolled prologue has one (no
+  // store is conditional), the runtime prologue covers the padded row.
+  const int nslot = kRowFirst ? row_slots(PC, W) : nblk;
   int8_t *qa_l = (int8_t *)lds;
-  float *sa_l = (float *)(lds + nblk * kBlock);
+  float *sa_l = (float *)(lds + nslot * kBlock);
 
+  float4 xv[XR];
+  if (kRowFirst) {
+#pragma unroll
+    for (int u = 0; u < XR; ++u) {
+      const int t = u * 64 * W + (int)threadIdx.x;
+      xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if ((t >> 3) < a.blocks) xv[u] = *(const float4 *)(a.x + t * 4);
+    }
+  }
+
+  // Waves past the last group stream the last group again (results unused)
+  // so that the loads below are unconditional: a branch around them would
+  // make the compiler wait for the whole ring at the join.
+  const int64_t gl = active ? g : a.groups - 1;
   const unsigned char *base[NMAT];
-  base[0] = a.w0 + g * passes * kPassBytes;
-  if (NMAT == 2) base[NMAT - 1] = a.w1 + g * passes * kPassBytes;
+  base[0] = a.w0 + gl * passes * kPassBytes;
+  if (NMAT == 2) base[NMAT - 1] = a.w1 + gl * passes * kPassBytes;
 
   uint4 q0[NMAT][D], q1[NMAT][D], x0[D], x1[D];
   uint32_t sc[NMAT][D];
@@ -335,119 +386,163 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
     }
     // Raw loads only: any use of the loaded values here (even a select)
     // would make the wave wait for them and drain the ring.  Padded blocks
-    // (blk >= blocks) are masked in consume().
-    const int blk = pc * kPassBlocks + j;
-    if (IN == IN_WAVE) {
-      const float *xp = a.x + (blk < a.blocks ? blk * kBlock + 8 * r : 0);
-      x0[slot] = *(const uint4 *)xp;
-      x1[slot] = *(const uint4 *)(xp + 4);
-    } else if (IN == IN_PRE) {
+    // (blk >= blocks) are masked in prepare().
+    if (IN == IN_PRE) {
+      const int blk = pc * kPassBlocks + j;
       x0[slot] = *(const uint4 *)(a.qa + blk * kBlock);
       x1[slot] = *(const uint4 *)(a.qa + blk * kBlock + 16);
       xs[slot] = a.sa[blk];
     }
   };
 
-  float acc[NMAT];
+  // sched_barrier(0) pins the ring right after the row loads; without it
+  // the scheduler sinks the loads toward their uses and only about one pass
+  // stays in flight.
 #pragma unroll
-  for (int mm = 0; mm < NMAT; ++mm) acc[mm] = 0.0f;
-
-  // Pass p in ring slot d: exact block dots, scale, then the serial chain
-  // over the pass's 16 blocks in block order -- after step t, lane t of each
-  // row holds the running sum through block 16p + t; lane 15 carries it
-  // into the next pass.
-  auto consume = [&](int d, int p) {
-    uint4 a0, a1;
-    float s_a;
-    const int blk = p * kPassBlocks + j;
-    const bool valid = blk < a.blocks;  // padded blocks: zero input
-    if (IN == IN_WAVE) {
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      quantize_shared_block(valid ? x0[d] : z, valid ? x1[d] : z, j, a0, a1,
-                            s_a);
-    } else if (IN == IN_PRE) {
-      a0 = x0[d];
-      a1 = x1[d];
-      s_a = valid ? xs[d] : 0.0f;
-    } else {
-      a0 = *(const uint4 *)(qa_l + blk * kBlock);
-      a1 = *(const uint4 *)(qa_l + blk * kBlock + 16);
-      s_a = sa_l[blk];
-    }
-    float contrib[NMAT];
-#pragma unroll
-    for (int mm = 0; mm < NMAT; ++mm) {
-      int dot = dot8(q0[mm][d], a0, 0);
-      dot = dot8(q1[mm][d], a1, dot);
-      const float factor = s_a * half_bits_to_float(sc[mm][d]);
-      contrib[mm] = (float)dot * factor;
-    }
-#pragma unroll
-    for (int t = 0; t < kPassBlocks; ++t) {
-#pragma unroll
-      for (int mm = 0; mm < NMAT; ++mm)
-        acc[mm] = row_rotate1(acc[mm]) + contrib[mm];
-    }
-  };
-
-  // sched_barrier(0) pins each refill right after the pass that frees its
-  // slot; without it the scheduler sinks the loads toward their uses and
-  // only about one pass stays in flight.
-  if (active) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) issue(d, d);
-  }
+  for (int d = 0; d < D; ++d) issue(d, d);
   __builtin_amdgcn_sched_barrier(0);
 
   if (IN == IN_WG) {
-    // Quantize the whole input row into LDS once per workgroup, 8 lanes per
-    // block, four blocks' loads in flight per lane (the weight ring above
-    // is already on its way).
-    constexpr int U = 4;
-    const int tasks = nblk * 8;
-    for (int t0 = 0; t0 < tasks; t0 += (int)blockDim.x * U) {
-      float4 v[U];
+    // Quantize the input row into LDS once per workgroup, 8 lanes per block
+    // (blocks past `blocks` become zero).
+    if (kRowFirst) {
+      // One basic block (no conditional store), so the rounds interleave.
+      // Blocks past `blocks` were loaded as zeros.
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int t = t0 + u * (int)blockDim.x + (int)threadIdx.x;
-        const int blk = t >> 3;
-        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (blk < a.blocks) v[u] = *(const float4 *)(a.x + blk * kBlock + (t & 7) * 4);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int t = t0 + u * (int)blockDim.x + (int)threadIdx.x;
-        const int blk = t >> 3;
+      for (int u = 0; u < XR; ++u) {
+        const int t = u * 64 * W + (int)threadIdx.x;
         int32_t q;
-        float sq = 0.0f;
-        quantize_block8(v[u], blk < a.blocks, lane, &q, &sq);
-        if (blk < nblk) {
-          ((int32_t *)qa_l)[t] = q;
-          if ((t & 7) == 0) sa_l[blk] = sq;
+        float sq;
+        quantize_block8(xv[u], true, &q, &sq);
+        ((int32_t *)qa_l)[t] = q;
+        sa_l[t >> 3] = sq;
+      }
+    } else {
+      constexpr int U = 4;
+      const int tasks = nblk * 8;
+      for (int t0 = 0; t0 < tasks; t0 += 64 * W * U) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int t = t0 + u * 64 * W + (int)threadIdx.x;
+          v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if ((t >> 3) < a.blocks) v[u] = *(const float4 *)(a.x + t * 4);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int t = t0 + u * 64 * W + (int)threadIdx.x;
+          const int blk = t >> 3;
+          int32_t q;
+          float sq;
+          quantize_block8(v[u], blk < a.blocks, &q, &sq);
+          if (blk < nblk) {
+            ((int32_t *)qa_l)[t] = q;
+            if ((t & 7) == 0) sa_l[blk] = sq;
+          }
         }
       }
     }
     __syncthreads();
   }
 
+  float acc[NMAT];
+#pragma unroll
+  for (int mm = 0; mm < NMAT; ++mm) acc[mm] = 0.0f;
+
+  // Contributions of pass p (ring slot d): exact block dots (two
+  // independent dot4 chains; integer sums are order-free), then
+  // f32(I) * (sa * dw).  Split in three parts so that the next pass's
+  // preparation can ride in the current pass's chain (see chain_with).
+  struct Next {
+    uint4 a0, a1;
+    float s_a;
+    int d0[NMAT], d1[NMAT];
+  };
+  auto load_act = [&](int d, int p, Next &n) {
+    const int blk = p * kPassBlocks + j;
+    if (IN == IN_PRE) {
+      n.a0 = x0[d];
+      n.a1 = x1[d];
+      n.s_a = blk < a.blocks ? xs[d] : 0.0f;  // padded blocks: zero input
+    } else {
+      n.a0 = *(const uint4 *)(qa_l + blk * kBlock);
+      n.a1 = *(const uint4 *)(qa_l + blk * kBlock + 16);
+      n.s_a = sa_l[blk];
+    }
+#pragma unroll
+    for (int mm = 0; mm < NMAT; ++mm) n.d0[mm] = n.d1[mm] = 0;
+  };
+  auto dot_part = [&](int d, int k, Next &n) {
+#pragma unroll
+    for (int mm = 0; mm < NMAT; ++mm) {
+      n.d0[mm] = __builtin_amdgcn_sdot4((int)word(q0[mm][d], k),
+                                        (int)word(n.a0, k), n.d0[mm], false);
+      n.d1[mm] = __builtin_amdgcn_sdot4((int)word(q1[mm][d], k),
+                                        (int)word(n.a1, k), n.d1[mm], false);
+    }
+  };
+  auto finish = [&](int d, Next &n, float (&c)[NMAT]) {
+#pragma unroll
+    for (int mm = 0; mm < NMAT; ++mm) {
+      const int dot = n.d0[mm] + n.d1[mm];
+      const float factor = n.s_a * half_bits_to_float(sc[mm][d]);
+      c[mm] = (float)dot * factor;
+    }
+  };
+  auto prepare = [&](int d, int p, float (&c)[NMAT]) {
+    Next n;
+    load_act(d, p, n);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dot_part(d, k, n);
+    finish(d, n, c);
+  };
+  // The serial chain over one pass's 16 blocks in block order: after step
+  // t, lane t of each row holds the running sum through block 16p + t;
+  // lane 15 carries it into the next pass.  The next pass's activation
+  // reads go out at step 0, its dots fill steps 4-7 and its scaling step
+  // 10, each pinned between DPP additions (whose dependent latency they
+  // hide) by sched_barrier.  The dots wait for the next pass's weights
+  // inside this chain, which costs nothing once the ring has landed.
+  auto chain_with = [&](const float (&c)[NMAT], bool has_next, int dn, int pn,
+                        float (&cn)[NMAT]) {
+    Next n;
+    if (has_next) load_act(dn, pn, n);
+#pragma unroll
+    for (int t = 0; t < kPassBlocks; ++t) {
+#pragma unroll
+      for (int mm = 0; mm < NMAT; ++mm)
+        acc[mm] = row_rotate1(acc[mm]) + c[mm];
+      if (has_next) {
+        if (t >= 4 && t < 8) dot_part(dn, t - 4, n);
+        if (t == 10) finish(dn, n, cn);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
   if (active) {
+    float cur[NMAT], nxt[NMAT];
+    prepare(0, 0, cur);
     if constexpr (PC > 0) {
 #pragma unroll
       for (int p = 0; p < PC; ++p) {
-        consume(p % D, p);
+        if (p + D < PC) issue(p % D, p + D);  // slot of pass p is free
         __builtin_amdgcn_sched_barrier(0);
-        if (p + D < PC) issue(p % D, p + D);
-        __builtin_amdgcn_sched_barrier(0);
+        chain_with(cur, p + 1 < PC, (p + 1) % D, p + 1, nxt);
+#pragma unroll
+        for (int mm = 0; mm < NMAT; ++mm) cur[mm] = nxt[mm];
       }
     } else {
       for (int p0 = 0; p0 < passes; p0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-          if (p0 + d < passes) {
-            consume(d, p0 + d);
+          const int p = p0 + d;
+          if (p < passes) {
+            issue(d, p + D);
             __builtin_amdgcn_sched_barrier(0);
-            issue(d, p0 + d + D);
-            __builtin_amdgcn_sched_barrier(0);
+            chain_with(cur, p + 1 < passes, (d + 1) % D, p + 1, nxt);
+#pragma unroll
+            for (int mm = 0; mm < NMAT; ++mm) cur[mm] = nxt[mm];
           }
         }
       }
@@ -463,29 +558,6 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
   const bool owner = active && j == 15;
   if (owner) a.y[row] = y;
 
-  if (QOUT) {
-    // The workgroup's 8 waves produced output rows 32*blockIdx.x .. +31.
-    // The last wave to finish (LDS arrival count, no barrier, so finished
-    // waves leave at once) quantizes that block (Q8Decode.cpp:83-120).
-    if (owner) y_l[wave * kLanes + r] = y;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    unsigned arrived = 0;
-    if (lane == 0) arrived = atomicAdd(&count_l, 1u);
-    arrived = (unsigned)__shfl((int)arrived, 0);
-    if (arrived == (unsigned)waves - 1) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      const float v = lane < kBlock ? y_l[lane] : 0.0f;
-      float m = fabsf(v);
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-      const float sq = m / 127.0f;
-      const float inv = m == 0.0f ? 0.0f : 1.0f / sq;
-      if (lane < kBlock)
-        a.qout[(int64_t)blockIdx.x * kBlock + lane] = (int8_t)(int)rintf(v * inv);
-      if (lane == 0) a.sout[blockIdx.x] = sq;
-    }
-  }
-
   if (ARGMAX) {
     unsigned long long key = owner ? argmax_key(y, row) : 0ull;
 #pragma unroll
@@ -493,12 +565,17 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
       const unsigned long long other = __shfl_xor(key, off);
       key = other > key ? other : key;
     }
-    if (lane == 0) key_l[wave] = key;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned long long best = key_l[0];
-      for (int w = 1; w < waves; ++w) best = key_l[w] > best ? key_l[w] : best;
-      a.keys[blockIdx.x] = best;
+    if (W == 1) {
+      if (lane == 0) a.keys[blockIdx.x] = key;
+    } else {
+      if (lane == 0) key_l[wave] = key;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        unsigned long long best = key_l[0];
+#pragma unroll
+        for (int w = 1; w < W; ++w) best = key_l[w] > best ? key_l[w] : best;
+        a.keys[blockIdx.x] = best;
+      }
     }
   }
 }
@@ -606,31 +683,65 @@ inline unsigned grid_for(int64_t threads, int block) {
   return (unsigned)((threads + block - 1) / block);
 }
 
-template <int NMAT, int ACT, bool ARGMAX, int IN, bool QOUT, int PC>
-hipError_t launch_gemv_p(const GemvArgs &args, int waves, hipStream_t s) {
-  constexpr int DMAX = NMAT == 2 ? 4 : 12;
-  constexpr int D = PC > 0 ? (PC < DMAX ? PC : DMAX) : (NMAT == 2 ? 4 : 8);
-  const unsigned grid = (unsigned)((args.groups + waves - 1) / waves);
-  const size_t lds = IN == IN_WG ? (size_t)args.passes * kPassBlocks * (kBlock + 4) : 0;
-  hipLaunchKernelGGL((gemv_kernel<NMAT, ACT, ARGMAX, IN, QOUT, D, PC>),
-                     dim3(grid), dim3(64 * waves), lds, s, args);
+// Ring depth: every pass in flight where the registers allow (two matrices:
+// 5 passes = 90 VGPRs; one matrix from LDS: 18 passes = 162 VGPRs; one
+// matrix with a pre-quantized row: 12 passes of weights + input).
+template <int NMAT, int IN, int PC>
+constexpr int ring_depth() {
+  constexpr int dmax = NMAT == 2 ? 5 : (IN == IN_WG ? 18 : 12);
+  return PC > 0 ? (PC < dmax ? PC : dmax) : (NMAT == 2 ? 4 : 8);
+}
+
+template <int NMAT, int ACT, bool ARGMAX, int IN, int W, int PC>
+hipError_t launch_gemv_p(const GemvArgs &args, hipStream_t s) {
+  constexpr int D = ring_depth<NMAT, IN, PC>();
+  const unsigned grid = (unsigned)((args.groups + W - 1) / W);
+  const size_t slots = PC > 0 ? row_slots(PC, W) : (size_t)args.passes * kPassBlocks;
+  const size_t lds = IN == IN_WG ? slots * (kBlock + 4) : 0;
+  hipLaunchKernelGGL((gemv_kernel<NMAT, ACT, ARGMAX, IN, W, D, PC>),
+                     dim3(grid), dim3(64 * W), lds, s, args);
   return hipGetLastError();
+}
+
+// IN_WG takes its workgroup width from the pass count (wg_waves); IN_PRE
+// runs one wave per workgroup, or four for very wide outputs.
+template <int NMAT, int ACT, bool ARGMAX, int IN, int PC>
+hipError_t launch_gemv_w(const GemvArgs &args, int waves, hipStream_t s) {
+  if constexpr (IN == IN_WG) {
+    return launch_gemv_p<NMAT, ACT, ARGMAX, IN, wg_waves(NMAT, PC), PC>(args, s);
+  } else {
+    if (waves == 4) return launch_gemv_p<NMAT, ACT, ARGMAX, IN, 4, PC>(args, s);
+    return launch_gemv_p<NMAT, ACT, ARGMAX, IN, 1, PC>(args, s);
+  }
 }
 
 // Pass counts with a fully unrolled kernel: K = 512, 1024, 1536, 2560
 // (hidden size), 4096 and 9216 (the MLP down projection).  Others take the
 // runtime loop.
-template <int NMAT, int ACT, bool ARGMAX, int IN, bool QOUT>
+template <int NMAT, int ACT, bool ARGMAX, int IN>
 hipError_t launch_gemv_t(const GemvArgs &args, int waves, hipStream_t s) {
   switch (args.passes) {
-    case 1: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 1>(args, waves, s);
-    case 2: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 2>(args, waves, s);
-    case 3: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 3>(args, waves, s);
-    case 5: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 5>(args, waves, s);
-    case 8: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 8>(args, waves, s);
-    case 18: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 18>(args, waves, s);
-    default: return launch_gemv_p<NMAT, ACT, ARGMAX, IN, QOUT, 0>(args, waves, s);
+    case 1: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 1>(args, waves, s);
+    case 2: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 2>(args, waves, s);
+    case 3: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 3>(args, waves, s);
+    case 5: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 5>(args, waves, s);
+    case 8: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 8>(args, waves, s);
+    case 18: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 18>(args, waves, s);
+    default: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 0>(args, waves, s);
   }
+}
+
+// Workgroup width of a launch (as launch_gemv_w picks it).
+static int gemv_waves(int64_t groups, int64_t passes, int in, int nmat) {
+  if (in == IN_WG) {
+    switch (passes) {
+      case 1: case 2: case 3: case 5: case 8: case 18:
+        return wg_waves(nmat, (int)passes);
+      default:
+        return wg_waves(nmat, 0);
+    }
+  }
+  return groups >= 8192 ? 4 : 1;
 }
 
 }  // namespace
@@ -661,6 +772,15 @@ hipError_t launch_pack_p4(const float *w, int64_t rows, int64_t cols,
   return hipGetLastError();
 }
 
+hipError_t launch_selftest_quantizer(unsigned long long *bad, hipStream_t s) {
+  // every non-negative float up to +inf: 0x00000000 .. 0x7f800000
+  const uint32_t lo = 0, hi = 0x7f800001u;
+  hipLaunchKernelGGL(selftest_quant_kernel,
+                     dim3(grid_for((int64_t)(hi - lo), 256)), dim3(256), 0, s,
+                     lo, hi, bad);
+  return hipGetLastError();
+}
+
 hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
                            int64_t cols, int8_t *qa, int64_t ldq, float *sa,
                            int64_t lds, int64_t blocks_pad, hipStream_t s) {
@@ -674,45 +794,21 @@ hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
   return hipGetLastError();
 }
 
-// Launch shape of a one-row GEMV over `rows` outputs.
-//   fused MLP gate/up (quantized output)   8 waves, input quantized per WG
-//   wide SwiGLU (>= 2048 groups)           8 waves, input quantized per WG
-//   <= kInLoopQuantMaxGroups groups        1 wave,  input quantized per wave
-//   wider (lm_head)                        4 waves, pre-quantized input
-struct GemvShape {
-  int waves;
-  int in;
-};
-
-static GemvShape gemv_shape(int64_t rows, int nmat, bool qout, bool have_x) {
-  const int64_t groups = rows / kLanes;
-  if (have_x && (qout || (nmat == 2 && groups >= 2048))) return {8, IN_WG};
-  if (have_x) return {1, IN_WAVE};
-  return {groups >= 8192 ? 4 : 1, IN_PRE};
-}
-
 bool gemv_quantizes_input(int64_t rows, int nmat) {
   return nmat == 2 || rows / kLanes <= kInLoopQuantMaxGroups;
 }
 
 int64_t gemv_workgroups(int64_t rows) {
-  // Argmax partials are only used by one-matrix GEMVs without QOUT.
-  const int64_t groups = rows / kLanes;
-  const int w = gemv_quantizes_input(rows, 1) ? 1 : (groups >= 8192 ? 4 : 1);
-  return (groups + w - 1) / w;
+  return rows / kLanes;  // one wave per workgroup is the widest grid
 }
 
 template <int IN>
 static hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
                                  int waves, hipStream_t s) {
-  if (l.nmat == 2) {
-    if (IN == IN_WG && l.qout) return launch_gemv_t<2, 0, false, IN, true>(a, waves, s);
-    return launch_gemv_t<2, 0, false, IN, false>(a, waves, s);
-  }
-  if (IN == IN_WG) return hipErrorInvalidValue;  // one-matrix GEMVs use WAVE/PRE
-  if (l.keys) return launch_gemv_t<1, 0, true, IN, false>(a, waves, s);
-  if (l.activation == 1) return launch_gemv_t<1, 1, false, IN, false>(a, waves, s);
-  return launch_gemv_t<1, 0, false, IN, false>(a, waves, s);
+  if (l.nmat == 2) return launch_gemv_t<2, 0, false, IN>(a, waves, s);
+  if (l.keys) return launch_gemv_t<1, 0, true, IN>(a, waves, s);
+  if (l.activation == 1) return launch_gemv_t<1, 1, false, IN>(a, waves, s);
+  return launch_gemv_t<1, 0, false, IN>(a, waves, s);
 }
 
 hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
@@ -724,24 +820,18 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
   a.w1 = l.w[1] ? l.w[1] : l.w[0];
   a.y = l.y;
   a.keys = l.keys;
-  a.qout = l.qout;
-  a.sout = l.sout;
   a.groups = l.rows / kLanes;
   a.blocks = (int32_t)(l.cols / kBlock);
   a.passes = (int32_t)passes_for(l.cols);
-  const GemvShape sh = gemv_shape(l.rows, l.nmat, l.qout != nullptr, l.x != nullptr);
-  if (l.qout && (sh.in != IN_WG || l.rows % kBlock)) return hipErrorInvalidValue;
-  hipError_t e;
-  if (sh.in == IN_WG)
-    e = launch_gemv_in<IN_WG>(a, l, sh.waves, s);
-  else if (sh.in == IN_WAVE)
-    e = launch_gemv_in<IN_WAVE>(a, l, sh.waves, s);
-  else
-    e = launch_gemv_in<IN_PRE>(a, l, sh.waves, s);
+  const int in = l.x ? IN_WG : IN_PRE;
+  if (l.x && (uintptr_t)l.x % 16) return hipErrorInvalidValue;
+  const int waves = gemv_waves(a.groups, a.passes, in, l.nmat);
+  hipError_t e = in == IN_WG ? launch_gemv_in<IN_WG>(a, l, waves, s)
+                             : launch_gemv_in<IN_PRE>(a, l, waves, s);
   if (e != hipSuccess || !l.keys) return e;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(1024), 0, s,
                      (const unsigned long long *)l.keys,
-                     (a.groups + sh.waves - 1) / sh.waves, l.argmax_out);
+                     (a.groups + waves - 1) / waves, l.argmax_out);
   return hipGetLastError();
 }
 

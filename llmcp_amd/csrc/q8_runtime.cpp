@@ -78,15 +78,10 @@ struct llmcp_q8_ctx {
   uint64_t qa_bytes = 0;
   uint64_t sa_bytes = 0;
   uint64_t keys_bytes = 0;
-  // Fused MLP: Q8_1 of the SwiGLU output for the down projection and an f32
-  // spill of h.
-  int8_t *hq = nullptr;
-  float *hs = nullptr;
+  // Fused MLP: the SwiGLU output h when the caller passes no buffer for it.
   float *hf = nullptr;
   float *up = nullptr;  // prefill SwiGLU: the up projection
   uint64_t up_bytes = 0;
-  uint64_t hq_bytes = 0;
-  uint64_t hs_bytes = 0;
   uint64_t hf_bytes = 0;
   hipGraph_t capture = nullptr;
   bool gemm_fma = true;  // prefill GEMM epilogue variant
@@ -155,17 +150,13 @@ int ensure_scratch(llmcp_q8_ctx *ctx, uint64_t qa_bytes, uint64_t sa_bytes,
 }
 
 // Workspace a one-row call against a [rows, cols] weight needs, including
-// the quantized-output buffers should its output feed another GEMV.
+// the f32 buffer for h should its output feed the fused MLP's down GEMV.
 int ensure_decode_scratch(llmcp_q8_ctx *ctx, int64_t rows, int64_t cols) {
   const uint64_t nblk = (uint64_t)passes_for(cols) * kPassBlocks;
   int rc = ensure_scratch(ctx, nblk * kBlock, nblk * 4,
                           (uint64_t)gemv_workgroups(rows) * 8u);
   if (rc || rows % kBlock) return rc;
-  const uint64_t oblk = (uint64_t)passes_for(rows) * kPassBlocks;
-  rc = grow(ctx, ctx->hq, ctx->hq_bytes, oblk * kBlock, "output quant scratch");
-  if (!rc) rc = grow(ctx, ctx->hs, ctx->hs_bytes, oblk * 4, "output scales");
-  if (!rc) rc = grow(ctx, ctx->hf, ctx->hf_bytes, (uint64_t)rows * 4, "mlp hidden");
-  return rc;
+  return grow(ctx, ctx->hf, ctx->hf_bytes, (uint64_t)rows * 4, "mlp hidden");
 }
 
 // Repacks device p4 bytes into a new registry entry under `key`.
@@ -317,8 +308,6 @@ int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx) {
   if (ctx->qa) (void)hipFree(ctx->qa);
   if (ctx->sa) (void)hipFree(ctx->sa);
   if (ctx->keys) (void)hipFree(ctx->keys);
-  if (ctx->hq) (void)hipFree(ctx->hq);
-  if (ctx->hs) (void)hipFree(ctx->hs);
   if (ctx->hf) (void)hipFree(ctx->hf);
   if (ctx->up) (void)hipFree(ctx->up);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -363,6 +352,26 @@ int llmcp_q8_ctx_check(llmcp_q8_ctx *ctx, int32_t *flag) {
                          hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipMemsetAsync(ctx->err_flag, 0, sizeof(int32_t), ctx->stream));
   HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_selftest_quantizer(llmcp_q8_ctx *ctx, uint64_t *mismatches) {
+  if (!ctx || !mismatches) return fail(LLMCP_Q8_EINVAL, "null argument");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  unsigned long long *bad = nullptr;
+  if (hipMalloc(&bad, sizeof(*bad)) != hipSuccess)
+    return fail(LLMCP_Q8_ENOMEM, "self-test counter");
+  unsigned long long host = 0;
+  hipError_t e = hipMemsetAsync(bad, 0, sizeof(*bad), ctx->stream);
+  if (e == hipSuccess) e = launch_selftest_quantizer(bad, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(&host, bad, sizeof(host), hipMemcpyDeviceToHost,
+                       ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(bad);
+  if (e != hipSuccess) return hip_fail(e, "quantizer self-test");
+  *mismatches = host;
   return LLMCP_Q8_OK;
 }
 
@@ -566,14 +575,12 @@ int llmcp_q8_upload_arena(llmcp_q8_ctx *ctx, const void *file,
 // the input inside the GEMV; wide ones (lm_head) quantize it once first.
 static int gemv_common(llmcp_q8_ctx *ctx, const float *x, const Tensor *w0,
                        const Tensor *w1, float *y, int activation,
-                       int64_t *argmax_dev, bool quantize_out) {
+                       int64_t *argmax_dev) {
   int rc = ensure_decode_scratch(ctx, w0->rows, w0->cols);
   if (rc) return rc;
   GemvLaunch l;
   const bool in_loop = gemv_quantizes_input(w0->rows, w1 ? 2 : 1) &&
                        (uintptr_t)x % 16 == 0;
-  if (quantize_out && !in_loop)
-    return fail(LLMCP_Q8_DECLINED, "fused MLP needs a 16-byte aligned input");
   if (in_loop) {
     l.x = x;
   } else {
@@ -595,10 +602,6 @@ static int gemv_common(llmcp_q8_ctx *ctx, const float *x, const Tensor *w0,
   if (argmax_dev) {
     l.keys = ctx->keys;
     l.argmax_out = argmax_dev;
-  }
-  if (quantize_out) {
-    l.qout = ctx->hq;
-    l.sout = ctx->hs;
   }
   hipError_t e = launch_gemv(l, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "gemv launch");
@@ -673,15 +676,13 @@ int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
       return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
                   (long long)m);
     return gemv_common(ctx, input->data + input->offset, w, nullptr,
-                       output->data + output->offset, activation, nullptr,
-                       false);
+                       output->data + output->offset, activation, nullptr);
   }
   if (execution_mode != LLMCP_Q8_PREFILL)
     return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
   if (m == 1)  // one row: the GEMV (scalar epilogue) beats a 1/128-full tile
     return gemv_common(ctx, input->data + input->offset, w, nullptr,
-                       output->data + output->offset, activation, nullptr,
-                       false);
+                       output->data + output->offset, activation, nullptr);
   return gemm_common(ctx, input, w, output, activation);
 }
 
@@ -723,8 +724,7 @@ int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
     return LLMCP_Q8_OK;
   }
   return gemv_common(ctx, input->data + input->offset, wg, wu,
-                     output->data + output->offset, LLMCP_Q8_ACT_NONE, nullptr,
-                     false);
+                     output->data + output->offset, LLMCP_Q8_ACT_NONE, nullptr);
 }
 
 int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
@@ -745,7 +745,7 @@ int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
     return fail(LLMCP_Q8_DECLINED, "lm_head for M > 1 not available");
   return gemv_common(ctx, hidden->data + hidden->offset, w, nullptr,
                      logits->data + logits->offset, LLMCP_Q8_ACT_NONE,
-                     argmax_dev, false);
+                     argmax_dev);
 }
 
 int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
@@ -777,32 +777,14 @@ int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
   if (m != 1) return fail(LLMCP_Q8_DECLINED, "fused MLP needs M == 1");
   if ((rc = set_device(ctx))) return rc;
   if ((rc = ensure_decode_scratch(ctx, wg->rows, wg->cols))) return rc;
+  // Gate/up with the SwiGLU epilogue into h (f32), then the down GEMV,
+  // which quantizes h per workgroup (Q8Decode.cpp:83-120) as its input.
   float *h = hidden ? hidden->data + hidden->offset : ctx->hf;
-  static const int down_in_loop = [] {
-    const char *v = std::getenv("LLMCP_Q8_MLP_DOWN_IN");
-    return v && std::strcmp(v, "wave") == 0 ? 1 : 0;
-  }();
-  if (down_in_loop) {
-    rc = gemv_common(ctx, input->data + input->offset, wg, wu, h,
-                     LLMCP_Q8_ACT_NONE, nullptr, false);
-    if (!rc)
-      rc = gemv_common(ctx, h, wd, nullptr, output->data + output->offset,
-                       LLMCP_Q8_ACT_NONE, nullptr, false);
-    return rc;
-  }
   rc = gemv_common(ctx, input->data + input->offset, wg, wu, h,
-                   LLMCP_Q8_ACT_NONE, nullptr, true);
+                   LLMCP_Q8_ACT_NONE, nullptr);
   if (rc) return rc;
-  GemvLaunch l;
-  l.qa = ctx->hq;
-  l.sa = ctx->hs;
-  l.w[0] = wd->dev;
-  l.y = output->data + output->offset;
-  l.rows = wd->rows;
-  l.cols = wd->cols;
-  hipError_t e = launch_gemv(l, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "down gemv launch");
-  return LLMCP_Q8_OK;
+  return gemv_common(ctx, h, wd, nullptr, output->data + output->offset,
+                     LLMCP_Q8_ACT_NONE, nullptr);
 }
 
 int llmcp_q8_embedding(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,

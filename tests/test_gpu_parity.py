@@ -288,11 +288,23 @@ def test_quantize_activations_bitwise(ctx, oracle):
     x[3, 0] = 127.0
     x[3, 1:8] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 126.5]
     x[3, 8:32] = 0.0
+    # scales far from 1: subnormal scale (the reciprocal's IEEE branch),
+    # subnormal inputs, and very large magnitudes (the fast branch)
+    x[4, 0:32] *= np.float32(1e-36)
+    x[4, 32:64] *= np.float32(1e-41)
+    x[4, 33] = np.float32(-1e-36)  # keeps 1/scale finite
+    x[5, 64:96] *= np.float32(1e37)
     xd, qd, sd = ctx.to_device(x), ctx.alloc(m * k), ctx.alloc(m * k // 32 * 4)
     ctx.quantize(xd, m, k, qd, sd)
     qa, sa = oracle.quantize_act_q8_1(x)
     assert np.array_equal(ctx.to_host(qd, (m, k), np.int8), qa)
     assert bits_equal(ctx.to_host(sd, (m, k // 32), np.float32), sa)
+
+
+def test_quantizer_division_identities(ctx):
+    """The quantizer replaces IEEE division by m*RN(1/127)+FMA correction and
+    v_rcp_f32+Newton; the device checks both over every float input."""
+    assert ctx.selftest_quantizer() == 0
 
 
 def test_block_dots_exact(ctx, oracle):
