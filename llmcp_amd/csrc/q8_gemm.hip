@@ -71,6 +71,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int stages = passes * (kPassBlocks / SB);
+  const int seg = seg_for(passes);  // weight unit layout (q8_common.h)
 
   // ---- global -> registers for one stage
   constexpr int AU = BM * 8 / NT;           // 16 B pieces of A per thread
@@ -98,10 +99,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
       rb[u] = make_uint4(0, 0, 0, 0);
       if (n < n_rows) {
         const int b = kb + (q >> 1);
+        int64_t unit;
+        int slot;
+        locate_seg(b, seg, unit, slot);
         const uint8_t *pass =
-            w + ((n >> 2) * passes + b / kPassBlocks) * (int64_t)kPassBytes;
+            w + ((n >> 2) * passes + unit) * (int64_t)kPassBytes;
         rb[u] = *(const uint4 *)(pass + (q & 1) * 1024 + (n & 3) * 256 +
-                                 (b % kPassBlocks) * 16);
+                                 slot * 16);
       }
     }
 #pragma unroll
@@ -119,10 +123,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
       rdw[u] = 0;
       if (idx < SB * BN && n < n_rows) {
         const int b = kb + bb;
+        int64_t unit;
+        int slot;
+        locate_seg(b, seg, unit, slot);
         const uint8_t *pass =
-            w + ((n >> 2) * passes + b / kPassBlocks) * (int64_t)kPassBytes;
-        rdw[u] = *(const uint16_t *)(pass + kPassQs +
-                                     2 * (16 * (n & 3) + b % kPassBlocks));
+            w + ((n >> 2) * passes + unit) * (int64_t)kPassBytes;
+        rdw[u] = *(const uint16_t *)(pass + kPassQs + 2 * (16 * (n & 3) + slot));
       }
     }
   };

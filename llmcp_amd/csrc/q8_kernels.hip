@@ -86,8 +86,10 @@ __global__ void repack_kernel(const uint8_t *__restrict__ p4,
     for (int c = 0; c < 8; ++c)
       w[c] = *(const uint32_t *)(rec + 8 + 16 * c + 4 * r);
   }
-  uint8_t *pass = out + (g * passes + b / kPassBlocks) * kPassBytes;
-  const int j = (int)(b % kPassBlocks);
+  int64_t u;
+  int j;
+  locate_seg(b, seg_for(passes), u, j);
+  uint8_t *pass = out + (g * passes + u) * kPassBytes;
   *(uint4 *)(pass + r * 256 + j * 16) = make_uint4(w[0], w[1], w[2], w[3]);
   *(uint4 *)(pass + 1024 + r * 256 + j * 16) =
       make_uint4(w[4], w[5], w[6], w[7]);
@@ -345,6 +347,13 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   const bool active = g < a.groups;
   const int j = lane & 15;
   const int r = lane >> 4;
+  // Units (PC or a.passes) of 16 blocks; S of them form one chain pass
+  // (seg_for: lane slot j holds S consecutive blocks of the pass).
+  constexpr int S = PC > 0 ? seg_for(PC) : 1;
+  // Block held by this lane's slot in unit u.
+  auto block_of = [&](int u) {
+    return (u / S) * (kPassBlocks * S) + S * j + (u % S);
+  };
   // IN_WG, compile-time pass count: the row's float4 loads, 8 per block.
   constexpr bool kRowFirst = IN == IN_WG && PC > 0;
   constexpr int XR = kRowFirst ? row_rounds(PC, W) : 1;
@@ -388,7 +397,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     // would make the wave wait for them and drain the ring.  Padded blocks
     // (blk >= blocks) are masked in prepare().
     if (IN == IN_PRE) {
-      const int blk = pc * kPassBlocks + j;
+      const int blk = block_of(pc);
       x0[slot] = *(const uint4 *)(a.qa + blk * kBlock);
       x1[slot] = *(const uint4 *)(a.qa + blk * kBlock + 16);
       xs[slot] = a.sa[blk];
@@ -449,7 +458,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
 #pragma unroll
   for (int mm = 0; mm < NMAT; ++mm) acc[mm] = 0.0f;
 
-  // Contributions of pass p (ring slot d): exact block dots (two
+  // Contributions of unit u (ring slot d): exact block dots (two
   // independent dot4 chains; integer sums are order-free), then
   // f32(I) * (sa * dw).  Split in three parts so that the next pass's
   // preparation can ride in the current pass's chain (see chain_with).
@@ -458,8 +467,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     float s_a;
     int d0[NMAT], d1[NMAT];
   };
-  auto load_act = [&](int d, int p, Next &n) {
-    const int blk = p * kPassBlocks + j;
+  auto load_act = [&](int d, int u, Next &n) {
+    const int blk = block_of(u);
     if (IN == IN_PRE) {
       n.a0 = x0[d];
       n.a1 = x1[d];
@@ -489,48 +498,79 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
       c[mm] = (float)dot * factor;
     }
   };
-  auto prepare = [&](int d, int p, float (&c)[NMAT]) {
-    Next n;
-    load_act(d, p, n);
+  // All S units of pass p.
+  auto prepare = [&](int p, float (&c)[S][NMAT]) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) dot_part(d, k, n);
-    finish(d, n, c);
+    for (int i = 0; i < S; ++i) {
+      const int u = p * S + i;
+      Next n;
+      load_act(u % D, u, n);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dot_part(u % D, k, n);
+      finish(u % D, n, c[i]);
+    }
   };
-  // The serial chain over one pass's 16 blocks in block order: after step
-  // t, lane t of each row holds the running sum through block 16p + t;
-  // lane 15 carries it into the next pass.  The next pass's activation
-  // reads go out at step 0, its dots fill steps 4-7 and its scaling step
-  // 10, each pinned between DPP additions (whose dependent latency they
-  // hide) by sched_barrier.  The dots wait for the next pass's weights
-  // inside this chain, which costs nothing once the ring has landed.
-  auto chain_with = [&](const float (&c)[NMAT], bool has_next, int dn, int pn,
-                        float (&cn)[NMAT]) {
-    Next n;
-    if (has_next) load_act(dn, pn, n);
+  // The serial chain over one pass's 16 lane slots in block order: at step
+  // t, slot t takes the running sum from slot t-1 (DPP row rotation) and
+  // adds its S blocks in order; after step t, lane t of each row holds the
+  // sum through block 16S*p + S*t + S-1, and lane 15 carries it into the
+  // next pass.  The next pass's activation reads go out at step 0; its
+  // dots and scalings (5 pieces per unit) are spread over steps 4-14, each
+  // pinned between chain additions (whose dependent latency they hide) by
+  // sched_barrier.  The dots wait for the next pass's weights inside this
+  // chain, which costs nothing once the ring has landed.
+  auto chain_with = [&](const float (&c)[S][NMAT], bool has_next, int pn,
+                        float (&cn)[S][NMAT]) {
+    Next n[S];
+    if (has_next) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) load_act((pn * S + i) % D, pn * S + i, n[i]);
+    }
 #pragma unroll
     for (int t = 0; t < kPassBlocks; ++t) {
 #pragma unroll
       for (int mm = 0; mm < NMAT; ++mm)
-        acc[mm] = row_rotate1(acc[mm]) + c[mm];
+        acc[mm] = row_rotate1(acc[mm]) + c[0][mm];
+#pragma unroll
+      for (int i = 1; i < S; ++i) {
+#pragma unroll
+        for (int mm = 0; mm < NMAT; ++mm) acc[mm] = acc[mm] + c[i][mm];
+      }
       if (has_next) {
-        if (t >= 4 && t < 8) dot_part(dn, t - 4, n);
-        if (t == 10) finish(dn, n, cn);
+#pragma unroll
+        for (int o = 0; o < 5 * S; ++o) {
+          if (4 + (o * 11) / (5 * S) != t) continue;
+          const int i = o / 5, k = o % 5;
+          const int d = (pn * S + i) % D;
+          if (k < 4)
+            dot_part(d, k, n[i]);
+          else
+            finish(d, n[i], cn[i]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
   if (active) {
-    float cur[NMAT], nxt[NMAT];
-    prepare(0, 0, cur);
+    float cur[S][NMAT], nxt[S][NMAT];
+    prepare(0, cur);
     if constexpr (PC > 0) {
+      constexpr int NP = PC / S;
 #pragma unroll
-      for (int p = 0; p < PC; ++p) {
-        if (p + D < PC) issue(p % D, p + D);  // slot of pass p is free
+      for (int p = 0; p < NP; ++p) {
+        // refill the slots of this pass's units (prepared already)
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          const int u = p * S + i;
+          if (u + D < PC) issue(u % D, u + D);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        chain_with(cur, p + 1 < PC, (p + 1) % D, p + 1, nxt);
+        chain_with(cur, p + 1 < NP, p + 1, nxt);
 #pragma unroll
-        for (int mm = 0; mm < NMAT; ++mm) cur[mm] = nxt[mm];
+        for (int i = 0; i < S; ++i)
+#pragma unroll
+          for (int mm = 0; mm < NMAT; ++mm) cur[i][mm] = nxt[i][mm];
       }
     } else {
       for (int p0 = 0; p0 < passes; p0 += D) {
@@ -540,9 +580,9 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
           if (p < passes) {
             issue(d, p + D);
             __builtin_amdgcn_sched_barrier(0);
-            chain_with(cur, p + 1 < passes, (d + 1) % D, p + 1, nxt);
+            chain_with(cur, p + 1 < passes, p + 1, nxt);
 #pragma unroll
-            for (int mm = 0; mm < NMAT; ++mm) cur[mm] = nxt[mm];
+            for (int mm = 0; mm < NMAT; ++mm) cur[0][mm] = nxt[0][mm];
           }
         }
       }
@@ -634,8 +674,10 @@ __global__ void embedding_kernel(const int64_t *__restrict__ tokens,
     const int r = (int)(tok & 3);
     const int64_t b = c16 >> 1;
     const int h = (int)(c16 & 1);
-    const int j = (int)(b % kPassBlocks);
-    const uint8_t *pass = t + (g * passes + b / kPassBlocks) * kPassBytes;
+    int64_t u;
+    int j;
+    locate_seg(b, seg_for(passes), u, j);
+    const uint8_t *pass = t + (g * passes + u) * kPassBytes;
     const uint4 q = *(const uint4 *)(pass + h * 1024 + r * 256 + j * 16);
     const float d = half_bits_to_float(
         *(const uint16_t *)(pass + kPassQs + 2 * (16 * r + j)));
@@ -668,8 +710,10 @@ __global__ void block_dots_kernel(const int8_t *__restrict__ qa, int64_t ldq,
   const int64_t mi = t / (blocks * rows);
   const int64_t g = n >> 2;
   const int r = (int)(n & 3);
-  const int j = (int)(b % kPassBlocks);
-  const uint8_t *pass = w + (g * passes + b / kPassBlocks) * kPassBytes;
+  int64_t u;
+  int j;
+  locate_seg(b, seg_for(passes), u, j);
+  const uint8_t *pass = w + (g * passes + u) * kPassBytes;
   const uint4 w0 = *(const uint4 *)(pass + r * 256 + j * 16);
   const uint4 w1 = *(const uint4 *)(pass + 1024 + r * 256 + j * 16);
   const int8_t *arow = qa + mi * ldq + b * kBlock;
@@ -688,7 +732,11 @@ inline unsigned grid_for(int64_t threads, int block) {
 // matrix with a pre-quantized row: 12 passes of weights + input).
 template <int NMAT, int IN, int PC>
 constexpr int ring_depth() {
-  constexpr int dmax = NMAT == 2 ? 5 : (IN == IN_WG ? 18 : 12);
+  // at least two passes of units, so the next pass is in flight while the
+  // current one chains
+  constexpr int two = 2 * seg_for(PC);
+  constexpr int base = NMAT == 2 ? 5 : (IN == IN_WG ? 18 : 12);
+  constexpr int dmax = base > two ? base : two;
   return PC > 0 ? (PC < dmax ? PC : dmax) : (NMAT == 2 ? 4 : 8);
 }
 

@@ -32,7 +32,8 @@ def gemm(ctx, p4, n, k, x, activation="none"):
 
 
 @pytest.mark.parametrize("m,n,k", [(2, 136, 288), (19, 136, 288), (64, 264, 512),
-                                   (130, 520, 1056), (256, 1024, 2560)])
+                                   (130, 520, 1056), (256, 1024, 2560),
+                                   (33, 136, 4096), (17, 264, 8864)])
 @pytest.mark.parametrize("epi", ["fma", "scalar"])
 def test_gemm_bitwise(ctx, oracle, m, n, k, epi):
     rng = np.random.default_rng(m * 7 + n + k)

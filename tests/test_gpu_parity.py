@@ -61,8 +61,11 @@ def test_golden_fixture_rows(ctx, oracle):
     ctx.release(wt)
 
 
+# 4096 / 3872 (8 units of 16 blocks) and 9216 / 8864 (18 units) use the
+# segmented unit layout (4 and 6 blocks per lane slot and pass); 3872 and
+# 8864 also end in padded blocks.
 @pytest.mark.parametrize("k", [32, 288, 512, 1024, 1536, 2048, 2560, 3072,
-                               4096, 5120, 9216])
+                               3872, 4096, 5120, 8864, 9216])
 def test_gemv_matches_scalar_reference_bitwise(ctx, oracle, k):
     rng = np.random.default_rng(100 + k)
     n = 264 if k != 2560 else 2560
@@ -258,9 +261,9 @@ def test_lm_head_full_vocab(ctx, oracle):
     ctx.release(t)
 
 
-def test_embedding_gather(ctx, oracle):
-    rng = np.random.default_rng(14)
-    v, k = 4096, 2560
+@pytest.mark.parametrize("v,k", [(4096, 2560), (1024, 3872), (512, 9216)])
+def test_embedding_gather(ctx, oracle, v, k):
+    rng = np.random.default_rng(14 + k)
     w = weights(rng, v, k)
     p4 = oracle.pack_q8_0_p4(w)
     t = ctx.upload_p4(p4, v, k)
@@ -307,9 +310,10 @@ def test_quantizer_division_identities(ctx):
     assert ctx.selftest_quantizer() == 0
 
 
-def test_block_dots_exact(ctx, oracle):
-    rng = np.random.default_rng(16)
-    m, n, k = 3, 72, 1056
+@pytest.mark.parametrize("k", [1056, 3872, 8864])
+def test_block_dots_exact(ctx, oracle, k):
+    rng = np.random.default_rng(16 + k)
+    m, n = 3, 72
     w = weights(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     p4 = oracle.pack_q8_0_p4(w)
