@@ -96,6 +96,17 @@ def bench_decode_mlp(ctx, q8, steps, warmup, hidden=2560, ffn=9216):
         for mats in pool:
             ctx.swiglu(xd, mats[0][0], mats[1][0], hd, 1)
 
+    def down_rotation():
+        for mats in pool:
+            ctx.linear(hd, mats[2][0], yd, 1)
+
+    # fixed cost of one kernel node in graph replay: a 32-element quantize
+    tq, ts = ctx.alloc(64), ctx.alloc(64)
+
+    def tiny_rotation():
+        for _ in pool:
+            ctx.quantize(xd, 1, 32, tq, ts)
+
     timer = Timer(ctx)
     g_step = graph_of(ctx, one_rotation)
     g_gu = graph_of(ctx, gateup_rotation)
@@ -110,6 +121,11 @@ def bench_decode_mlp(ctx, q8, steps, warmup, hidden=2560, ffn=9216):
     run_graph(ctx, timer, g_gu, rounds_w)
     ms_gu = run_graph(ctx, timer, g_gu, rounds)
     gu_launch_us = ms_gu * 1e3 / (rounds * copies)
+    g_down, g_tiny = graph_of(ctx, down_rotation), graph_of(ctx, tiny_rotation)
+    run_graph(ctx, timer, g_down, rounds_w)
+    down_launch_us = run_graph(ctx, timer, g_down, rounds) * 1e3 / (rounds * copies)
+    run_graph(ctx, timer, g_tiny, rounds_w)
+    tiny_launch_us = run_graph(ctx, timer, g_tiny, rounds) * 1e3 / (rounds * copies)
     gu_bytes = 2 * p4_bytes(ffn, hidden) + hidden * 4 + ffn * 4
     gu_gbs = gu_bytes / (gu_launch_us * 1e-6) / 1e9
 
@@ -118,6 +134,7 @@ def bench_decode_mlp(ctx, q8, steps, warmup, hidden=2560, ffn=9216):
     res = dict(ms=ms, steps=n_steps, gb_s=gb_s, step_bytes=step_bytes,
                copies=copies, pool_bytes=copies * per_copy,
                gu_launch_us=gu_launch_us, gu_bytes=gu_bytes, gu_gbs=gu_gbs,
+               down_launch_us=down_launch_us, tiny_launch_us=tiny_launch_us,
                x=x, host_p4=host, hidden=hidden, ffn=ffn)
     for mats in pool:
         for w, p4d in mats:
@@ -400,10 +417,13 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": (load_traffic() or {}).get("hbm_bytes_per_launch"),
-                     "kernel": "gemv_kernel<NMAT=2,QIN> (fused gate/up SwiGLU, "
-                               "timed alone via llmcp_q8_swiglu)",
+                     "kernel": "gemv_kernel<2,0,false,IN_WG,3,5,5> (fused gate/up "
+                               "SwiGLU, 3-wave workgroups, input row quantized "
+                               "per workgroup; timed alone via llmcp_q8_swiglu)",
                      "launch_us": round(res["gu_launch_us"], 3),
-                     "algorithmic_bytes": res["gu_bytes"]},
+                     "algorithmic_bytes": res["gu_bytes"],
+                     "down_launch_us": round(res["down_launch_us"], 3),
+                     "graph_kernel_floor_us": round(res["tiny_launch_us"], 3)},
         "cpu_baseline": None if cpu is None else {
             k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()},
         "extra": extra,

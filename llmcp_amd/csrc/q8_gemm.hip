@@ -41,7 +41,7 @@ __device__ __forceinline__ float silu_f(float v) {
 // outer product (one exact product, one rounding -- the same value as the
 // VALU multiply) whose output layout is the int8 MFMA's, leaving two VALU
 // ops per element and block.
-template <int WM, int WN, int TM, int TN, bool FMA, int ACT>
+template <int WM, int WN, int TM, int TN, bool FMA, int ACT, int SEG>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     const int8_t *__restrict__ qa, int64_t ldq, const float *__restrict__ sa,
     int64_t lds, const uint8_t *__restrict__ w, int64_t n_rows, int64_t m_rows,
@@ -71,7 +71,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int stages = passes * (kPassBlocks / SB);
-  const int seg = seg_for(passes);  // weight unit layout (q8_common.h)
 
   // ---- global -> registers for one stage
   constexpr int AU = BM * 8 / NT;           // 16 B pieces of A per thread
@@ -101,7 +100,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
         const int b = kb + (q >> 1);
         int64_t unit;
         int slot;
-        locate_seg(b, seg, unit, slot);
+        locate<SEG>(b, unit, slot);  // weight unit layout (q8_common.h)
         const uint8_t *pass =
             w + ((n >> 2) * passes + unit) * (int64_t)kPassBytes;
         rb[u] = *(const uint4 *)(pass + (q & 1) * 1024 + (n & 3) * 256 +
@@ -125,7 +124,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
         const int b = kb + bb;
         int64_t unit;
         int slot;
-        locate_seg(b, seg, unit, slot);
+        locate<SEG>(b, unit, slot);
         const uint8_t *pass =
             w + ((n >> 2) * passes + unit) * (int64_t)kPassBytes;
         rdw[u] = *(const uint16_t *)(pass + kPassQs + 2 * (16 * (n & 3) + slot));
@@ -277,9 +276,23 @@ static hipError_t launch_gemm_t(const GemmLaunch &l, hipStream_t s) {
   const int32_t n_tiles = (int32_t)((l.rows + BN - 1) / BN);
   const int32_t n_tiles8 = (n_tiles + 7) / 8 * 8;
   const unsigned grid = (unsigned)(n_tiles8 * m_tiles);
-  hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, ACT>), dim3(grid),
-                     dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
-                     l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+  // the weight's unit layout is fixed at registration (seg_for)
+  switch (seg_for(passes)) {
+    case 6:
+      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, ACT, 6>), dim3(grid),
+                         dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
+                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+      break;
+    case 4:
+      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, ACT, 4>), dim3(grid),
+                         dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
+                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, ACT, 1>), dim3(grid),
+                         dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
+                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+  }
   return hipGetLastError();
 }
 
