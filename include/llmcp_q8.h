@@ -42,7 +42,7 @@ extern "C" {
 /* Version of this C ABI.  The model ABI of the AOT library
  * (llmcp_model_abi_version() == 2, include/llmcp/Support/AotAbi.h:12) is not
  * changed by this library. */
-#define LLMCP_Q8_ABI_VERSION 1
+#define LLMCP_Q8_ABI_VERSION 2
 
 enum llmcp_q8_status {
   LLMCP_Q8_OK = 0,
@@ -55,7 +55,16 @@ enum llmcp_q8_status {
   LLMCP_Q8_ENOMEM = 7     /* device allocation failed */
 };
 
-enum llmcp_q8_activation { LLMCP_Q8_ACT_NONE = 0, LLMCP_Q8_ACT_SILU = 1 };
+/* The activations llmcp.linear accepts (LLMCPOps.cpp:74-77), applied to the
+ * f32 accumulator before the store (applyMatmulActivation,
+ * MatmulLoweringCommon.cpp:78-103): silu v/(1+exp(-v)) as v*(1/(1+exp(-v))),
+ * sigmoid 1/(1+exp(-v)), softplus log1p(exp(v)). */
+enum llmcp_q8_activation {
+  LLMCP_Q8_ACT_NONE = 0,
+  LLMCP_Q8_ACT_SILU = 1,
+  LLMCP_Q8_ACT_SIGMOID = 2,
+  LLMCP_Q8_ACT_SOFTPLUS = 3
+};
 
 /* Per-block epilogue of the prefill GEMM.  Both are the reference's math:
  * FMA    acc = fma(f32(I), sa*dw, acc)  -- the SDOT GEMM, Q8Matmul.cpp:204-223
@@ -74,6 +83,16 @@ typedef struct {
   int64_t sizes[2];
   int64_t strides[2];
 } llmcp_memref_f32_2d;
+
+/* bf16 activations: the same descriptor with 16-bit elements (raw bf16
+ * bits; the real model's hidden state is bf16, ModelBuilder.cpp:72). */
+typedef struct {
+  uint16_t *base;
+  uint16_t *data;
+  int64_t offset;
+  int64_t sizes[2];
+  int64_t strides[2];
+} llmcp_memref_bf16_2d;
 
 typedef struct {
   int8_t *base;
@@ -149,12 +168,21 @@ int llmcp_q8_arena_inspect(const void *file, uint64_t file_bytes,
 /* llmcp.linear with weight_format q8_0_p4 (LowerToLinalg.cpp:143-209):
  * y[M,N] = act(x[M,K] . W[N,K]^T), x quantized per call to Q8_1 blocks.
  * execution_mode DECODE requires M == 1 and runs the GEMV; PREFILL runs the
- * int8-MFMA GEMM for any M (its epilogue: llmcp_q8_set_gemm_epilogue).  activation: NONE or SILU
- * (applyMatmulActivation, MatmulLoweringCommon.cpp:78-103). */
+ * int8-MFMA GEMM for M > 1 (its epilogue: llmcp_q8_set_gemm_epilogue) and
+ * the GEMV for M == 1.  activation: llmcp_q8_activation. */
 int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                     const llmcp_memref_i8_1d *weight,
                     llmcp_memref_f32_2d *output, int32_t activation,
                     int32_t execution_mode);
+
+/* The same with bf16 input and output (the hook's tensor<MxK x bf16> ->
+ * MxN bf16 case): x is widened exactly before Q8_1 quantization
+ * (Q8Decode.cpp:97-98) and the activated f32 result is rounded to bf16
+ * (arith.truncf, round to nearest even; Q8Decode.cpp:126-127). */
+int llmcp_q8_linear_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                         const llmcp_memref_i8_1d *weight,
+                         llmcp_memref_bf16_2d *output, int32_t activation,
+                         int32_t execution_mode);
 
 /* Fused SwiGLU hidden: h = silu(x . Wg^T) * (x . Wu^T), the pair
  * `linear{activation=silu}` + `mul` that FuseSiluMul produces
@@ -164,16 +192,32 @@ int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                     const llmcp_memref_i8_1d *w_up,
                     llmcp_memref_f32_2d *output, int32_t execution_mode);
 
+/* bf16 in and out: both linears' results are rounded to bf16 before the
+ * bf16 multiply, h = bf16(bf16(silu(g)) * bf16(u)), as the pair
+ * linear{silu} + mul computes on bf16 tensors. */
+int llmcp_q8_swiglu_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                         const llmcp_memref_i8_1d *w_gate,
+                         const llmcp_memref_i8_1d *w_up,
+                         llmcp_memref_bf16_2d *output, int32_t execution_mode);
+
 /* Decode MLP of one layer, ModelBuilder.cpp:205-216 with FuseSiluMul:
- * h = silu(x . Wg^T) * (x . Wu^T), y = h . Wd^T.  Two kernels: the fused
- * gate/up GEMV also quantizes h (Q8_1, as the down linear's quantizer
- * would), so the down GEMV reads it directly.  `hidden` (nullable) receives
- * h in f32.  Results equal llmcp_q8_swiglu followed by llmcp_q8_linear. */
+ * h = silu(x . Wg^T) * (x . Wu^T), y = h . Wd^T, for M == 1.  Two kernels:
+ * the fused gate/up GEMV, then the down GEMV (which quantizes h once per
+ * workgroup).  `hidden` (nullable) receives h.  Results equal
+ * llmcp_q8_swiglu followed by llmcp_q8_linear. */
 int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                  const llmcp_memref_i8_1d *w_gate,
                  const llmcp_memref_i8_1d *w_up,
                  const llmcp_memref_i8_1d *w_down, llmcp_memref_f32_2d *hidden,
                  llmcp_memref_f32_2d *output, int32_t execution_mode);
+
+/* bf16 in, hidden and out (llmcp_q8_swiglu_bf16 then llmcp_q8_linear_bf16). */
+int llmcp_q8_mlp_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                      const llmcp_memref_i8_1d *w_gate,
+                      const llmcp_memref_i8_1d *w_up,
+                      const llmcp_memref_i8_1d *w_down,
+                      llmcp_memref_bf16_2d *hidden,
+                      llmcp_memref_bf16_2d *output, int32_t execution_mode);
 
 /* llmcp.lm_head (LowerToLinalg.cpp:729-765): f32 logits [M,V] over the tied
  * table, plus the first-maximum index of the last row written to
@@ -184,6 +228,13 @@ int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
                      llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
                      int32_t execution_mode);
 
+/* bf16 hidden state, f32 logits (the AOT ABI's logits are f32,
+ * AotRuntime.cpp:87-118). */
+int llmcp_q8_lm_head_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *hidden,
+                          const llmcp_memref_i8_1d *table,
+                          llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
+                          int32_t execution_mode);
+
 /* llmcp.embedding with weight_format q8_0_p4 (emitQ8PackedEmbedding,
  * LowerToLinalg.cpp:435-531): out[t, c] = f32(q(token_t, c)) * f32(d).
  * Tokens outside [0, rows) produce a zero row and set the context's
@@ -191,6 +242,13 @@ int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
 int llmcp_q8_embedding(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
                        const llmcp_memref_i8_1d *table,
                        llmcp_memref_f32_2d *output);
+
+/* bf16 result: the exact f32 product rounded to bf16 (the truncf the
+ * lowering emits for a bf16 embedding). */
+int llmcp_q8_embedding_bf16(llmcp_q8_ctx *ctx,
+                            const llmcp_memref_i64_1d *tokens,
+                            const llmcp_memref_i8_1d *table,
+                            llmcp_memref_bf16_2d *output);
 
 /* Activation quantizer Q8_1 (Q8Decode.cpp:83-120): qa_dev int8 [M,K] and
  * sa_dev f32 [M,K/32], both dense row-major device buffers. */
@@ -259,6 +317,24 @@ int32_t _mlir_ciface_llmcp_q8_lm_head(llmcp_memref_f32_2d *hidden,
 int32_t _mlir_ciface_llmcp_q8_embedding(llmcp_memref_i64_1d *tokens,
                                         llmcp_memref_i8_1d *table,
                                         llmcp_memref_f32_2d *output);
+int32_t _mlir_ciface_llmcp_q8_linear_bf16(llmcp_memref_bf16_2d *input,
+                                          llmcp_memref_i8_1d *weight,
+                                          llmcp_memref_bf16_2d *output,
+                                          int32_t activation,
+                                          int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_swiglu_bf16(llmcp_memref_bf16_2d *input,
+                                          llmcp_memref_i8_1d *w_gate,
+                                          llmcp_memref_i8_1d *w_up,
+                                          llmcp_memref_bf16_2d *output,
+                                          int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_lm_head_bf16(llmcp_memref_bf16_2d *hidden,
+                                           llmcp_memref_i8_1d *table,
+                                           llmcp_memref_f32_2d *logits,
+                                           llmcp_memref_i64_1d *argmax,
+                                           int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_embedding_bf16(llmcp_memref_i64_1d *tokens,
+                                             llmcp_memref_i8_1d *table,
+                                             llmcp_memref_bf16_2d *output);
 
 /* ------------------------------------------- device plumbing (host use) -- */
 /* Small helpers so hosts without a HIP toolchain (ctypes, cgo) can move data

@@ -17,7 +17,8 @@ LIB_PATH = os.path.join(HERE, "libllmcp_q8.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "llmcp_q8.h")
 
 OK, DECLINED, EINVAL, ENOTFOUND, EHIP, EFORMAT, EIO, ENOMEM = range(8)
-ACT = {"none": 0, "silu": 1}
+ACT = {"none": 0, "silu": 1, "sigmoid": 2, "softplus": 3}
+DTYPES = ("f32", "bf16")
 MODE = {"prefill": 0, "decode": 1}
 
 _lib = None
@@ -69,6 +70,10 @@ EXPORTS = [
     "llmcp_q8_event_elapsed_ms", "llmcp_q8_graph_begin", "llmcp_q8_graph_end",
     "llmcp_q8_graph_launch", "llmcp_q8_graph_destroy",
     "llmcp_q8_device_bytes", "llmcp_q8_selftest_quantizer",
+    "llmcp_q8_linear_bf16", "llmcp_q8_swiglu_bf16", "llmcp_q8_mlp_bf16",
+    "llmcp_q8_lm_head_bf16", "llmcp_q8_embedding_bf16",
+    "_mlir_ciface_llmcp_q8_linear_bf16", "_mlir_ciface_llmcp_q8_swiglu_bf16",
+    "_mlir_ciface_llmcp_q8_lm_head_bf16", "_mlir_ciface_llmcp_q8_embedding_bf16",
 ]
 
 
@@ -130,6 +135,15 @@ def lib():
         "llmcp_q8_graph_destroy": (I, [P]),
         "llmcp_q8_device_bytes": (U64, [P, P]),
         "llmcp_q8_selftest_quantizer": (I, [P, ctypes.POINTER(U64)]),
+        "llmcp_q8_linear_bf16": (I, [P, P, P, P, I32, I32]),
+        "llmcp_q8_swiglu_bf16": (I, [P, P, P, P, P, I32]),
+        "llmcp_q8_mlp_bf16": (I, [P, P, P, P, P, P, P, I32]),
+        "llmcp_q8_lm_head_bf16": (I, [P, P, P, P, P, I32]),
+        "llmcp_q8_embedding_bf16": (I, [P, P, P, P]),
+        "_mlir_ciface_llmcp_q8_linear_bf16": (I32, [P, P, P, I32, I32]),
+        "_mlir_ciface_llmcp_q8_swiglu_bf16": (I32, [P, P, P, P, I32]),
+        "_mlir_ciface_llmcp_q8_lm_head_bf16": (I32, [P, P, P, P, I32]),
+        "_mlir_ciface_llmcp_q8_embedding_bf16": (I32, [P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -301,45 +315,54 @@ class Context:
                                           file_bytes.nbytes, ctypes.byref(n)))
         return n.value
 
-    # ---- ops (device pointers in, device pointers out)
-    def linear(self, x, w, y, m, activation="none", mode="decode"):
+    # ---- ops (device pointers in, device pointers out).  dtype "bf16"
+    # selects the *_bf16 entry: bf16 activations in and out (raw uint16
+    # bits; the lm_head keeps f32 logits).  The descriptor layout is the
+    # same for both element types.
+    @staticmethod
+    def _entry(name, dtype):
+        if dtype not in DTYPES:
+            raise ValueError("dtype must be one of %r" % (DTYPES,))
+        return getattr(lib(), name + ("_bf16" if dtype == "bf16" else ""))
+
+    def linear(self, x, w, y, m, activation="none", mode="decode", dtype="f32"):
         xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, w.cols)
         yo = f32_memref(y.ptr if hasattr(y, "ptr") else y, m, w.rows)
-        check(lib().llmcp_q8_linear(self.handle, ctypes.byref(xi),
-                                    ctypes.byref(w.memref()), ctypes.byref(yo),
-                                    ACT[activation], MODE[mode]))
+        check(self._entry("llmcp_q8_linear", dtype)(
+            self.handle, ctypes.byref(xi), ctypes.byref(w.memref()),
+            ctypes.byref(yo), ACT[activation], MODE[mode]))
 
-    def swiglu(self, x, wg, wu, h, m, mode="decode"):
+    def swiglu(self, x, wg, wu, h, m, mode="decode", dtype="f32"):
         xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, wg.cols)
         ho = f32_memref(h.ptr if hasattr(h, "ptr") else h, m, wg.rows)
-        check(lib().llmcp_q8_swiglu(self.handle, ctypes.byref(xi),
-                                    ctypes.byref(wg.memref()),
-                                    ctypes.byref(wu.memref()), ctypes.byref(ho),
-                                    MODE[mode]))
+        check(self._entry("llmcp_q8_swiglu", dtype)(
+            self.handle, ctypes.byref(xi), ctypes.byref(wg.memref()),
+            ctypes.byref(wu.memref()), ctypes.byref(ho), MODE[mode]))
 
-    def mlp(self, x, wg, wu, wd, y, h=None, m=1, mode="decode"):
+    def mlp(self, x, wg, wu, wd, y, h=None, m=1, mode="decode", dtype="f32"):
         xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, wg.cols)
         yo = f32_memref(y.ptr if hasattr(y, "ptr") else y, m, wd.rows)
         ho = f32_memref(h.ptr if hasattr(h, "ptr") else h, m, wg.rows) if h is not None else None
-        check(lib().llmcp_q8_mlp(self.handle, ctypes.byref(xi),
-                                 ctypes.byref(wg.memref()), ctypes.byref(wu.memref()),
-                                 ctypes.byref(wd.memref()),
-                                 ctypes.byref(ho) if ho is not None else None,
-                                 ctypes.byref(yo), MODE[mode]))
+        check(self._entry("llmcp_q8_mlp", dtype)(
+            self.handle, ctypes.byref(xi), ctypes.byref(wg.memref()),
+            ctypes.byref(wu.memref()), ctypes.byref(wd.memref()),
+            ctypes.byref(ho) if ho is not None else None,
+            ctypes.byref(yo), MODE[mode]))
 
-    def lm_head(self, x, w, logits, m, argmax=None, mode="decode"):
+    def lm_head(self, x, w, logits, m, argmax=None, mode="decode", dtype="f32"):
         xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, w.cols)
         lo = f32_memref(logits.ptr if hasattr(logits, "ptr") else logits, m, w.rows)
         am = argmax.ptr if argmax is not None else None
-        check(lib().llmcp_q8_lm_head(self.handle, ctypes.byref(xi),
-                                     ctypes.byref(w.memref()), ctypes.byref(lo),
-                                     am, MODE[mode]))
+        check(self._entry("llmcp_q8_lm_head", dtype)(
+            self.handle, ctypes.byref(xi), ctypes.byref(w.memref()),
+            ctypes.byref(lo), am, MODE[mode]))
 
-    def embedding(self, tokens, count, w, out):
+    def embedding(self, tokens, count, w, out, dtype="f32"):
         t = i64_memref(tokens.ptr, count)
         o = f32_memref(out.ptr, count, w.cols)
-        check(lib().llmcp_q8_embedding(self.handle, ctypes.byref(t),
-                                       ctypes.byref(w.memref()), ctypes.byref(o)))
+        check(self._entry("llmcp_q8_embedding", dtype)(
+            self.handle, ctypes.byref(t), ctypes.byref(w.memref()),
+            ctypes.byref(o)))
 
     def quantize(self, x, m, k, qa, sa):
         xi = f32_memref(x.ptr, m, k)

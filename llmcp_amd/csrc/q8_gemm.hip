@@ -19,6 +19,8 @@
 // into that XCD's L2 once and reused.
 #include "q8_kernels.h"
 
+#include "q8_device.h"
+
 namespace llmcp_q8 {
 namespace {
 
@@ -29,24 +31,18 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int SB = 4;                  // blocks per stage
 constexpr int ROW = SB * kBlock + 16;  // LDS row stride (bytes), padded
 
-__device__ __forceinline__ float silu_f(float v) {
-  const float e = (float)exp((double)(-v));
-  const float sig = 1.0f / (1.0f + e);
-  return v * sig;
-}
-
 // Workgroup of WM x WN waves; each wave owns TM x TN tiles of 32x32, so the
 // workgroup tile is BM = 32*WM*TM rows of activations by BN = 32*WN*TN
 // weight rows.  The per-block scale tile sa (x) dw is formed by an f32 MFMA
 // outer product (one exact product, one rounding -- the same value as the
 // VALU multiply) whose output layout is the int8 MFMA's, leaving two VALU
 // ops per element and block.
-template <int WM, int WN, int TM, int TN, bool FMA, int ACT, int SEG>
+template <int WM, int WN, int TM, int TN, bool FMA, int SEG>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     const int8_t *__restrict__ qa, int64_t ldq, const float *__restrict__ sa,
     int64_t lds, const uint8_t *__restrict__ w, int64_t n_rows, int64_t m_rows,
-    int32_t passes, int32_t m_tiles, int32_t n_tiles, float *__restrict__ y,
-    int64_t ldy) {
+    int32_t passes, int32_t m_tiles, int32_t n_tiles, void *__restrict__ y,
+    int64_t ldy, int act, int y_bf16) {
   constexpr int NT = 64 * WM * WN;
   constexpr int BM = 32 * WM * TM;
   constexpr int BN = 32 * WN * TN;
@@ -245,30 +241,43 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
       for (int v = 0; v < 16; ++v) {
         const int64_t m = m0 + mrow + 32 * tm + 8 * (v >> 2) + 4 * lh + (v & 3);
         if (m < m_rows && n < n_rows) {
-          float o = acc[tm][tn][v];
-          if (ACT == 1) o = silu_f(o);
-          y[m * ldy + n] = o;
+          const float o = activate(acc[tm][tn][v], act);
+          if (y_bf16)
+            ((uint16_t *)y)[m * ldy + n] = float_to_bf16(o);
+          else
+            ((float *)y)[m * ldy + n] = o;
         }
       }
     }
 }
 
-__global__ void mul_kernel(float *__restrict__ h, const float *__restrict__ u,
-                           int64_t count) {
+// SwiGLU multiply of the prefill path: gate (SiLU applied) and up in f32.
+// f32: h = g * u in place.  bf16 result: each linear's output rounds to
+// bf16 first, then the bf16 multiply (FuseSiluMul on bf16 tensors).
+__global__ void mul_kernel(float *__restrict__ g, const float *__restrict__ u,
+                           uint16_t *__restrict__ out_bf16, int64_t count) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < count) h[i] = h[i] * u[i];
+  if (i >= count) return;
+  if (out_bf16) {
+    const float gb = bf16_to_float(float_to_bf16(g[i]));
+    const float ub = bf16_to_float(float_to_bf16(u[i]));
+    out_bf16[i] = float_to_bf16(gb * ub);
+  } else {
+    g[i] = g[i] * u[i];
+  }
 }
 
 }  // namespace
 
-hipError_t launch_mul(float *h, const float *u, int64_t count, hipStream_t s) {
+hipError_t launch_mul(float *g, const float *u, uint16_t *out_bf16,
+                      int64_t count, hipStream_t s) {
   if (count == 0) return hipSuccess;
   hipLaunchKernelGGL(mul_kernel, dim3((unsigned)((count + 255) / 256)),
-                     dim3(256), 0, s, h, u, count);
+                     dim3(256), 0, s, g, u, out_bf16, count);
   return hipGetLastError();
 }
 
-template <int WM, int WN, int TM, int TN, bool FMA, int ACT>
+template <int WM, int WN, int TM, int TN, bool FMA>
 static hipError_t launch_gemm_t(const GemmLaunch &l, hipStream_t s) {
   constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
   const int32_t passes = (int32_t)passes_for(l.cols);
@@ -279,38 +288,37 @@ static hipError_t launch_gemm_t(const GemmLaunch &l, hipStream_t s) {
   // the weight's unit layout is fixed at registration (seg_for)
   switch (seg_for(passes)) {
     case 6:
-      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, ACT, 6>), dim3(grid),
+      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, 6>), dim3(grid),
                          dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
-                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
+                         l.activation, l.y_bf16 ? 1 : 0);
       break;
     case 4:
-      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, ACT, 4>), dim3(grid),
+      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, 4>), dim3(grid),
                          dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
-                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
+                         l.activation, l.y_bf16 ? 1 : 0);
       break;
     default:
-      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, ACT, 1>), dim3(grid),
+      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, 1>), dim3(grid),
                          dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
-                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
+                         l.activation, l.y_bf16 ? 1 : 0);
   }
   return hipGetLastError();
 }
 
-template <bool FMA, int ACT>
+template <bool FMA>
 static hipError_t launch_gemm_shape(const GemmLaunch &l, hipStream_t s) {
   // 8 waves: up to 64 rows a 64x128 workgroup tile of one 32x32 tile per
   // wave (more workgroups share the weight stream); else 128x128 with a
   // 32x64 tile per wave, whose two scale tiles come from one MFMA.
-  if (l.m <= 64) return launch_gemm_t<2, 4, 1, 1, FMA, ACT>(l, s);
-  return launch_gemm_t<4, 2, 1, 2, FMA, ACT>(l, s);
+  if (l.m <= 64) return launch_gemm_t<2, 4, 1, 1, FMA>(l, s);
+  return launch_gemm_t<4, 2, 1, 2, FMA>(l, s);
 }
 
 hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s) {
-  if (l.fma)
-    return l.activation == 1 ? launch_gemm_shape<true, 1>(l, s)
-                             : launch_gemm_shape<true, 0>(l, s);
-  return l.activation == 1 ? launch_gemm_shape<false, 1>(l, s)
-                           : launch_gemm_shape<false, 0>(l, s);
+  return l.fma ? launch_gemm_shape<true>(l, s) : launch_gemm_shape<false>(l, s);
 }
 
 }  // namespace llmcp_q8

@@ -21,9 +21,10 @@ hipError_t launch_synth(uint64_t seed, int64_t rows, int64_t cols,
 hipError_t launch_pack_p4(const float *w, int64_t rows, int64_t cols,
                           uint8_t *p4, hipStream_t s);
 
-// Q8_1 activation quantizer: x [m, cols] (row stride ldx floats) ->
-// qa [m, ldq] int8 and sa [m, lds] f32, zero-filled up to blocks_pad blocks.
-hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
+// Q8_1 activation quantizer: x [m, cols] f32 or bf16 (row stride ldx
+// elements) -> qa [m, ldq] int8 and sa [m, lds] f32, zero-filled up to
+// blocks_pad blocks.
+hipError_t launch_quantize(const void *x, bool x_bf16, int64_t m, int64_t ldx,
                            int64_t cols, int8_t *qa, int64_t ldq, float *sa,
                            int64_t lds, int64_t blocks_pad, hipStream_t s);
 
@@ -32,16 +33,17 @@ hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
 hipError_t launch_selftest_quantizer(unsigned long long *bad, hipStream_t s);
 
 struct GemvLaunch {
-  const float *x = nullptr;      // f32 input row (16 B aligned), quantized
-                                 // once per workgroup into LDS
+  const void *x = nullptr;       // input row (f32 16 B / bf16 8 B aligned),
+  bool x_bf16 = false;           // quantized once per workgroup into LDS
   const int8_t *qa = nullptr;    // or: Q8_1 input row, padded to passes*16
   const float *sa = nullptr;     //     blocks (used when x is null)
-  const uint8_t *w[2] = {nullptr, nullptr};  // pass-layout weights
-  float *y = nullptr;            // f32 output [rows]
+  const uint8_t *w[2] = {nullptr, nullptr};  // unit-layout weights
+  void *y = nullptr;             // output [rows], f32 or bf16
+  bool y_bf16 = false;
   int64_t rows = 0;              // N
   int64_t cols = 0;              // K
   int nmat = 1;                  // 2 = fused SwiGLU (gate, up)
-  int activation = 0;            // 0 none, 1 silu (nmat == 1 only)
+  int activation = 0;            // llmcp_q8_activation (nmat == 1 only)
   unsigned long long *keys = nullptr;  // non-null: fused argmax partials,
   int64_t *argmax_out = nullptr;       // gemv_workgroups(rows) entries
 };
@@ -67,21 +69,24 @@ struct GemmLaunch {
   int64_t rows = 0;            // N
   int64_t cols = 0;            // K
   int64_t m = 0;               // M
-  float *y = nullptr;
+  void *y = nullptr;             // f32 or bf16 [m, ldy]
+  bool y_bf16 = false;
   int64_t ldy = 0;
-  int activation = 0;
+  int activation = 0;            // llmcp_q8_activation
   bool fma = true;             // epilogue: fma (SDOT GEMM) or mul+add (scalar)
 };
 
 hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);
 
-// h[i] = h[i] * u[i] (f32), the SwiGLU multiply of the prefill path.
-hipError_t launch_mul(float *h, const float *u, int64_t count, hipStream_t s);
+// SwiGLU multiply of the prefill path from f32 gate (SiLU applied) and up:
+// f32 h = g * u in place in g, or bf16 out = bf16(bf16(g) * bf16(u)).
+hipError_t launch_mul(float *g, const float *u, uint16_t *out_bf16,
+                      int64_t count, hipStream_t s);
 
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             const uint8_t *table, int64_t rows, int64_t cols,
-                            float *out, int64_t ldo, int32_t *err_flag,
-                            hipStream_t s);
+                            void *out, bool out_bf16, int64_t ldo,
+                            int32_t *err_flag, hipStream_t s);
 
 hipError_t launch_block_dots(const int8_t *qa, int64_t ldq, int64_t m,
                              const uint8_t *w, int64_t rows, int64_t cols,

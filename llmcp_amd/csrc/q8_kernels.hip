@@ -14,28 +14,10 @@
 
 #include <math.h>
 
+#include "q8_device.h"
+
 namespace llmcp_q8 {
 namespace {
-
-__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
-}
-
-__device__ __forceinline__ uint16_t float_to_half_bits(float v) {
-  return __builtin_bit_cast(uint16_t, (_Float16)v);  // v_cvt_f16_f32: RNE
-}
-
-// Correctly rounded f32 exp via f64: the same definition the oracle uses.
-__device__ __forceinline__ float exp_f32(float v) {
-  return (float)exp((double)v);
-}
-
-// applyMatmulActivation "silu" (MatmulLoweringCommon.cpp:85-92).
-__device__ __forceinline__ float silu(float v) {
-  float e = exp_f32(-v);
-  float sig = 1.0f / (1.0f + e);
-  return v * sig;
-}
 
 __device__ __forceinline__ uint32_t word(const uint4 &v, int k) {
   return k == 0 ? v.x : (k == 1 ? v.y : (k == 2 ? v.z : v.w));
@@ -225,9 +207,23 @@ __device__ __forceinline__ void quantize_block8(float4 v, bool valid,
   *s_out = s;  // the same in all 8 lanes of the block
 }
 
-__device__ __forceinline__ float4 load_float4(const float *p, bool aligned) {
-  if (aligned) return *(const float4 *)p;
-  return make_float4(p[0], p[1], p[2], p[3]);
+// Four consecutive activations as f32: an f32 row (one float4 when 16 B
+// aligned) or a bf16 row (widened exactly, one 8 B load when aligned).
+__device__ __forceinline__ float4 load_act4(const void *p, int64_t i,
+                                            bool bf16, bool aligned) {
+  if (bf16) {
+    const uint16_t *h = (const uint16_t *)p + i;
+    if (aligned) {
+      const uint2 w = *(const uint2 *)h;
+      return make_float4(bf16_to_float(w.x & 0xffffu), bf16_to_float(w.x >> 16),
+                         bf16_to_float(w.y & 0xffffu), bf16_to_float(w.y >> 16));
+    }
+    return make_float4(bf16_to_float(h[0]), bf16_to_float(h[1]),
+                       bf16_to_float(h[2]), bf16_to_float(h[3]));
+  }
+  const float *f = (const float *)p + i;
+  if (aligned) return *(const float4 *)f;
+  return make_float4(f[0], f[1], f[2], f[3]);
 }
 
 // Exhaustive check of div127 and recip against IEEE division over the
@@ -254,10 +250,10 @@ __global__ void selftest_quant_kernel(uint32_t lo, uint32_t hi,
 }
 
 // Grid: x covers (row, padded block) in units of 8 blocks per wave.
-__global__ void quantize_kernel(const float *__restrict__ x, int64_t m,
-                                int64_t ldx, int64_t blocks, int8_t *qa,
-                                int64_t ldq, float *sa, int64_t lds,
-                                int64_t blocks_pad, int aligned) {
+__global__ void quantize_kernel(const void *__restrict__ x, int x_bf16,
+                                int64_t m, int64_t ldx, int64_t blocks,
+                                int8_t *qa, int64_t ldq, float *sa,
+                                int64_t lds, int64_t blocks_pad, int aligned) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t blk_all = t >> 3;  // global (row, block) index
   const int lane = threadIdx.x & 63;
@@ -267,7 +263,8 @@ __global__ void quantize_kernel(const float *__restrict__ x, int64_t m,
   const bool valid = in_range && blk < blocks;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (valid)
-    v = load_float4(x + row * ldx + blk * kBlock + (lane & 7) * 4, aligned);
+    v = load_act4(x, row * ldx + blk * kBlock + (lane & 7) * 4, x_bf16 != 0,
+                  aligned != 0);
   int32_t q;
   float s;
   quantize_block8(v, valid, &q, &s);
@@ -280,16 +277,19 @@ __global__ void quantize_kernel(const float *__restrict__ x, int64_t m,
 // --------------------------------------------------------------- GEMV -- //
 
 struct GemvArgs {
-  const float *x;    // IN_WG: f32 input row, 16 B aligned
+  const void *x;     // IN_WG: input row, f32 (16 B aligned) or bf16 (8 B)
   const int8_t *qa;  // IN_PRE: Q8_1 input, padded to passes * 16 blocks
   const float *sa;
   const uint8_t *w0;
   const uint8_t *w1;
-  float *y;
+  void *y;           // output row, f32 or bf16
   unsigned long long *keys;  // ARGMAX: one (value, index) key per workgroup
   int64_t groups;
   int32_t blocks;
   int32_t passes;
+  int32_t act;       // llmcp_q8_activation (one-matrix GEMVs)
+  int32_t x_bf16;
+  int32_t y_bf16;
 };
 
 // Where the GEMV's input row comes from.
@@ -335,7 +335,7 @@ __host__ __device__ constexpr int row_slots(int pc, int w) {
 // Per pass, prepare() forms the 16 blocks' contributions and chain() adds
 // them in block order; the next pass's prepare() is scheduled together with
 // the current chain(), so the dots overlap the serial DPP additions.
-template <int NMAT, int ACT, bool ARGMAX, int IN, int W, int D, int PC>
+template <int NMAT, bool ARGMAX, int IN, int W, int D, int PC>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];  // IN_WG input row
   __shared__ unsigned long long key_l[W];
@@ -363,13 +363,22 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   int8_t *qa_l = (int8_t *)lds;
   float *sa_l = (float *)(lds + nslot * kBlock);
 
-  float4 xv[XR];
+  // Raw row words: f32 fills all four, bf16 the first two (4 values).
+  uint4 xr[XR];
   if (kRowFirst) {
 #pragma unroll
     for (int u = 0; u < XR; ++u) {
       const int t = u * 64 * W + (int)threadIdx.x;
-      xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if ((t >> 3) < a.blocks) xv[u] = *(const float4 *)(a.x + t * 4);
+      xr[u] = make_uint4(0, 0, 0, 0);
+      if ((t >> 3) < a.blocks) {
+        if (a.x_bf16) {
+          const uint2 w2 = *(const uint2 *)((const uint16_t *)a.x + t * 4);
+          xr[u].x = w2.x;
+          xr[u].y = w2.y;
+        } else {
+          xr[u] = *(const uint4 *)((const float *)a.x + t * 4);
+        }
+      }
     }
   }
 
@@ -422,7 +431,13 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         const int t = u * 64 * W + (int)threadIdx.x;
         int32_t q;
         float sq;
-        quantize_block8(xv[u], true, &q, &sq);
+        const float4 v =
+            a.x_bf16 ? make_float4(bf16_to_float(xr[u].x & 0xffffu),
+                                   bf16_to_float(xr[u].x >> 16),
+                                   bf16_to_float(xr[u].y & 0xffffu),
+                                   bf16_to_float(xr[u].y >> 16))
+                     : __builtin_bit_cast(float4, xr[u]);
+        quantize_block8(v, true, &q, &sq);
         ((int32_t *)qa_l)[t] = q;
         sa_l[t >> 3] = sq;
       }
@@ -435,7 +450,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         for (int u = 0; u < U; ++u) {
           const int t = t0 + u * 64 * W + (int)threadIdx.x;
           v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-          if ((t >> 3) < a.blocks) v[u] = *(const float4 *)(a.x + t * 4);
+          if ((t >> 3) < a.blocks) v[u] = load_act4(a.x, t * 4, a.x_bf16 != 0, true);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -590,16 +605,30 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   }
 
   const int64_t row = g * kLanes + r;
+  // Epilogue (MatmulLoweringCommon.cpp:78-103).  SwiGLU: h = silu(gate) *
+  // up; with a bf16 result each linear's output is rounded to bf16 before
+  // the bf16 multiply (FuseSiluMul: linear{silu} + mul on bf16 tensors).
   float y;
-  if (NMAT == 2)
-    y = silu(acc[0]) * acc[NMAT - 1];
-  else
-    y = ACT == 1 ? silu(acc[0]) : acc[0];
+  if (NMAT == 2) {
+    const float gs = silu_f32(acc[0]);
+    y = a.y_bf16 ? bf16_to_float(float_to_bf16(gs)) *
+                       bf16_to_float(float_to_bf16(acc[NMAT - 1]))
+                 : gs * acc[NMAT - 1];
+  } else {
+    y = activate(acc[0], a.act);
+  }
   const bool owner = active && j == 15;
-  if (owner) a.y[row] = y;
+  if (owner) {
+    if (a.y_bf16)
+      ((uint16_t *)a.y)[row] = float_to_bf16(y);
+    else
+      ((float *)a.y)[row] = y;
+  }
 
   if (ARGMAX) {
-    unsigned long long key = owner ? argmax_key(y, row) : 0ull;
+    // the key of the value as stored
+    const float ys = a.y_bf16 ? bf16_to_float(float_to_bf16(y)) : y;
+    unsigned long long key = owner ? argmax_key(ys, row) : 0ull;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const unsigned long long other = __shfl_xor(key, off);
@@ -658,8 +687,8 @@ __global__ __launch_bounds__(1024) void argmax_reduce_kernel(
 __global__ void embedding_kernel(const int64_t *__restrict__ tokens,
                                  int64_t count, const uint8_t *__restrict__ t,
                                  int64_t rows, int64_t passes, int64_t chunks,
-                                 float *__restrict__ out, int64_t ldo,
-                                 int32_t *err, int aligned) {
+                                 void *__restrict__ out, int out_bf16,
+                                 int64_t ldo, int32_t *err, int aligned) {
   const int64_t c16 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t ti = blockIdx.y;
   if (c16 >= chunks || ti >= count) return;
@@ -686,7 +715,24 @@ __global__ void embedding_kernel(const int64_t *__restrict__ tokens,
     for (int e = 0; e < 16; ++e)
       v[e] = (float)(int8_t)(words[e >> 2] >> (8 * (e & 3))) * d;
   }
-  float *o = out + ti * ldo + c16 * 16;
+  if (out_bf16) {
+    // truncf to a bf16 result (LowerToLinalg.cpp:435-531)
+    uint16_t *o = (uint16_t *)out + ti * ldo + c16 * 16;
+    uint32_t p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      p[e] = (uint32_t)float_to_bf16(v[2 * e]) |
+             ((uint32_t)float_to_bf16(v[2 * e + 1]) << 16);
+    if (aligned) {
+      *(uint4 *)o = make_uint4(p[0], p[1], p[2], p[3]);
+      *(uint4 *)(o + 8) = make_uint4(p[4], p[5], p[6], p[7]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[e] = float_to_bf16(v[e]);
+    }
+    return;
+  }
+  float *o = (float *)out + ti * ldo + c16 * 16;
   if (aligned) {
 #pragma unroll
     for (int e = 0; e < 16; e += 4)
@@ -740,42 +786,42 @@ constexpr int ring_depth() {
   return PC > 0 ? (PC < dmax ? PC : dmax) : (NMAT == 2 ? 4 : 8);
 }
 
-template <int NMAT, int ACT, bool ARGMAX, int IN, int W, int PC>
+template <int NMAT, bool ARGMAX, int IN, int W, int PC>
 hipError_t launch_gemv_p(const GemvArgs &args, hipStream_t s) {
   constexpr int D = ring_depth<NMAT, IN, PC>();
   const unsigned grid = (unsigned)((args.groups + W - 1) / W);
   const size_t slots = PC > 0 ? row_slots(PC, W) : (size_t)args.passes * kPassBlocks;
   const size_t lds = IN == IN_WG ? slots * (kBlock + 4) : 0;
-  hipLaunchKernelGGL((gemv_kernel<NMAT, ACT, ARGMAX, IN, W, D, PC>),
+  hipLaunchKernelGGL((gemv_kernel<NMAT, ARGMAX, IN, W, D, PC>),
                      dim3(grid), dim3(64 * W), lds, s, args);
   return hipGetLastError();
 }
 
 // IN_WG takes its workgroup width from the pass count (wg_waves); IN_PRE
 // runs one wave per workgroup, or four for very wide outputs.
-template <int NMAT, int ACT, bool ARGMAX, int IN, int PC>
+template <int NMAT, bool ARGMAX, int IN, int PC>
 hipError_t launch_gemv_w(const GemvArgs &args, int waves, hipStream_t s) {
   if constexpr (IN == IN_WG) {
-    return launch_gemv_p<NMAT, ACT, ARGMAX, IN, wg_waves(NMAT, PC), PC>(args, s);
+    return launch_gemv_p<NMAT, ARGMAX, IN, wg_waves(NMAT, PC), PC>(args, s);
   } else {
-    if (waves == 4) return launch_gemv_p<NMAT, ACT, ARGMAX, IN, 4, PC>(args, s);
-    return launch_gemv_p<NMAT, ACT, ARGMAX, IN, 1, PC>(args, s);
+    if (waves == 4) return launch_gemv_p<NMAT, ARGMAX, IN, 4, PC>(args, s);
+    return launch_gemv_p<NMAT, ARGMAX, IN, 1, PC>(args, s);
   }
 }
 
 // Pass counts with a fully unrolled kernel: K = 512, 1024, 1536, 2560
 // (hidden size), 4096 and 9216 (the MLP down projection).  Others take the
 // runtime loop.
-template <int NMAT, int ACT, bool ARGMAX, int IN>
+template <int NMAT, bool ARGMAX, int IN>
 hipError_t launch_gemv_t(const GemvArgs &args, int waves, hipStream_t s) {
   switch (args.passes) {
-    case 1: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 1>(args, waves, s);
-    case 2: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 2>(args, waves, s);
-    case 3: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 3>(args, waves, s);
-    case 5: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 5>(args, waves, s);
-    case 8: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 8>(args, waves, s);
-    case 18: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 18>(args, waves, s);
-    default: return launch_gemv_w<NMAT, ACT, ARGMAX, IN, 0>(args, waves, s);
+    case 1: return launch_gemv_w<NMAT, ARGMAX, IN, 1>(args, waves, s);
+    case 2: return launch_gemv_w<NMAT, ARGMAX, IN, 2>(args, waves, s);
+    case 3: return launch_gemv_w<NMAT, ARGMAX, IN, 3>(args, waves, s);
+    case 5: return launch_gemv_w<NMAT, ARGMAX, IN, 5>(args, waves, s);
+    case 8: return launch_gemv_w<NMAT, ARGMAX, IN, 8>(args, waves, s);
+    case 18: return launch_gemv_w<NMAT, ARGMAX, IN, 18>(args, waves, s);
+    default: return launch_gemv_w<NMAT, ARGMAX, IN, 0>(args, waves, s);
   }
 }
 
@@ -829,16 +875,17 @@ hipError_t launch_selftest_quantizer(unsigned long long *bad, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_quantize(const float *x, int64_t m, int64_t ldx,
+hipError_t launch_quantize(const void *x, bool x_bf16, int64_t m, int64_t ldx,
                            int64_t cols, int8_t *qa, int64_t ldq, float *sa,
                            int64_t lds, int64_t blocks_pad, hipStream_t s) {
   const int64_t blocks = cols / kBlock;
   const int64_t threads = m * blocks_pad * 8;
+  const int64_t esz = x_bf16 ? 2 : 4;
   const int aligned =
-      ((uintptr_t)x % 16 == 0) && (ldx % 4 == 0) ? 1 : 0;
+      ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
   hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(threads, 256)), dim3(256),
-                     0, s, x, m, ldx, blocks, qa, ldq, sa, lds, blocks_pad,
-                     aligned);
+                     0, s, x, x_bf16 ? 1 : 0, m, ldx, blocks, qa, ldq, sa, lds,
+                     blocks_pad, aligned);
   return hipGetLastError();
 }
 
@@ -853,10 +900,9 @@ int64_t gemv_workgroups(int64_t rows) {
 template <int IN>
 static hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
                                  int waves, hipStream_t s) {
-  if (l.nmat == 2) return launch_gemv_t<2, 0, false, IN>(a, waves, s);
-  if (l.keys) return launch_gemv_t<1, 0, true, IN>(a, waves, s);
-  if (l.activation == 1) return launch_gemv_t<1, 1, false, IN>(a, waves, s);
-  return launch_gemv_t<1, 0, false, IN>(a, waves, s);
+  if (l.nmat == 2) return launch_gemv_t<2, false, IN>(a, waves, s);
+  if (l.keys) return launch_gemv_t<1, true, IN>(a, waves, s);
+  return launch_gemv_t<1, false, IN>(a, waves, s);
 }
 
 hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
@@ -871,8 +917,11 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
   a.groups = l.rows / kLanes;
   a.blocks = (int32_t)(l.cols / kBlock);
   a.passes = (int32_t)passes_for(l.cols);
+  a.act = l.activation;
+  a.x_bf16 = l.x_bf16 ? 1 : 0;
+  a.y_bf16 = l.y_bf16 ? 1 : 0;
   const int in = l.x ? IN_WG : IN_PRE;
-  if (l.x && (uintptr_t)l.x % 16) return hipErrorInvalidValue;
+  if (l.x && (uintptr_t)l.x % (l.x_bf16 ? 8 : 16)) return hipErrorInvalidValue;
   const int waves = gemv_waves(a.groups, a.passes, in, l.nmat);
   hipError_t e = in == IN_WG ? launch_gemv_in<IN_WG>(a, l, waves, s)
                              : launch_gemv_in<IN_PRE>(a, l, waves, s);
@@ -885,15 +934,18 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
 
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             const uint8_t *table, int64_t rows, int64_t cols,
-                            float *out, int64_t ldo, int32_t *err_flag,
-                            hipStream_t s) {
+                            void *out, bool out_bf16, int64_t ldo,
+                            int32_t *err_flag, hipStream_t s) {
   if (count == 0) return hipSuccess;
   const int64_t chunks = cols / 16;
-  const int aligned = ((uintptr_t)out % 16 == 0) && (ldo % 4 == 0) ? 1 : 0;
+  const int aligned = out_bf16
+      ? ((uintptr_t)out % 16 == 0) && (ldo % 8 == 0)
+      : ((uintptr_t)out % 16 == 0) && (ldo % 4 == 0);
   hipLaunchKernelGGL(embedding_kernel,
                      dim3(grid_for(chunks, 256), (unsigned)count), dim3(256),
                      0, s, tokens, count, table, rows, passes_for(cols),
-                     chunks, out, ldo, err_flag, aligned);
+                     chunks, out, out_bf16 ? 1 : 0, ldo, err_flag,
+                     aligned ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -119,9 +119,28 @@ int resolve_weight(llmcp_q8_ctx *ctx, const llmcp_memref_i8_1d *w,
   return LLMCP_Q8_OK;
 }
 
-bool dense_rows(const llmcp_memref_f32_2d *d) {
+template <class M>
+bool dense_rows(const M *d) {
   return d && d->data && d->strides[1] == 1 && d->sizes[0] >= 0 &&
          d->sizes[1] > 0 && (d->sizes[0] <= 1 || d->strides[0] >= d->sizes[1]);
+}
+
+// A row-major [rows, cols] activation view in device memory, f32 or bf16.
+struct Rows {
+  void *data = nullptr;
+  int64_t rows = 0, cols = 0, ld = 0;
+  bool bf16 = false;
+};
+
+template <class M>
+bool view_of(const M *d, bool bf16, Rows &r) {
+  if (!dense_rows(d)) return false;
+  r.data = (void *)(d->data + d->offset);
+  r.rows = d->sizes[0];
+  r.cols = d->sizes[1];
+  r.ld = d->sizes[0] <= 1 ? d->sizes[1] : d->strides[0];
+  r.bf16 = bf16;
+  return true;
 }
 
 template <typename T>
@@ -573,20 +592,21 @@ int llmcp_q8_upload_arena(llmcp_q8_ctx *ctx, const void *file,
 
 // One-row GEMV (decode, or prefill with M == 1).  Narrow outputs quantize
 // the input inside the GEMV; wide ones (lm_head) quantize it once first.
-static int gemv_common(llmcp_q8_ctx *ctx, const float *x, const Tensor *w0,
-                       const Tensor *w1, float *y, int activation,
+static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
+                       const Tensor *w1, const Rows &y, int activation,
                        int64_t *argmax_dev) {
   int rc = ensure_decode_scratch(ctx, w0->rows, w0->cols);
   if (rc) return rc;
   GemvLaunch l;
   const bool in_loop = gemv_quantizes_input(w0->rows, w1 ? 2 : 1) &&
-                       (uintptr_t)x % 16 == 0;
+                       (uintptr_t)x.data % (x.bf16 ? 8 : 16) == 0;
   if (in_loop) {
-    l.x = x;
+    l.x = x.data;
+    l.x_bf16 = x.bf16;
   } else {
     const int64_t nblk = passes_for(w0->cols) * kPassBlocks;
-    hipError_t e = launch_quantize(x, 1, w0->cols, w0->cols, ctx->qa,
-                                   nblk * kBlock, ctx->sa, nblk, nblk,
+    hipError_t e = launch_quantize(x.data, x.bf16, 1, w0->cols, w0->cols,
+                                   ctx->qa, nblk * kBlock, ctx->sa, nblk, nblk,
                                    ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
     l.qa = ctx->qa;
@@ -594,7 +614,8 @@ static int gemv_common(llmcp_q8_ctx *ctx, const float *x, const Tensor *w0,
   }
   l.w[0] = w0->dev;
   l.w[1] = w1 ? w1->dev : nullptr;
-  l.y = y;
+  l.y = y.data;
+  l.y_bf16 = y.bf16;
   l.rows = w0->rows;
   l.cols = w0->cols;
   l.nmat = w1 ? 2 : 1;
@@ -608,18 +629,16 @@ static int gemv_common(llmcp_q8_ctx *ctx, const float *x, const Tensor *w0,
   return LLMCP_Q8_OK;
 }
 
-// Prefill: quantize all M rows once (zero-padded to whole passes), then the
+// Prefill: quantize all M rows once (zero-padded to whole units), then the
 // int8-MFMA GEMM.  The activation scratch grows on first use for a larger M.
-static int gemm_common(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
-                       const Tensor *w, llmcp_memref_f32_2d *output,
-                       int activation) {
-  const int64_t m = input->sizes[0];
+static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
+                       const Rows &out, int activation) {
+  const int64_t m = in.rows;
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   int rc = ensure_scratch(ctx, (uint64_t)(m * nblk * kBlock),
                           (uint64_t)(m * nblk * 4));
   if (rc) return rc;
-  hipError_t e = launch_quantize(input->data + input->offset, m,
-                                 input->strides[0], w->cols, ctx->qa,
+  hipError_t e = launch_quantize(in.data, in.bf16, m, in.ld, w->cols, ctx->qa,
                                  nblk * kBlock, ctx->sa, nblk, nblk,
                                  ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "quantize launch");
@@ -632,8 +651,9 @@ static int gemm_common(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
   g.rows = w->rows;
   g.cols = w->cols;
   g.m = m;
-  g.y = output->data + output->offset;
-  g.ldy = output->strides[0];
+  g.y = out.data;
+  g.y_bf16 = out.bf16;
+  g.ldy = out.ld;
   g.activation = activation;
   g.fma = ctx->gemm_fma;
   e = launch_gemm(g, ctx->stream);
@@ -641,119 +661,116 @@ static int gemm_common(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
   return LLMCP_Q8_OK;
 }
 
-static int check_linear_shapes(const llmcp_memref_f32_2d *input,
-                               const Tensor *w, llmcp_memref_f32_2d *output) {
-  if (!dense_rows(input) || !dense_rows(output))
-    return fail(LLMCP_Q8_DECLINED, "activations must be row-major f32 memrefs");
-  if (input->sizes[1] != w->cols)
+static int check_linear_shapes(const Rows &in, const Tensor *w,
+                               const Rows &out) {
+  if (in.cols != w->cols)
     return fail(LLMCP_Q8_DECLINED, "input K %lld != weight K %lld",
-                (long long)input->sizes[1], (long long)w->cols);
-  if (output->sizes[1] != w->rows)
+                (long long)in.cols, (long long)w->cols);
+  if (out.cols != w->rows)
     return fail(LLMCP_Q8_DECLINED, "output N %lld != weight N %lld",
-                (long long)output->sizes[1], (long long)w->rows);
-  if (output->sizes[0] != input->sizes[0])
+                (long long)out.cols, (long long)w->rows);
+  if (out.rows != in.rows)
     return fail(LLMCP_Q8_DECLINED, "output outer dimension must match input");
   return LLMCP_Q8_OK;
 }
 
-int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
-                    const llmcp_memref_i8_1d *weight,
-                    llmcp_memref_f32_2d *output, int32_t activation,
-                    int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+static int check_mode(int32_t mode) {
+  if (mode != LLMCP_Q8_DECODE && mode != LLMCP_Q8_PREFILL)
+    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", mode);
+  return LLMCP_Q8_OK;
+}
+
+static const char *kDenseMsg = "activations must be row-major memrefs";
+
+static int linear_impl(llmcp_q8_ctx *ctx, const Rows &in,
+                       const llmcp_memref_i8_1d *weight, const Rows &out,
+                       int32_t activation, int32_t execution_mode) {
   const Tensor *w = nullptr;
   int rc = resolve_weight(ctx, weight, &w);
   if (rc) return rc;
-  rc = check_linear_shapes(input, w, output);
-  if (rc) return rc;
-  if (activation != LLMCP_Q8_ACT_NONE && activation != LLMCP_Q8_ACT_SILU)
+  if ((rc = check_linear_shapes(in, w, out))) return rc;
+  if (activation < LLMCP_Q8_ACT_NONE || activation > LLMCP_Q8_ACT_SOFTPLUS)
     return fail(LLMCP_Q8_DECLINED, "unsupported activation %d", activation);
-  const int64_t m = input->sizes[0];
+  if ((rc = check_mode(execution_mode))) return rc;
+  const int64_t m = in.rows;
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
-  if (execution_mode == LLMCP_Q8_DECODE) {
-    if (m != 1)
-      return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
-                  (long long)m);
-    return gemv_common(ctx, input->data + input->offset, w, nullptr,
-                       output->data + output->offset, activation, nullptr);
-  }
-  if (execution_mode != LLMCP_Q8_PREFILL)
-    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
-  if (m == 1)  // one row: the GEMV (scalar epilogue) beats a 1/128-full tile
-    return gemv_common(ctx, input->data + input->offset, w, nullptr,
-                       output->data + output->offset, activation, nullptr);
-  return gemm_common(ctx, input, w, output, activation);
+  if (execution_mode == LLMCP_Q8_DECODE && m != 1)
+    return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
+                (long long)m);
+  // One row (decode, or a one-row prefill such as the last-row lm_head):
+  // the GEMV (scalar epilogue) beats a 1/128-full GEMM tile.
+  if (m == 1) return gemv_common(ctx, in, w, nullptr, out, activation, nullptr);
+  return gemm_common(ctx, in, w, out, activation);
 }
 
-int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
-                    const llmcp_memref_i8_1d *w_gate,
-                    const llmcp_memref_i8_1d *w_up,
-                    llmcp_memref_f32_2d *output, int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
+                       const llmcp_memref_i8_1d *w_gate,
+                       const llmcp_memref_i8_1d *w_up, const Rows &out,
+                       int32_t execution_mode) {
   const Tensor *wg = nullptr, *wu = nullptr;
   int rc = resolve_weight(ctx, w_gate, &wg);
   if (rc) return rc;
   if ((rc = resolve_weight(ctx, w_up, &wu))) return rc;
   if (wg->rows != wu->rows || wg->cols != wu->cols)
     return fail(LLMCP_Q8_DECLINED, "gate and up weights differ in shape");
-  if ((rc = check_linear_shapes(input, wg, output))) return rc;
-  const int64_t m = input->sizes[0];
+  if ((rc = check_linear_shapes(in, wg, out))) return rc;
+  if ((rc = check_mode(execution_mode))) return rc;
+  const int64_t m = in.rows;
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
-  if (execution_mode != LLMCP_Q8_DECODE && execution_mode != LLMCP_Q8_PREFILL)
-    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
-  if (m != 1) {
-    // Prefill: gate GEMM with SiLU into the output, up GEMM into scratch,
-    // then h = gate * up (MulOpLowering, LowerToLinalg.cpp:377-393).
-    if (output->strides[0] != wg->rows)
-      return fail(LLMCP_Q8_DECLINED, "prefill SwiGLU output must be dense");
-    rc = grow(ctx, ctx->up, ctx->up_bytes, (uint64_t)(m * wg->rows * 4),
-              "prefill up scratch");
-    if (rc) return rc;
-    rc = gemm_common(ctx, input, wg, output, LLMCP_Q8_ACT_SILU);
-    if (rc) return rc;
-    llmcp_memref_f32_2d up = *output;
-    up.base = up.data = ctx->up;
-    up.offset = 0;
-    rc = gemm_common(ctx, input, wu, &up, LLMCP_Q8_ACT_NONE);
-    if (rc) return rc;
-    hipError_t e = launch_mul(output->data + output->offset, ctx->up,
-                              m * wg->rows, ctx->stream);
-    if (e != hipSuccess) return hip_fail(e, "mul launch");
-    return LLMCP_Q8_OK;
+  if (m == 1) return gemv_common(ctx, in, wg, wu, out, LLMCP_Q8_ACT_NONE, nullptr);
+  if (execution_mode == LLMCP_Q8_DECODE)
+    return fail(LLMCP_Q8_DECLINED, "decode SwiGLU requires M == 1");
+  // Prefill: gate GEMM with SiLU, up GEMM, then the multiply
+  // (MulOpLowering, LowerToLinalg.cpp:377-393).  f32: gate straight into
+  // the output, up into scratch.  bf16: both in f32 scratch, the multiply
+  // rounds each to bf16 first.
+  if (out.ld != wg->rows)
+    return fail(LLMCP_Q8_DECLINED, "prefill SwiGLU output must be dense");
+  const uint64_t n = (uint64_t)(m * wg->rows);
+  rc = grow(ctx, ctx->up, ctx->up_bytes, (out.bf16 ? 2 : 1) * n * 4,
+            "prefill SwiGLU scratch");
+  if (rc) return rc;
+  Rows g = out, u = out;
+  u.data = ctx->up;
+  u.bf16 = false;
+  u.ld = wg->rows;
+  if (out.bf16) {
+    g = u;
+    g.data = ctx->up + n;
   }
-  return gemv_common(ctx, input->data + input->offset, wg, wu,
-                     output->data + output->offset, LLMCP_Q8_ACT_NONE, nullptr);
+  if ((rc = gemm_common(ctx, in, wg, g, LLMCP_Q8_ACT_SILU))) return rc;
+  if ((rc = gemm_common(ctx, in, wu, u, LLMCP_Q8_ACT_NONE))) return rc;
+  hipError_t e = launch_mul((float *)g.data, (const float *)u.data,
+                            out.bf16 ? (uint16_t *)out.data : nullptr,
+                            (int64_t)n, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "mul launch");
+  return LLMCP_Q8_OK;
 }
 
-int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
-                     const llmcp_memref_i8_1d *table,
-                     llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
-                     int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+static int lm_head_impl(llmcp_q8_ctx *ctx, const Rows &in,
+                        const llmcp_memref_i8_1d *table, const Rows &logits,
+                        int64_t *argmax_dev, int32_t execution_mode) {
   const Tensor *w = nullptr;
   int rc = resolve_weight(ctx, table, &w);
   if (rc) return rc;
-  if ((rc = check_linear_shapes(hidden, w, logits))) return rc;
-  const int64_t m = hidden->sizes[0];
+  if ((rc = check_linear_shapes(in, w, logits))) return rc;
+  if ((rc = check_mode(execution_mode))) return rc;
+  const int64_t m = in.rows;
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
-  if (execution_mode != LLMCP_Q8_DECODE && execution_mode != LLMCP_Q8_PREFILL)
-    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
   if (m != 1)
     return fail(LLMCP_Q8_DECLINED, "lm_head for M > 1 not available");
-  return gemv_common(ctx, hidden->data + hidden->offset, w, nullptr,
-                     logits->data + logits->offset, LLMCP_Q8_ACT_NONE,
+  return gemv_common(ctx, in, w, nullptr, logits, LLMCP_Q8_ACT_NONE,
                      argmax_dev);
 }
 
-int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
-                 const llmcp_memref_i8_1d *w_gate,
-                 const llmcp_memref_i8_1d *w_up,
-                 const llmcp_memref_i8_1d *w_down, llmcp_memref_f32_2d *hidden,
-                 llmcp_memref_f32_2d *output, int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+static int mlp_impl(llmcp_q8_ctx *ctx, const Rows &in,
+                    const llmcp_memref_i8_1d *w_gate,
+                    const llmcp_memref_i8_1d *w_up,
+                    const llmcp_memref_i8_1d *w_down, const Rows *hidden,
+                    const Rows &out, int32_t execution_mode) {
   const Tensor *wg = nullptr, *wu = nullptr, *wd = nullptr;
   int rc = resolve_weight(ctx, w_gate, &wg);
   if (!rc) rc = resolve_weight(ctx, w_up, &wu);
@@ -764,51 +781,169 @@ int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
     return fail(LLMCP_Q8_DECLINED, "gate/up [F,H] and down [H,F] shapes differ");
   if (wg->rows % kBlock)
     return fail(LLMCP_Q8_DECLINED, "MLP width must be a multiple of 32");
-  if (!dense_rows(input) || !dense_rows(output) || input->sizes[1] != wg->cols ||
-      output->sizes[1] != wd->rows || output->sizes[0] != input->sizes[0])
+  if (in.cols != wg->cols || out.cols != wd->rows || out.rows != in.rows)
     return fail(LLMCP_Q8_DECLINED, "MLP input/output must be [M, H] row-major");
-  if (hidden && (!dense_rows(hidden) || hidden->sizes[1] != wg->rows ||
-                 hidden->sizes[0] != input->sizes[0]))
+  if (hidden && (hidden->cols != wg->rows || hidden->rows != in.rows))
     return fail(LLMCP_Q8_DECLINED, "MLP hidden must be [M, F] row-major");
-  if (execution_mode != LLMCP_Q8_DECODE && execution_mode != LLMCP_Q8_PREFILL)
-    return fail(LLMCP_Q8_EINVAL, "unknown execution mode %d", execution_mode);
-  const int64_t m = input->sizes[0];
+  if ((rc = check_mode(execution_mode))) return rc;
+  const int64_t m = in.rows;
   if (m == 0) return LLMCP_Q8_OK;
   if (m != 1) return fail(LLMCP_Q8_DECLINED, "fused MLP needs M == 1");
   if ((rc = set_device(ctx))) return rc;
   if ((rc = ensure_decode_scratch(ctx, wg->rows, wg->cols))) return rc;
-  // Gate/up with the SwiGLU epilogue into h (f32), then the down GEMV,
-  // which quantizes h per workgroup (Q8Decode.cpp:83-120) as its input.
-  float *h = hidden ? hidden->data + hidden->offset : ctx->hf;
-  rc = gemv_common(ctx, input->data + input->offset, wg, wu, h,
-                   LLMCP_Q8_ACT_NONE, nullptr);
+  // Gate/up with the SwiGLU epilogue into h, then the down GEMV, which
+  // quantizes h per workgroup (Q8Decode.cpp:83-120) as its input.  h has
+  // the output's element type unless the caller passes its own buffer.
+  Rows h;
+  if (hidden) {
+    h = *hidden;
+  } else {
+    h.data = ctx->hf;
+    h.rows = 1;
+    h.cols = h.ld = wg->rows;
+    h.bf16 = out.bf16;
+  }
+  rc = gemv_common(ctx, in, wg, wu, h, LLMCP_Q8_ACT_NONE, nullptr);
   if (rc) return rc;
-  return gemv_common(ctx, h, wd, nullptr, output->data + output->offset,
-                     LLMCP_Q8_ACT_NONE, nullptr);
+  return gemv_common(ctx, h, wd, nullptr, out, LLMCP_Q8_ACT_NONE, nullptr);
 }
 
-int llmcp_q8_embedding(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
-                       const llmcp_memref_i8_1d *table,
-                       llmcp_memref_f32_2d *output) {
-  if (!ctx || !tokens || !output) return fail(LLMCP_Q8_EINVAL, "null argument");
+static int embedding_impl(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
+                          const llmcp_memref_i8_1d *table, const Rows &out) {
   const Tensor *w = nullptr;
   int rc = resolve_weight(ctx, table, &w);
   if (rc) return rc;
   if (tokens->strides[0] != 1 && tokens->sizes[0] > 1)
     return fail(LLMCP_Q8_DECLINED, "tokens must be contiguous");
-  if (!dense_rows(output) || output->sizes[1] != w->cols ||
-      output->sizes[0] != tokens->sizes[0])
+  if (out.cols != w->cols || out.rows != tokens->sizes[0])
     return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
   if (tokens->sizes[0] > 65535)
     return fail(LLMCP_Q8_DECLINED, "at most 65535 tokens per call");
   if ((rc = set_device(ctx))) return rc;
   hipError_t e = launch_embedding(tokens->data + tokens->offset,
                                   tokens->sizes[0], w->dev, w->rows, w->cols,
-                                  output->data + output->offset,
-                                  output->strides[0], ctx->err_flag,
+                                  out.data, out.bf16, out.ld, ctx->err_flag,
                                   ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
   return LLMCP_Q8_OK;
+}
+
+// ---- public entries: f32 and bf16 activations
+
+int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                    const llmcp_memref_i8_1d *weight,
+                    llmcp_memref_f32_2d *output, int32_t activation,
+                    int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  Rows in, out;
+  if (!view_of(input, false, in) || !view_of(output, false, out))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return linear_impl(ctx, in, weight, out, activation, execution_mode);
+}
+
+int llmcp_q8_linear_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                         const llmcp_memref_i8_1d *weight,
+                         llmcp_memref_bf16_2d *output, int32_t activation,
+                         int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  Rows in, out;
+  if (!view_of(input, true, in) || !view_of(output, true, out))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return linear_impl(ctx, in, weight, out, activation, execution_mode);
+}
+
+int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                    const llmcp_memref_i8_1d *w_gate,
+                    const llmcp_memref_i8_1d *w_up,
+                    llmcp_memref_f32_2d *output, int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  Rows in, out;
+  if (!view_of(input, false, in) || !view_of(output, false, out))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return swiglu_impl(ctx, in, w_gate, w_up, out, execution_mode);
+}
+
+int llmcp_q8_swiglu_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                         const llmcp_memref_i8_1d *w_gate,
+                         const llmcp_memref_i8_1d *w_up,
+                         llmcp_memref_bf16_2d *output, int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  Rows in, out;
+  if (!view_of(input, true, in) || !view_of(output, true, out))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return swiglu_impl(ctx, in, w_gate, w_up, out, execution_mode);
+}
+
+int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
+                     const llmcp_memref_i8_1d *table,
+                     llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
+                     int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  Rows in, out;
+  if (!view_of(hidden, false, in) || !view_of(logits, false, out))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode);
+}
+
+int llmcp_q8_lm_head_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *hidden,
+                          const llmcp_memref_i8_1d *table,
+                          llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
+                          int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  Rows in, out;
+  if (!view_of(hidden, true, in) || !view_of(logits, false, out))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode);
+}
+
+int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                 const llmcp_memref_i8_1d *w_gate,
+                 const llmcp_memref_i8_1d *w_up,
+                 const llmcp_memref_i8_1d *w_down, llmcp_memref_f32_2d *hidden,
+                 llmcp_memref_f32_2d *output, int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  Rows in, out, h;
+  if (!view_of(input, false, in) || !view_of(output, false, out) ||
+      (hidden && !view_of(hidden, false, h)))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return mlp_impl(ctx, in, w_gate, w_up, w_down, hidden ? &h : nullptr, out,
+                  execution_mode);
+}
+
+int llmcp_q8_mlp_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                      const llmcp_memref_i8_1d *w_gate,
+                      const llmcp_memref_i8_1d *w_up,
+                      const llmcp_memref_i8_1d *w_down,
+                      llmcp_memref_bf16_2d *hidden,
+                      llmcp_memref_bf16_2d *output, int32_t execution_mode) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  Rows in, out, h;
+  if (!view_of(input, true, in) || !view_of(output, true, out) ||
+      (hidden && !view_of(hidden, true, h)))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return mlp_impl(ctx, in, w_gate, w_up, w_down, hidden ? &h : nullptr, out,
+                  execution_mode);
+}
+
+int llmcp_q8_embedding(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
+                       const llmcp_memref_i8_1d *table,
+                       llmcp_memref_f32_2d *output) {
+  if (!ctx || !tokens || !output) return fail(LLMCP_Q8_EINVAL, "null argument");
+  Rows out;
+  if (!view_of(output, false, out))
+    return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
+  return embedding_impl(ctx, tokens, table, out);
+}
+
+int llmcp_q8_embedding_bf16(llmcp_q8_ctx *ctx,
+                            const llmcp_memref_i64_1d *tokens,
+                            const llmcp_memref_i8_1d *table,
+                            llmcp_memref_bf16_2d *output) {
+  if (!ctx || !tokens || !output) return fail(LLMCP_Q8_EINVAL, "null argument");
+  Rows out;
+  if (!view_of(output, true, out))
+    return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
+  return embedding_impl(ctx, tokens, table, out);
 }
 
 int llmcp_q8_quantize_activations(llmcp_q8_ctx *ctx,
@@ -821,7 +956,7 @@ int llmcp_q8_quantize_activations(llmcp_q8_ctx *ctx,
   if (rc) return rc;
   const int64_t m = input->sizes[0], k = input->sizes[1];
   if (m == 0) return LLMCP_Q8_OK;
-  hipError_t e = launch_quantize(input->data + input->offset, m,
+  hipError_t e = launch_quantize(input->data + input->offset, false, m,
                                  input->strides[0], k, qa_dev, k, sa_dev,
                                  k / kBlock, k / kBlock, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "quantize launch");
@@ -841,7 +976,7 @@ int llmcp_q8_block_dots(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = ensure_scratch(ctx, (uint64_t)(m * k), (uint64_t)(m * b * 4))))
     return rc;
-  hipError_t e = launch_quantize(input->data + input->offset, m,
+  hipError_t e = launch_quantize(input->data + input->offset, false, m,
                                  input->strides[0], k, ctx->qa, k, ctx->sa, b,
                                  b, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "quantize launch");
@@ -1020,6 +1155,44 @@ int32_t _mlir_ciface_llmcp_q8_embedding(llmcp_memref_i64_1d *tokens,
                                         llmcp_memref_f32_2d *output) {
   if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
   return llmcp_q8_embedding(g_default_ctx, tokens, table, output);
+}
+
+int32_t _mlir_ciface_llmcp_q8_linear_bf16(llmcp_memref_bf16_2d *input,
+                                          llmcp_memref_i8_1d *weight,
+                                          llmcp_memref_bf16_2d *output,
+                                          int32_t activation,
+                                          int32_t execution_mode) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  return llmcp_q8_linear_bf16(g_default_ctx, input, weight, output, activation,
+                              execution_mode);
+}
+
+int32_t _mlir_ciface_llmcp_q8_swiglu_bf16(llmcp_memref_bf16_2d *input,
+                                          llmcp_memref_i8_1d *w_gate,
+                                          llmcp_memref_i8_1d *w_up,
+                                          llmcp_memref_bf16_2d *output,
+                                          int32_t execution_mode) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  return llmcp_q8_swiglu_bf16(g_default_ctx, input, w_gate, w_up, output,
+                              execution_mode);
+}
+
+int32_t _mlir_ciface_llmcp_q8_lm_head_bf16(llmcp_memref_bf16_2d *hidden,
+                                           llmcp_memref_i8_1d *table,
+                                           llmcp_memref_f32_2d *logits,
+                                           llmcp_memref_i64_1d *argmax,
+                                           int32_t execution_mode) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  int64_t *am = argmax ? argmax->data + argmax->offset : nullptr;
+  return llmcp_q8_lm_head_bf16(g_default_ctx, hidden, table, logits, am,
+                               execution_mode);
+}
+
+int32_t _mlir_ciface_llmcp_q8_embedding_bf16(llmcp_memref_i64_1d *tokens,
+                                             llmcp_memref_i8_1d *table,
+                                             llmcp_memref_bf16_2d *output) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  return llmcp_q8_embedding_bf16(g_default_ctx, tokens, table, output);
 }
 
 // --------------------------------------------------- device plumbing --

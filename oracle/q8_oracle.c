@@ -26,7 +26,10 @@
  *   block_dots          brute-force int64 einsum.
  *   linear_*            exact-operand construction of run_numeric.py:690-732
  *                       against an float64 matmul at rel 1e-5 / abs 1e-6.
- *   silu                float64 silu within 1 ulp-level tolerance.
+ *   silu/sigmoid/       float64 closed forms within ulp-level tolerance
+ *   softplus            (softplus also against log1p(exp) at the overflow end).
+ *   f32_to_bf16         torch's float32 -> bfloat16 conversion (round to
+ *                       nearest even) on ties, subnormals, inf and NaN.
  *   argmax              numpy argmax (first maximum), std::max_element rule.
  *   embedding           exact dequantization from the unpacked matrix.
  */
@@ -272,19 +275,38 @@ void oracle_block_dots(const int8_t *qa, const uint8_t *p4, int64_t rows,
  * round once to f32, so the two agree bit for bit. */
 float oracle_expf(float x) { return (float)exp((double)x); }
 
-/* applyMatmulActivation (MatmulLoweringCommon.cpp:78-103):
- * silu(v) = v * (1 / (1 + exp(-v))); sigmoid = 1/(1+exp(-v)). */
-float oracle_silu(float v) {
+/* log1p for the softplus activation (math.log1p -> libm log1pf), evaluated
+ * in double and rounded once, like oracle_expf. */
+float oracle_log1pf(float x) { return (float)log1p((double)x); }
+
+/* applyMatmulActivation (MatmulLoweringCommon.cpp:78-103), one MLIR op at a
+ * time in f32: sigmoid = 1/(1+exp(-v)); silu(v) = v * sigmoid(v);
+ * softplus(v) = log1p(exp(v)). */
+float oracle_sigmoid(float v) {
   float e = oracle_expf(-v);
-  float sig = 1.0f / (1.0f + e);
+  return 1.0f / (1.0f + e);
+}
+
+float oracle_silu(float v) {
+  float sig = oracle_sigmoid(v);
   return v * sig;
 }
 
-enum { ACT_NONE = 0, ACT_SILU = 1 };
+float oracle_softplus(float v) {
+  float e = oracle_expf(v);
+  return oracle_log1pf(e);
+}
+
+enum { ACT_NONE = 0, ACT_SILU = 1, ACT_SIGMOID = 2, ACT_SOFTPLUS = 3 };
 enum { EPI_SCALAR = 0, EPI_FMA = 1 };
 
 static float activate(float v, int act) {
-  return act == ACT_SILU ? oracle_silu(v) : v;
+  switch (act) {
+    case ACT_SILU: return oracle_silu(v);
+    case ACT_SIGMOID: return oracle_sigmoid(v);
+    case ACT_SOFTPLUS: return oracle_softplus(v);
+    default: return v;
+  }
 }
 
 /* One output element over all blocks, in block order b = 0..B-1.

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(HERE, "libq8oracle.so")
 
 QK = 32
 RECORD = 136
-ACT = {"none": 0, "silu": 1}
+ACT = {"none": 0, "silu": 1, "sigmoid": 2, "softplus": 3}
 EPI = {"scalar": 0, "fma": 1}
 
 _lib = None
@@ -61,8 +61,9 @@ def _declare(L):
     L.oracle_block_dots.argtypes = [P, P, I64, I64, I64, P]
     L.oracle_expf.restype = ctypes.c_float
     L.oracle_expf.argtypes = [ctypes.c_float]
-    L.oracle_silu.restype = ctypes.c_float
-    L.oracle_silu.argtypes = [ctypes.c_float]
+    for name in ("oracle_silu", "oracle_sigmoid", "oracle_softplus"):
+        getattr(L, name).restype = ctypes.c_float
+        getattr(L, name).argtypes = [ctypes.c_float]
     L.oracle_linear.argtypes = [P, P, I64, I64, I64, I, I, P]
     L.oracle_linear_colpar.argtypes = [P, P, I64, I64, I64, I, I, P]
     L.oracle_swiglu.argtypes = [P, P, P, I64, I64, I64, I, P, I]
@@ -155,10 +156,35 @@ def block_dots(qa, p4, n):
     return out
 
 
-def silu(v):
-    f = lib().oracle_silu
+def _scalar_map(name, v):
+    f = getattr(lib(), name)
     v = _c(np.atleast_1d(v), np.float32)
     return np.array([f(float(a)) for a in v.ravel()], np.float32).reshape(v.shape)
+
+
+def silu(v):
+    return _scalar_map("oracle_silu", v)
+
+
+def sigmoid(v):
+    return _scalar_map("oracle_sigmoid", v)
+
+
+def softplus(v):
+    return _scalar_map("oracle_softplus", v)
+
+
+def f32_to_bf16_bits(v):
+    """Round to nearest even f32 -> bf16 (raw uint16 bits)."""
+    f = lib().oracle_f32_to_bf16
+    v = _c(np.atleast_1d(v), np.float32)
+    return np.array([f(float(a)) for a in v.ravel()], np.uint16).reshape(v.shape)
+
+
+def bf16_bits_to_f32(b):
+    """Exact bf16 -> f32 widening of raw uint16 bits."""
+    b = np.asarray(b, np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
 
 
 def linear(x, p4, n, activation="none", epilogue="scalar", colpar=False):

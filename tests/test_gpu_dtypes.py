@@ -1,0 +1,163 @@
+"""GPU parity of the linear activations (none, silu, sigmoid, softplus --
+LLMCPOps.cpp:74-77) and of bf16 activations in and out (the hook's
+f32|bf16 tensors, Q8Decode.cpp:97-98 widening, :126-127 truncf) against the
+CPU oracle, bit for bit.  bf16 references: the f32 oracle result on the
+exactly widened input, rounded to bf16 (round to nearest even)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def bits_equal(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    if a.dtype == np.uint16 or b.dtype == np.uint16:
+        return np.array_equal(a.astype(np.uint16), b.astype(np.uint16))
+    return np.array_equal(a.astype(np.float32).view(np.uint32),
+                          b.astype(np.float32).view(np.uint32))
+
+
+def weights(rng, n, k, scale=0.02):
+    return (rng.standard_normal((n, k)) * scale).astype(np.float32)
+
+
+def to_bf16(oracle, x):
+    return oracle.f32_to_bf16_bits(np.asarray(x, np.float32))
+
+
+@pytest.mark.parametrize("act", ["none", "silu", "sigmoid", "softplus"])
+@pytest.mark.parametrize("m", [1, 40])
+def test_linear_activations(ctx, oracle, act, m):
+    rng = np.random.default_rng(300 + m)
+    n, k = 264, 1056
+    w = weights(rng, n, k, 0.2)  # outputs of a few units: both tails of each act
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    p4 = oracle.pack_q8_0_p4(w)
+    t = ctx.upload_p4(p4, n, k)
+    xd, yd = ctx.to_device(x), ctx.alloc(m * n * 4)
+    mode = "decode" if m == 1 else "prefill"
+    ctx.linear(xd, t, yd, m, activation=act, mode=mode)
+    y = ctx.to_host(yd, (m, n), np.float32)
+    epi = "scalar" if m == 1 else "fma"  # GEMV: scalar path; GEMM: default fma
+    assert bits_equal(y, oracle.linear(x, p4, n, activation=act, epilogue=epi))
+    ctx.release(t)
+
+
+@pytest.mark.parametrize("m,k,act", [(1, 2560, "none"), (1, 9216, "silu"),
+                                     (1, 1056, "softplus"), (37, 2560, "none"),
+                                     (64, 1056, "sigmoid")])
+def test_linear_bf16(ctx, oracle, m, k, act):
+    rng = np.random.default_rng(310 + m + k)
+    n = 264
+    w = weights(rng, n, k)
+    xb = to_bf16(oracle, rng.standard_normal((m, k)))
+    p4 = oracle.pack_q8_0_p4(w)
+    t = ctx.upload_p4(p4, n, k)
+    xd, yd = ctx.to_device(xb), ctx.alloc(m * n * 2)
+    mode = "decode" if m == 1 else "prefill"
+    ctx.linear(xd, t, yd, m, activation=act, mode=mode, dtype="bf16")
+    y = ctx.to_host(yd, (m, n), np.uint16)
+    epi = "scalar" if m == 1 else "fma"
+    ref = oracle.linear(oracle.bf16_bits_to_f32(xb), p4, n, activation=act,
+                        epilogue=epi)
+    assert bits_equal(y, to_bf16(oracle, ref))
+    ctx.release(t)
+
+
+def test_linear_bf16_misaligned_row(ctx, oracle):
+    # a row that is not 8-byte aligned takes the separate quantize kernel
+    rng = np.random.default_rng(320)
+    n, k = 136, 2560
+    w = weights(rng, n, k)
+    xb = to_bf16(oracle, rng.standard_normal((1, k)))
+    p4 = oracle.pack_q8_0_p4(w)
+    t = ctx.upload_p4(p4, n, k)
+    buf = ctx.alloc(k * 2 + 64)
+    from llmcp_amd import lib
+    lib().llmcp_q8_memcpy_h2d(ctx.handle, buf.ptr + 2, xb.ctypes.data, k * 2)
+    yd = ctx.alloc(n * 2)
+    ctx.linear(buf.ptr + 2, t, yd, 1, dtype="bf16")
+    y = ctx.to_host(yd, (1, n), np.uint16)
+    ref = oracle.linear(oracle.bf16_bits_to_f32(xb), p4, n)
+    assert bits_equal(y, to_bf16(oracle, ref))
+    ctx.release(t)
+
+
+def swiglu_ref_bf16(oracle, xf, p4g, p4u, n):
+    g = to_bf16(oracle, oracle.linear(xf, p4g, n, activation="silu",
+                                      epilogue="scalar" if xf.shape[0] == 1 else "fma"))
+    u = to_bf16(oracle, oracle.linear(xf, p4u, n,
+                                      epilogue="scalar" if xf.shape[0] == 1 else "fma"))
+    prod = oracle.bf16_bits_to_f32(g) * oracle.bf16_bits_to_f32(u)  # exact in f32
+    return to_bf16(oracle, prod)
+
+
+@pytest.mark.parametrize("m", [1, 33])
+def test_swiglu_bf16(ctx, oracle, m):
+    rng = np.random.default_rng(330 + m)
+    n, k = 1056, 2560
+    wg, wu = weights(rng, n, k, 0.05), weights(rng, n, k, 0.05)
+    xb = to_bf16(oracle, rng.standard_normal((m, k)))
+    p4g, p4u = oracle.pack_q8_0_p4(wg), oracle.pack_q8_0_p4(wu)
+    tg, tu = ctx.upload_p4(p4g, n, k), ctx.upload_p4(p4u, n, k)
+    xd, hd = ctx.to_device(xb), ctx.alloc(m * n * 2)
+    ctx.swiglu(xd, tg, tu, hd, m, mode="decode" if m == 1 else "prefill", dtype="bf16")
+    h = ctx.to_host(hd, (m, n), np.uint16)
+    assert bits_equal(h, swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb), p4g, p4u, n))
+    ctx.release(tg)
+    ctx.release(tu)
+
+
+def test_mlp_bf16(ctx, oracle):
+    rng = np.random.default_rng(340)
+    hdim, f = 512, 1056
+    wg, wu, wd = weights(rng, f, hdim, 0.05), weights(rng, f, hdim, 0.05), weights(rng, hdim, f)
+    xb = to_bf16(oracle, rng.standard_normal((1, hdim)))
+    p4g, p4u, p4d = (oracle.pack_q8_0_p4(w) for w in (wg, wu, wd))
+    tg, tu, td = ctx.upload_p4(p4g, f, hdim), ctx.upload_p4(p4u, f, hdim), ctx.upload_p4(p4d, hdim, f)
+    xd, hd, yd = ctx.to_device(xb), ctx.alloc(f * 2), ctx.alloc(hdim * 2)
+    ctx.mlp(xd, tg, tu, td, yd, h=hd, dtype="bf16")
+    h = ctx.to_host(hd, (1, f), np.uint16)
+    y = ctx.to_host(yd, (1, hdim), np.uint16)
+    href = swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb), p4g, p4u, f)
+    assert bits_equal(h, href)
+    yref = to_bf16(oracle, oracle.linear(oracle.bf16_bits_to_f32(href), p4d, hdim))
+    assert bits_equal(y, yref)
+    # without a caller buffer for h the result is the same
+    y2d = ctx.alloc(hdim * 2)
+    ctx.mlp(xd, tg, tu, td, y2d, dtype="bf16")
+    assert bits_equal(ctx.to_host(y2d, (1, hdim), np.uint16), yref)
+    for t in (tg, tu, td):
+        ctx.release(t)
+
+
+def test_lm_head_bf16_hidden(ctx, oracle):
+    rng = np.random.default_rng(350)
+    v, k = 16384, 2560
+    w = weights(rng, v, k)
+    xb = to_bf16(oracle, rng.standard_normal((1, k)))
+    p4 = oracle.pack_q8_0_p4(w)
+    t = ctx.upload_p4(p4, v, k)
+    xd, ld, am = ctx.to_device(xb), ctx.alloc(v * 4), ctx.alloc(8)
+    ctx.lm_head(xd, t, ld, 1, argmax=am, dtype="bf16")
+    logits = ctx.to_host(ld, (1, v), np.float32)
+    ref = oracle.linear(oracle.bf16_bits_to_f32(xb), p4, v)
+    assert bits_equal(logits, ref)
+    assert int(ctx.to_host(am, (1,), np.int64)[0]) == oracle.argmax(ref[0])
+    ctx.release(t)
+
+
+@pytest.mark.parametrize("k", [2560, 9216])
+def test_embedding_bf16(ctx, oracle, k):
+    rng = np.random.default_rng(360 + k)
+    v = 1024
+    w = weights(rng, v, k)
+    p4 = oracle.pack_q8_0_p4(w)
+    t = ctx.upload_p4(p4, v, k)
+    tokens = rng.integers(0, v, 300).astype(np.int64)
+    td, od = ctx.to_device(tokens), ctx.alloc(tokens.size * k * 2)
+    ctx.embedding(td, tokens.size, t, od, dtype="bf16")
+    out = ctx.to_host(od, (tokens.size, k), np.uint16)
+    assert bits_equal(out, to_bf16(oracle, oracle.embedding(tokens, p4, k)))
+    assert ctx.check_flag() == 0
+    ctx.release(t)

@@ -346,3 +346,42 @@ def test_golden_small_case_regression(oracle):
     n = z["w"].shape[0]
     assert np.array_equal(oracle.linear(z["x"], z["p4"], n), z["y_scalar"])
     assert np.array_equal(oracle.linear(z["x"], z["p4"], n, epilogue="fma"), z["y_fma"])
+
+
+def test_f32_to_bf16_matches_torch(oracle):
+    # arith.truncf f32 -> bf16 is round to nearest, ties to even; torch's
+    # float32 -> bfloat16 conversion is the independent restatement.
+    import torch
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    # exact ties (low 16 bits 0x8000) with even and odd kept parts
+    ties = (rng.integers(0, 2**16, 20000, dtype=np.uint32) << 16) | 0x8000
+    special = np.array([0x00000000, 0x80000000, 0x7f800000, 0xff800000,
+                        0x00000001, 0x007fffff, 0x3f808000, 0x3f818000,
+                        0x7f7fffff, 0x7f7f8000, 0x3f7fffff], np.uint32)
+    allb = np.concatenate([bits, ties, special])
+    x = allb.view(np.float32)
+    finite = np.isfinite(x) | np.isinf(x)
+    got = oracle.f32_to_bf16_bits(x[finite])
+    ref = torch.from_numpy(x[finite].copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    # NaN stays NaN (quiet)
+    nan = oracle.f32_to_bf16_bits(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7f80) == 0x7f80 and (nan & 0x007f) != 0
+
+
+def test_activations_closed_form(oracle):
+    # applyMatmulActivation (MatmulLoweringCommon.cpp:78-103) against float64
+    # closed forms; f32 intermediate roundings keep them within a few ulp.
+    v = np.concatenate([np.linspace(-30, 30, 6001), [-1e-3, 1e-3, 0.0]]).astype(np.float32)
+    d = v.astype(np.float64)
+    sig = oracle.sigmoid(v)
+    assert np.allclose(sig, 1.0 / (1.0 + np.exp(-d)), rtol=4e-7, atol=1e-30)
+    silu = oracle.silu(v)
+    assert np.array_equal(silu, (v * sig).astype(np.float32))  # v * sigmoid(v)
+    sp = oracle.softplus(v)
+    assert np.allclose(sp, np.log1p(np.exp(d)), rtol=4e-7, atol=1e-30)
+    # softplus overflows where f32 exp does (exp(89) = inf), like the
+    # reference's log1p(exp(v)) on f32
+    assert np.isinf(oracle.softplus(np.array([89.0], np.float32))[0])
+    assert oracle.softplus(np.array([88.0], np.float32))[0] == np.float32(np.log1p(np.float32(np.exp(88.0))))
