@@ -28,7 +28,8 @@ COMMON = [
 
 
 def build(verbose=False):
-    objs = []
+    # the sources compile independently: run the compilers side by side
+    objs, procs = [], []
     for src in SOURCES:
         path = os.path.join(CSRC, src)
         if not os.path.exists(path):
@@ -39,8 +40,11 @@ def build(verbose=False):
             cmd = [HIPCC] + COMMON + ["-fopenmp", "-x", "hip", "-c", path, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True)
+        procs.append((src, subprocess.Popen(cmd)))
         objs.append(obj)
+    failed = [src for src, p in procs if p.wait() != 0]
+    if failed:
+        raise subprocess.CalledProcessError(1, "hipcc " + " ".join(failed))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fopenmp", "-o", tmp] + objs
     if verbose:

@@ -37,12 +37,14 @@ constexpr int ROW = SB * kBlock + 16;  // LDS row stride (bytes), padded
 // outer product (one exact product, one rounding -- the same value as the
 // VALU multiply) whose output layout is the int8 MFMA's, leaving two VALU
 // ops per element and block.
-template <int WM, int WN, int TM, int TN, bool FMA, int SEG>
+// EPI: activation code in bits 0-1, bf16 output in bit 2 (compile time:
+// the epilogue is inlined for every accumulator element).
+template <int WM, int WN, int TM, int TN, bool FMA, int SEG, int EPI>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
     const int8_t *__restrict__ qa, int64_t ldq, const float *__restrict__ sa,
     int64_t lds, const uint8_t *__restrict__ w, int64_t n_rows, int64_t m_rows,
     int32_t passes, int32_t m_tiles, int32_t n_tiles, void *__restrict__ y,
-    int64_t ldy, int act, int y_bf16) {
+    int64_t ldy) {
   constexpr int NT = 64 * WM * WN;
   constexpr int BM = 32 * WM * TM;
   constexpr int BN = 32 * WN * TN;
@@ -241,8 +243,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(
       for (int v = 0; v < 16; ++v) {
         const int64_t m = m0 + mrow + 32 * tm + 8 * (v >> 2) + 4 * lh + (v & 3);
         if (m < m_rows && n < n_rows) {
-          const float o = activate(acc[tm][tn][v], act);
-          if (y_bf16)
+          const float o = activate(acc[tm][tn][v], EPI & 3);
+          if constexpr ((EPI & 4) != 0)
             ((uint16_t *)y)[m * ldy + n] = float_to_bf16(o);
           else
             ((float *)y)[m * ldy + n] = o;
@@ -277,6 +279,29 @@ hipError_t launch_mul(float *g, const float *u, uint16_t *out_bf16,
   return hipGetLastError();
 }
 
+template <int WM, int WN, int TM, int TN, bool FMA, int SEG, int EPI>
+static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
+                          int32_t n_tiles, unsigned grid, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, SEG, EPI>), dim3(grid),
+                     dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
+                     l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+}
+
+template <int WM, int WN, int TM, int TN, bool FMA, int SEG>
+static void launch_gemm_a(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
+                          int32_t n_tiles, unsigned grid, hipStream_t s) {
+  // activation and output type are template arguments: inlined for every
+  // accumulator element, runtime switches bloat the kernel and slow it
+#define LLMCP_GEMM_EPI(E) \
+  case E: return launch_gemm_k<WM, WN, TM, TN, FMA, SEG, E>(l, passes, m_tiles, n_tiles, grid, s);
+  switch ((l.activation & 3) | (l.y_bf16 ? 4 : 0)) {
+    LLMCP_GEMM_EPI(1) LLMCP_GEMM_EPI(2) LLMCP_GEMM_EPI(3) LLMCP_GEMM_EPI(4)
+    LLMCP_GEMM_EPI(5) LLMCP_GEMM_EPI(6) LLMCP_GEMM_EPI(7)
+    default: return launch_gemm_k<WM, WN, TM, TN, FMA, SEG, 0>(l, passes, m_tiles, n_tiles, grid, s);
+  }
+#undef LLMCP_GEMM_EPI
+}
+
 template <int WM, int WN, int TM, int TN, bool FMA>
 static hipError_t launch_gemm_t(const GemmLaunch &l, hipStream_t s) {
   constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
@@ -287,23 +312,9 @@ static hipError_t launch_gemm_t(const GemmLaunch &l, hipStream_t s) {
   const unsigned grid = (unsigned)(n_tiles8 * m_tiles);
   // the weight's unit layout is fixed at registration (seg_for)
   switch (seg_for(passes)) {
-    case 6:
-      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, 6>), dim3(grid),
-                         dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
-                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
-                         l.activation, l.y_bf16 ? 1 : 0);
-      break;
-    case 4:
-      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, 4>), dim3(grid),
-                         dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
-                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
-                         l.activation, l.y_bf16 ? 1 : 0);
-      break;
-    default:
-      hipLaunchKernelGGL((gemm_kernel<WM, WN, TM, TN, FMA, 1>), dim3(grid),
-                         dim3(64 * WM * WN), 0, s, l.qa, l.ldq, l.sa, l.lds, l.w,
-                         l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
-                         l.activation, l.y_bf16 ? 1 : 0);
+    case 6: launch_gemm_a<WM, WN, TM, TN, FMA, 6>(l, passes, m_tiles, n_tiles, grid, s); break;
+    case 4: launch_gemm_a<WM, WN, TM, TN, FMA, 4>(l, passes, m_tiles, n_tiles, grid, s); break;
+    default: launch_gemm_a<WM, WN, TM, TN, FMA, 1>(l, passes, m_tiles, n_tiles, grid, s);
   }
   return hipGetLastError();
 }

@@ -288,8 +288,6 @@ struct GemvArgs {
   int32_t blocks;
   int32_t passes;
   int32_t act;       // llmcp_q8_activation (one-matrix GEMVs)
-  int32_t x_bf16;
-  int32_t y_bf16;
 };
 
 // Where the GEMV's input row comes from.
@@ -335,8 +333,13 @@ __host__ __device__ constexpr int row_slots(int pc, int w) {
 // Per pass, prepare() forms the 16 blocks' contributions and chain() adds
 // them in block order; the next pass's prepare() is scheduled together with
 // the current chain(), so the dots overlap the serial DPP additions.
-template <int NMAT, bool ARGMAX, int IN, int W, int D, int PC>
+// V packs the compile-time variant: bit 0 the input row is bf16 (IN_WG),
+// bit 1 the output is bf16, bit 2 a one-matrix GEMV applies a.act.
+template <int NMAT, bool ARGMAX, int IN, int W, int D, int PC, int V>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
+  constexpr bool XB = (V & 1) != 0;
+  constexpr bool YB = (V & 2) != 0;
+  constexpr bool ACTV = (V & 4) != 0;
   extern __shared__ __align__(16) unsigned char lds[];  // IN_WG input row
   __shared__ unsigned long long key_l[W];
   const int passes = PC > 0 ? PC : a.passes;
@@ -371,7 +374,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
       const int t = u * 64 * W + (int)threadIdx.x;
       xr[u] = make_uint4(0, 0, 0, 0);
       if ((t >> 3) < a.blocks) {
-        if (a.x_bf16) {
+        if constexpr (XB) {
           const uint2 w2 = *(const uint2 *)((const uint16_t *)a.x + t * 4);
           xr[u].x = w2.x;
           xr[u].y = w2.y;
@@ -432,7 +435,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         int32_t q;
         float sq;
         const float4 v =
-            a.x_bf16 ? make_float4(bf16_to_float(xr[u].x & 0xffffu),
+            XB ? make_float4(bf16_to_float(xr[u].x & 0xffffu),
                                    bf16_to_float(xr[u].x >> 16),
                                    bf16_to_float(xr[u].y & 0xffffu),
                                    bf16_to_float(xr[u].y >> 16))
@@ -450,7 +453,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         for (int u = 0; u < U; ++u) {
           const int t = t0 + u * 64 * W + (int)threadIdx.x;
           v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-          if ((t >> 3) < a.blocks) v[u] = load_act4(a.x, t * 4, a.x_bf16 != 0, true);
+          if ((t >> 3) < a.blocks) v[u] = load_act4(a.x, t * 4, XB, true);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -611,15 +614,15 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   float y;
   if (NMAT == 2) {
     const float gs = silu_f32(acc[0]);
-    y = a.y_bf16 ? bf16_to_float(float_to_bf16(gs)) *
+    y = YB ? bf16_to_float(float_to_bf16(gs)) *
                        bf16_to_float(float_to_bf16(acc[NMAT - 1]))
                  : gs * acc[NMAT - 1];
   } else {
-    y = activate(acc[0], a.act);
+    y = ACTV ? activate(acc[0], a.act) : acc[0];
   }
   const bool owner = active && j == 15;
   if (owner) {
-    if (a.y_bf16)
+    if constexpr (YB)
       ((uint16_t *)a.y)[row] = float_to_bf16(y);
     else
       ((float *)a.y)[row] = y;
@@ -627,7 +630,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
 
   if (ARGMAX) {
     // the key of the value as stored
-    const float ys = a.y_bf16 ? bf16_to_float(float_to_bf16(y)) : y;
+    const float ys = YB ? bf16_to_float(float_to_bf16(y)) : y;
     unsigned long long key = owner ? argmax_key(ys, row) : 0ull;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -786,47 +789,43 @@ constexpr int ring_depth() {
   return PC > 0 ? (PC < dmax ? PC : dmax) : (NMAT == 2 ? 4 : 8);
 }
 
-template <int NMAT, bool ARGMAX, int IN, int W, int PC>
+template <int NMAT, bool ARGMAX, int IN, int W, int PC, int V>
 hipError_t launch_gemv_p(const GemvArgs &args, hipStream_t s) {
   constexpr int D = ring_depth<NMAT, IN, PC>();
   const unsigned grid = (unsigned)((args.groups + W - 1) / W);
   const size_t slots = PC > 0 ? row_slots(PC, W) : (size_t)args.passes * kPassBlocks;
   const size_t lds = IN == IN_WG ? slots * (kBlock + 4) : 0;
-  hipLaunchKernelGGL((gemv_kernel<NMAT, ARGMAX, IN, W, D, PC>),
+  hipLaunchKernelGGL((gemv_kernel<NMAT, ARGMAX, IN, W, D, PC, V>),
                      dim3(grid), dim3(64 * W), lds, s, args);
   return hipGetLastError();
 }
 
 // IN_WG takes its workgroup width from the pass count (wg_waves); IN_PRE
-// runs one wave per workgroup, or four for very wide outputs.
-template <int NMAT, bool ARGMAX, int IN, int PC>
-hipError_t launch_gemv_w(const GemvArgs &args, int waves, hipStream_t s) {
-  if constexpr (IN == IN_WG) {
-    return launch_gemv_p<NMAT, ARGMAX, IN, wg_waves(NMAT, PC), PC>(args, s);
-  } else {
-    if (waves == 4) return launch_gemv_p<NMAT, ARGMAX, IN, 4, PC>(args, s);
-    return launch_gemv_p<NMAT, ARGMAX, IN, 1, PC>(args, s);
-  }
+// (wide outputs) runs four waves per workgroup.
+template <int NMAT, bool ARGMAX, int IN, int PC, int V>
+hipError_t launch_gemv_w(const GemvArgs &args, hipStream_t s) {
+  constexpr int W = IN == IN_WG ? wg_waves(NMAT, PC) : 4;
+  return launch_gemv_p<NMAT, ARGMAX, IN, W, PC, V>(args, s);
 }
 
 // Pass counts with a fully unrolled kernel: K = 512, 1024, 1536, 2560
 // (hidden size), 4096 and 9216 (the MLP down projection).  Others take the
 // runtime loop.
-template <int NMAT, bool ARGMAX, int IN>
-hipError_t launch_gemv_t(const GemvArgs &args, int waves, hipStream_t s) {
+template <int NMAT, bool ARGMAX, int IN, int V>
+hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t s) {
   switch (args.passes) {
-    case 1: return launch_gemv_w<NMAT, ARGMAX, IN, 1>(args, waves, s);
-    case 2: return launch_gemv_w<NMAT, ARGMAX, IN, 2>(args, waves, s);
-    case 3: return launch_gemv_w<NMAT, ARGMAX, IN, 3>(args, waves, s);
-    case 5: return launch_gemv_w<NMAT, ARGMAX, IN, 5>(args, waves, s);
-    case 8: return launch_gemv_w<NMAT, ARGMAX, IN, 8>(args, waves, s);
-    case 18: return launch_gemv_w<NMAT, ARGMAX, IN, 18>(args, waves, s);
-    default: return launch_gemv_w<NMAT, ARGMAX, IN, 0>(args, waves, s);
+    case 1: return launch_gemv_w<NMAT, ARGMAX, IN, 1, V>(args, s);
+    case 2: return launch_gemv_w<NMAT, ARGMAX, IN, 2, V>(args, s);
+    case 3: return launch_gemv_w<NMAT, ARGMAX, IN, 3, V>(args, s);
+    case 5: return launch_gemv_w<NMAT, ARGMAX, IN, 5, V>(args, s);
+    case 8: return launch_gemv_w<NMAT, ARGMAX, IN, 8, V>(args, s);
+    case 18: return launch_gemv_w<NMAT, ARGMAX, IN, 18, V>(args, s);
+    default: return launch_gemv_w<NMAT, ARGMAX, IN, 0, V>(args, s);
   }
 }
 
 // Workgroup width of a launch (as launch_gemv_w picks it).
-static int gemv_waves(int64_t groups, int64_t passes, int in, int nmat) {
+static int gemv_waves(int64_t passes, int in, int nmat) {
   if (in == IN_WG) {
     switch (passes) {
       case 1: case 2: case 3: case 5: case 8: case 18:
@@ -835,7 +834,7 @@ static int gemv_waves(int64_t groups, int64_t passes, int in, int nmat) {
         return wg_waves(nmat, 0);
     }
   }
-  return groups >= 8192 ? 4 : 1;
+  return 4;
 }
 
 }  // namespace
@@ -897,12 +896,43 @@ int64_t gemv_workgroups(int64_t rows) {
   return rows / kLanes;  // one wave per workgroup is the widest grid
 }
 
+// The compile-time variants the C ABI needs (V bits as in gemv_kernel):
+// SwiGLU f32 or bf16 in and out; the argmax GEMV (lm_head) with f32 logits
+// from an f32 or bf16 row; plain GEMVs with or without an activation, f32 or
+// bf16 in and out.  IN_PRE reads an already quantized row (no input type).
 template <int IN>
 static hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
-                                 int waves, hipStream_t s) {
-  if (l.nmat == 2) return launch_gemv_t<2, false, IN>(a, waves, s);
-  if (l.keys) return launch_gemv_t<1, true, IN>(a, waves, s);
-  return launch_gemv_t<1, false, IN>(a, waves, s);
+                                 hipStream_t s) {
+  const int xb = (IN == IN_WG && l.x_bf16) ? 1 : 0;
+  const int yb = l.y_bf16 ? 2 : 0;
+  const int av = (l.nmat == 1 && !l.keys && l.activation != 0) ? 4 : 0;
+  const int v = xb | yb | av;
+  if (l.nmat == 2) {
+    if (v == 0) return launch_gemv_t<2, false, IN, 0>(a, s);
+    if (v == (IN == IN_WG ? 3 : 2)) return launch_gemv_t<2, false, IN, IN == IN_WG ? 3 : 2>(a, s);
+    return hipErrorInvalidValue;
+  }
+  if (l.keys) {
+    if (v == 0) return launch_gemv_t<1, true, IN, 0>(a, s);
+    if (IN == IN_WG && v == 1) return launch_gemv_t<1, true, IN, 1>(a, s);
+    return hipErrorInvalidValue;
+  }
+  if (IN == IN_WG) {
+    switch (v) {
+      case 0: return launch_gemv_t<1, false, IN, 0>(a, s);
+      case 3: return launch_gemv_t<1, false, IN, 3>(a, s);
+      case 4: return launch_gemv_t<1, false, IN, 4>(a, s);
+      case 7: return launch_gemv_t<1, false, IN, 7>(a, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (v) {
+    case 0: return launch_gemv_t<1, false, IN, 0>(a, s);
+    case 2: return launch_gemv_t<1, false, IN, 2>(a, s);
+    case 4: return launch_gemv_t<1, false, IN, 4>(a, s);
+    case 6: return launch_gemv_t<1, false, IN, 6>(a, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
@@ -918,13 +948,11 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
   a.blocks = (int32_t)(l.cols / kBlock);
   a.passes = (int32_t)passes_for(l.cols);
   a.act = l.activation;
-  a.x_bf16 = l.x_bf16 ? 1 : 0;
-  a.y_bf16 = l.y_bf16 ? 1 : 0;
   const int in = l.x ? IN_WG : IN_PRE;
   if (l.x && (uintptr_t)l.x % (l.x_bf16 ? 8 : 16)) return hipErrorInvalidValue;
-  const int waves = gemv_waves(a.groups, a.passes, in, l.nmat);
-  hipError_t e = in == IN_WG ? launch_gemv_in<IN_WG>(a, l, waves, s)
-                             : launch_gemv_in<IN_PRE>(a, l, waves, s);
+  const int waves = gemv_waves(a.passes, in, l.nmat);
+  hipError_t e = in == IN_WG ? launch_gemv_in<IN_WG>(a, l, s)
+                             : launch_gemv_in<IN_PRE>(a, l, s);
   if (e != hipSuccess || !l.keys) return e;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(1024), 0, s,
                      (const unsigned long long *)l.keys,
