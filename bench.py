@@ -312,7 +312,7 @@ def cpu_baseline(res, budget_s=12.0):
         h = o.swiglu(x, pg, pu, ffn)              # row-parallel: 1 thread at M=1
         o.linear(h, pd, hidden)
         n += 1
-        if time.perf_counter() - t0 > budget_s or n >= 50:
+        if time.perf_counter() - t0 > budget_s or n >= 250:
             break
     dt = (time.perf_counter() - t0) / n
     t0 = time.perf_counter()
@@ -417,7 +417,7 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": (load_traffic() or {}).get("hbm_bytes_per_launch"),
-                     "kernel": "gemv_kernel<2,0,false,IN_WG,3,5,5> (fused gate/up "
+                     "kernel": "gemv_kernel<2,false,IN_WG,3,5,5,0> (fused gate/up "
                                "SwiGLU, 3-wave workgroups, input row quantized "
                                "per workgroup; timed alone via llmcp_q8_swiglu)",
                      "launch_us": round(res["gu_launch_us"], 3),
