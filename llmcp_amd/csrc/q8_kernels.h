@@ -61,11 +61,11 @@ int64_t gemv_workgroups(int64_t rows);
 // Prefill GEMM on int8 MFMA.  qa/sa: Q8_1 activations [m, ldq] / [m, lds],
 // zero-padded to passes*16 blocks (launch_quantize with blocks_pad).
 struct GemmLaunch {
-  const int8_t *qa = nullptr;
-  int64_t ldq = 0;
+  const int8_t *qa = nullptr;  // tiled Q8_1 input (launch_quantize_tiled)
   const float *sa = nullptr;
-  int64_t lds = 0;
-  const uint8_t *w = nullptr;  // pass layout
+  int32_t row_tiles = 0;       // 32-row tiles in qa / sa
+  int32_t nblk = 0;            // padded blocks per row (units * 16)
+  const uint8_t *w = nullptr;  // unit layout
   int64_t rows = 0;            // N
   int64_t cols = 0;            // K
   int64_t m = 0;               // M
@@ -77,6 +77,14 @@ struct GemmLaunch {
 };
 
 hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);
+
+// Q8_1 activations in the GEMM's tiled layout: the 32 rows x 32 values of
+// row tile t and block b are 1 KiB at (t * blocks_pad + b) * 1024 (row r at
+// r * 32), their scales 32 floats at (t * blocks_pad + b) * 32.  Rows past m
+// in the last tile are left unwritten (their results are never stored).
+hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
+                                 int64_t ldx, int64_t cols, int8_t *qa,
+                                 float *sa, int64_t blocks_pad, hipStream_t s);
 
 // SwiGLU multiply of the prefill path from f32 gate (SiLU applied) and up:
 // f32 h = g * u in place in g, or bf16 out = bf16(bf16(g) * bf16(u)).

@@ -250,10 +250,13 @@ __global__ void selftest_quant_kernel(uint32_t lo, uint32_t hi,
 }
 
 // Grid: x covers (row, padded block) in units of 8 blocks per wave.
+// tiled != 0 writes the GEMM's tiled layout (launch_quantize_tiled) and
+// ignores ldq / lds.
 __global__ void quantize_kernel(const void *__restrict__ x, int x_bf16,
                                 int64_t m, int64_t ldx, int64_t blocks,
                                 int8_t *qa, int64_t ldq, float *sa,
-                                int64_t lds, int64_t blocks_pad, int aligned) {
+                                int64_t lds, int64_t blocks_pad, int aligned,
+                                int tiled) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t blk_all = t >> 3;  // global (row, block) index
   const int lane = threadIdx.x & 63;
@@ -269,8 +272,14 @@ __global__ void quantize_kernel(const void *__restrict__ x, int x_bf16,
   float s;
   quantize_block8(v, valid, &q, &s);
   if (in_range) {
-    *(int32_t *)(qa + row * ldq + blk * kBlock + (lane & 7) * 4) = q;
-    if ((lane & 7) == 0) sa[row * lds + blk] = s;
+    if (tiled) {
+      const int64_t tile = (row >> 5) * blocks_pad + blk;
+      *(int32_t *)(qa + tile * 1024 + (row & 31) * kBlock + (lane & 7) * 4) = q;
+      if ((lane & 7) == 0) sa[tile * 32 + (row & 31)] = s;
+    } else {
+      *(int32_t *)(qa + row * ldq + blk * kBlock + (lane & 7) * 4) = q;
+      if ((lane & 7) == 0) sa[row * lds + blk] = s;
+    }
   }
 }
 
@@ -884,7 +893,21 @@ hipError_t launch_quantize(const void *x, bool x_bf16, int64_t m, int64_t ldx,
       ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
   hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(threads, 256)), dim3(256),
                      0, s, x, x_bf16 ? 1 : 0, m, ldx, blocks, qa, ldq, sa, lds,
-                     blocks_pad, aligned);
+                     blocks_pad, aligned, 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
+                                 int64_t ldx, int64_t cols, int8_t *qa,
+                                 float *sa, int64_t blocks_pad, hipStream_t s) {
+  const int64_t blocks = cols / kBlock;
+  const int64_t threads = m * blocks_pad * 8;
+  const int64_t esz = x_bf16 ? 2 : 4;
+  const int aligned =
+      ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(threads, 256)), dim3(256),
+                     0, s, x, x_bf16 ? 1 : 0, m, ldx, blocks, qa, (int64_t)0, sa,
+                     (int64_t)0, blocks_pad, aligned, 1);
   return hipGetLastError();
 }
 

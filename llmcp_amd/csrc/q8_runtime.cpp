@@ -635,18 +635,18 @@ static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
                        const Rows &out, int activation) {
   const int64_t m = in.rows;
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
-  int rc = ensure_scratch(ctx, (uint64_t)(m * nblk * kBlock),
-                          (uint64_t)(m * nblk * 4));
+  const int64_t row_tiles = (m + 31) / 32;  // the tiled layout pads M to 32
+  int rc = ensure_scratch(ctx, (uint64_t)(row_tiles * 32 * nblk * kBlock),
+                          (uint64_t)(row_tiles * 32 * nblk * 4));
   if (rc) return rc;
-  hipError_t e = launch_quantize(in.data, in.bf16, m, in.ld, w->cols, ctx->qa,
-                                 nblk * kBlock, ctx->sa, nblk, nblk,
-                                 ctx->stream);
+  hipError_t e = launch_quantize_tiled(in.data, in.bf16, m, in.ld, w->cols,
+                                       ctx->qa, ctx->sa, nblk, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "quantize launch");
   GemmLaunch g;
   g.qa = ctx->qa;
-  g.ldq = nblk * kBlock;
   g.sa = ctx->sa;
-  g.lds = nblk;
+  g.row_tiles = (int32_t)row_tiles;
+  g.nblk = (int32_t)nblk;
   g.w = w->dev;
   g.rows = w->rows;
   g.cols = w->cols;
