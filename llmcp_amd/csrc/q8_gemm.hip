@@ -16,6 +16,10 @@
 // stage buffers (see gemm_kernel).
 #include "q8_kernels.h"
 
+#include <stddef.h>
+
+#include <utility>
+
 #include "q8_device.h"
 
 namespace llmcp_q8 {
@@ -49,22 +53,45 @@ constexpr int kStageBlocks = 4;
 
 template <int WM, int WN, int SEG>
 struct GemmStage {
-  static constexpr int DWC = SEG > 1 ? 2 : 1;  // dw pieces per column tile
-  static constexpr int CA = WM * kStageBlocks;  // A tiles (1 KiB)
-  static constexpr int CS = WM * 2;             // sa pairs (256 B)
-  static constexpr int CB = WN * 4;             // weight chunks (1 KiB)
-  static constexpr int CD = WN * DWC;           // dw pieces (256 B)
-  static constexpr int TOTAL = CA + CS + CB + CD;
   static constexpr int W = WM * WN;
-  // DMA instructions per wave and stage: op o goes to wave o % W.
-  static constexpr int ops_of(int wave) {
-    return TOTAL / W + (wave < TOTAL % W ? 1 : 0);
-  }
+  // DMA ops of a stage.  16 B per lane (1 KiB per op): the A tiles (row
+  // tile, block), the weight chunks (4 per column tile), the activation
+  // scales (two row tiles per op: 4 blocks x 32 rows each) and, for S = 1,
+  // each column tile's 8 scale blocks of 128 B (the whole unit's scales, so
+  // one op instead of scattered 4 B pieces).  4 B per lane: for S > 1 the
+  // weight scales of the stage's blocks, which sit in different units.
+  static constexpr int CA = WM * kStageBlocks;
+  static constexpr int CB = WN * 4;
+  static constexpr int CS = (WM + 1) / 2;
+  static constexpr int CD16 = SEG == 1 ? WN : 0;
+  static constexpr int CD4 = SEG == 1 ? 0 : 2 * WN;
+  // Every wave issues the same number of each size (S16, S4),
+  // unconditionally: a branch around a DMA, or a branch between DMAs of
+  // different sizes, makes the compiler's wait tracking merge states and
+  // wait for all loads before the next LDS read.  Where a class does not
+  // divide evenly, waves repeat another wave's op (same bytes, same place).
+  static constexpr int T16 = CA + CB + CS + CD16;
+  static constexpr int T4 = CD4;
+  static constexpr int S16 = (T16 + W - 1) / W;
+  static constexpr int S4 = (T4 + W - 1) / W;
+  static constexpr int OPS = S16 + S4;  // DMA instructions per wave and stage
   __align__(16) int8_t a[WM][kStageBlocks][1024];
   __align__(16) int8_t b[WN][4 * 1024];
-  __align__(16) float sa[WM][2][64];
-  __align__(16) uint32_t dw[WN][DWC][64];
+  __align__(16) float sa[2 * CS][kStageBlocks][32];
+  __align__(16) uint8_t dw16[CD16 > 0 ? WN : 1][1024];
+  __align__(16) uint32_t dw4[CD4 > 0 ? WN : 1][2][64];
 };
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1,
+// so that every private-array index in the body is a constant.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -81,21 +108,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
 }
-// Waits until at most n of this wave's vector-memory ops are outstanding
-// (n wave-uniform, at most NMAX).
-template <int NMAX>
-__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
-  if constexpr (NMAX > 0) {
-    if (n >= NMAX) {
-      wait_vmcnt<NMAX>();
-      return;
-    }
-    wait_vmcnt_dyn<NMAX - 1>(n);
-  } else {
-    wait_vmcnt<0>();
-  }
-}
-
 // Workgroup barrier without a memory fence: the LDS data it publishes came
 // by DMA, whose completion each wave establishes with its own vmcnt wait
 // first (a fenced barrier would wait for every load in flight).  The
@@ -116,16 +128,25 @@ __device__ __forceinline__ const T *uniform_ptr(const T *p) {
   return (const T *)(((uint64_t)hi << 32) | lo);
 }
 
-// Byte offset of block b's slot within its group's units, for the segment
-// sizes whose blocks do not sit at a fixed lane offset from the stage's
-// first block (S = 6).
-template <int SEG>
-__device__ __forceinline__ uint32_t block_offset(int b) {
-  int64_t unit;
-  int slot;
-  locate<SEG>(b, unit, slot);
-  return (uint32_t)(unit * kPassBytes + slot * 16);
-}
+// S = 6 (18 units, passes of 96 blocks): block kb + p of a stage (kb a
+// multiple of 4, p < 4) sits at unit 6P + d', slot q + wrap, where
+// rem = kb mod 96 = 6q + r (r in {0, 2, 4}), d = r + p, wrap = (d >= 6) and
+// d' = d - 6 wrap.  Per lane only (r, p) matter: the kernel keeps the three
+// per-lane variants and selects one per stage by the wave-uniform r.
+struct Seg6 {
+  static __device__ __forceinline__ int wrap(int r, int p) { return r + p >= 6 ? 1 : 0; }
+  // byte offset of the block's 16 B piece, relative to unit 6P, slot q
+  static __device__ __forceinline__ uint32_t qs(int r, int p) {
+    const int w6 = wrap(r, p);
+    return (uint32_t)((r + p - 6 * w6) * kPassBytes + w6 * 16);
+  }
+  // byte offset of the f16 pair holding the block's scale, relative to
+  // unit 6P, slot pair (q & ~1)
+  static __device__ __forceinline__ uint32_t scale(int r, int q, int p) {
+    const int w6 = wrap(r, p);
+    return (uint32_t)((r + p - 6 * w6) * kPassBytes + 2 * ((q + w6) & ~1) - 2 * (q & ~1));
+  }
+};
 
 // The occupancy the LDS allows (12 waves: one workgroup per CU, three waves
 // per SIMD; 4 waves: two workgroups per CU) is declared so that the kernel
@@ -139,14 +160,13 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
                  int64_t n_rows, int64_t m_rows, int32_t passes, int32_t m_tiles,
                  int32_t n_tiles, void *__restrict__ y, int64_t ldy) {
   typedef GemmStage<WM, WN, SEG> St;
-  static_assert(NST >= 2 && NST <= 5, "stage buffers");
+  static_assert(NST == 2 || NST == 4, "stage buffers");
   constexpr int W = WM * WN;
   constexpr int BM = 32 * WM, BN = 32 * WN;
-  constexpr int OPS_MAX = St::ops_of(0);
   constexpr int UNIT_S4 = SEG == 4;  // blocks of a stage: one slot, 4 units
   // one LDS object per stage buffer (see above)
   __shared__ St st0, st1, st2, st3, st4;
-  auto stage = [&](int i) -> St & {
+  auto stage = [&](int i) __attribute__((always_inline)) -> St & {
     return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : i == 3 ? st3 : st4;
   };
 
@@ -168,83 +188,132 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane & 31, lh = lane >> 5;
   const int stages = passes * (kPassBlocks / kStageBlocks);
-  const int ops = St::ops_of(wave);
   const int64_t wrow = (int64_t)passes * kPassBytes;  // bytes per lane group
 
-  // Loop-invariant per-lane byte offsets of this wave's DMA ops (a tensor
-  // is below 4 GiB); the per-stage part of each address is wave-uniform
-  // (plus, for S = 6, a per-lane block offset).
-  uint32_t off[OPS_MAX];
-  int bpiece[OPS_MAX];  // S = 6: the block of the stage this lane loads
+  // This wave's DMA ops.  Per op: a loop-invariant per-lane byte offset (a
+  // tensor is below 4 GiB), its kind and LDS destination (wave-uniform);
+  // the per-stage part of each address is wave-uniform too (plus, for
+  // S = 6, a per-lane block offset).
+  enum { K_A = 0, K_B = 1, K_SA = 2, K_DW = 3 };
+  uint32_t off16[St::S16], off4[St::S4 > 0 ? St::S4 : 1];
+  int kind[St::S16], abb[St::S16], dst16[St::S16], piece16[St::S16];
+  int dst4[St::S4 > 0 ? St::S4 : 1], piece4[St::S4 > 0 ? St::S4 : 1];
+  // S = 6: per-lane block offsets for r = 0, 2, 4 (Seg6), in three arrays
+  // indexed only at compile time (a runtime index would put them in scratch)
+  uint32_t x16r0[St::S16], x16r2[St::S16], x16r4[St::S16];
 #pragma unroll
-  for (int u = 0; u < OPS_MAX; ++u) {
-    const int o = wave + u * W;
-    off[u] = 0;
-    bpiece[u] = 0;
+  for (int u = 0; u < St::S16; ++u) {
+    int o = wave + u * W;
+    if (o >= St::T16) o -= St::T16;
+    abb[u] = o % kStageBlocks;
+    piece16[u] = 0;
     if (o < St::CA) {
+      kind[u] = K_A;
       const int64_t rt = min((int64_t)m_tile * WM + o / kStageBlocks, (int64_t)row_tiles - 1);
-      off[u] = (uint32_t)(rt * nblk * 1024 + li * 32 + lh * 16);
-    } else if (o < St::CA + St::CS) {
+      off16[u] = (uint32_t)(rt * nblk * 1024 + li * 32 + lh * 16);
+      dst16[u] = (int)offsetof(St, a) + o * 1024;
+    } else if (o < St::CA + St::CB) {
+      kind[u] = K_B;
       const int c = o - St::CA;
-      const int64_t rt = min((int64_t)m_tile * WM + c / 2, (int64_t)row_tiles - 1);
-      off[u] = (uint32_t)((rt * nblk * 32 + lane) * 4);
-    } else if (o < St::CA + St::CS + St::CB) {
-      const int c = o - St::CA - St::CS;
       const int q = lane >> 2;
       const int ri = 16 * (c & 3) + q;
       const int64_t n = min(n0 + 32 * (c >> 2) + (ri & 31), n_rows - 1);
       const int piece = (lane & 3) ^ ((q >> 2) & 3);
-      bpiece[u] = piece;
-      off[u] = (uint32_t)((n >> 2) * wrow + (ri >> 5) * 1024 + (n & 3) * 256 +
-                          (SEG == 1 ? piece * 16 : SEG == 4 ? piece * kPassBytes : 0));
-    } else if (o < St::TOTAL) {
-      const int c = o - St::CA - St::CS - St::CB;
-      const int64_t n = min(n0 + 32 * (c / St::DWC) + li, n_rows - 1);
-      const int j = c % St::DWC;
-      // S == 1: lane half lh takes the pair (2lh, 2lh+1) of the stage's 4
-      // slots; S > 1: block 2j + lh of the stage, one f16 per dword
-      bpiece[u] = 2 * j + lh;
-      off[u] = (uint32_t)((n >> 2) * wrow + kPassQs + 32 * (n & 3) +
-                          (SEG == 1 ? 4 * lh : SEG == 4 ? (2 * j + lh) * kPassBytes : 0));
+      piece16[u] = piece;
+      off16[u] = (uint32_t)((n >> 2) * wrow + (ri >> 5) * 1024 + (n & 3) * 256 +
+                            (SEG == 1 ? piece * 16 : SEG == 4 ? piece * kPassBytes : 0));
+      dst16[u] = (int)offsetof(St, b) + c * 1024;
+    } else if (o < St::CA + St::CB + St::CS) {
+      kind[u] = K_SA;
+      // lanes 0-31: row tile 2c, lanes 32-63: row tile 2c+1 (512 B each)
+      const int c = o - St::CA - St::CB;
+      const int64_t rt = min((int64_t)m_tile * WM + 2 * c + lh, (int64_t)row_tiles - 1);
+      off16[u] = (uint32_t)(rt * nblk * 128 + li * 16);
+      dst16[u] = (int)offsetof(St, sa) + c * 1024;
+    } else {
+      kind[u] = K_DW;
+      // column tile c: lane l takes 16 B of group l/8's 128 B scale block
+      const int c = o - St::CA - St::CB - St::CS;
+      const int64_t ng = min(n0 + 32 * c + 4 * (lane >> 3), n_rows - 4);
+      off16[u] = (uint32_t)((ng >> 2) * wrow + kPassQs + (lane & 7) * 16);
+      dst16[u] = (int)offsetof(St, dw16) + c * 1024;
     }
   }
-
-  // Issue the DMA of stage s into buffer `buf`.
-  auto issue = [&](int s, St &buf) {
-    const int kb = s * kStageBlocks;  // first block of the stage
-    int64_t unit;
-    int slot;
-    locate<SEG>(kb, unit, slot);
 #pragma unroll
-    for (int u = 0; u < OPS_MAX; ++u) {
-      const int o = wave + u * W;
-      if (o < St::CA) {
-        const int bb = o % kStageBlocks;
-        dma16(uniform_ptr(qa + (int64_t)(kb + bb) * 1024) + off[u],
-              buf.a[o / kStageBlocks][bb]);
-      } else if (o < St::CA + St::CS) {
-        const int c = o - St::CA;
-        dma4(uniform_ptr((const uint8_t *)(sa + (int64_t)(kb + 2 * (c & 1)) * 32)) + off[u],
-             buf.sa[c / 2][c & 1]);
-      } else if (o < St::CA + St::CS + St::CB) {
-        const int c = o - St::CA - St::CS;
-        const uint8_t *base = SEG == 6 ? w : uniform_ptr(w + unit * kPassBytes + slot * 16);
-        const uint32_t extra = SEG == 6 ? block_offset<SEG>(kb + bpiece[u]) : 0u;
-        dma16(base + off[u] + extra, buf.b[c >> 2] + (c & 3) * 1024);
-      } else if (o < St::TOTAL) {
-        const int c = o - St::CA - St::CS - St::CB;
-        const uint8_t *base =
-            SEG == 6 ? w : uniform_ptr(w + unit * kPassBytes + 2 * (slot & ~1));
-        uint32_t extra = 0;
-        if constexpr (SEG == 6) {
-          int64_t ub;
-          int sb;
-          locate<SEG>(kb + bpiece[u], ub, sb);
-          extra = (uint32_t)(ub * kPassBytes + 2 * (sb & ~1));
-        }
-        dma4(base + off[u] + extra, buf.dw[c / St::DWC][c % St::DWC]);
-      }
+  for (int u = 0; u < St::S4; ++u) {
+    int o = wave + u * W;
+    if (o >= St::T4) o -= St::T4;
+    // S > 1, column tile o/2, block 2(o%2) + lh of the stage, one f16 per
+    // dword
+    const int64_t n = min(n0 + 32 * (o / 2) + li, n_rows - 1);
+    const int j = o % 2;
+    piece4[u] = 2 * j + lh;
+    off4[u] = (uint32_t)((n >> 2) * wrow + kPassQs + 32 * (n & 3) +
+                         (SEG == 4 ? (2 * j + lh) * kPassBytes : 0));
+    dst4[u] = (int)offsetof(St, dw4) + o * 256;
+  }
+
+#pragma unroll
+  for (int u = 0; u < St::S16; ++u) {
+    const bool seg = SEG == 6 && kind[u] == K_B;
+    x16r0[u] = seg ? Seg6::qs(0, piece16[u]) : 0u;
+    x16r2[u] = seg ? Seg6::qs(2, piece16[u]) : 0u;
+    x16r4[u] = seg ? Seg6::qs(4, piece16[u]) : 0u;
+  }
+
+  // Wave-uniform position of a stage's first block in the unit layout:
+  // S = 1, 4: its unit and slot; S = 6: unit 6P, slot q and r (Seg6).
+  struct StagePos {
+    int64_t unit;
+    int slot, r;
+  };
+  auto stage_pos = [&](int kb) __attribute__((always_inline)) {
+    StagePos sp;
+    if constexpr (SEG == 6) {
+      const int pass = kb / 96, rem = kb - 96 * pass;
+      sp.unit = 6 * pass;
+      sp.slot = rem / 6;
+      sp.r = rem - 6 * sp.slot;
+    } else {
+      locate<SEG>(kb, sp.unit, sp.slot);
+      sp.r = 0;
     }
+    return sp;
+  };
+
+  // Issue DMA op j (j < S16: 16 B class, else 4 B class) of stage s into
+  // buffer `buf`: branch-free, the same instruction sequence in every wave.
+  auto issue_op = [&](int s, St &buf, auto J) __attribute__((always_inline)) {
+    constexpr int j = decltype(J)::value;
+    const int kb = s * kStageBlocks;  // first block of the stage
+    const StagePos sp = stage_pos(kb);
+    int8_t *lds_base = (int8_t *)&buf;
+    if constexpr (j < St::S16) {
+      const int u = j;
+      const uint8_t *wb = w + sp.unit * kPassBytes + sp.slot * 16;
+      const uint8_t *ab = (const uint8_t *)qa + (int64_t)(kb + abb[u]) * 1024;
+      const uint8_t *sab = (const uint8_t *)sa + (int64_t)kb * 128;
+      const uint8_t *db = w + sp.unit * kPassBytes;
+      const uint8_t *base = kind[u] == K_A ? ab : kind[u] == K_B ? wb : kind[u] == K_SA ? sab : db;
+      uint32_t extra = 0;
+      if constexpr (SEG == 6) {
+        // masks, not a select between array elements (which the compiler
+        // turns into a load through a selected pointer, forcing the arrays
+        // into scratch)
+        const uint32_t m0 = sp.r == 0 ? ~0u : 0u, m2 = sp.r == 2 ? ~0u : 0u;
+        extra = (x16r0[u] & m0) | (x16r2[u] & m2) | (x16r4[u] & ~(m0 | m2));
+      }
+      dma16(uniform_ptr(base) + off16[u] + extra, lds_base + dst16[u]);
+    } else {
+      const int u = j - St::S16;
+      const uint8_t *db = w + sp.unit * kPassBytes + 2 * (sp.slot & ~1);
+      uint32_t extra = 0;
+      if constexpr (SEG == 6) extra = Seg6::scale(sp.r, sp.slot, piece4[u]);
+      dma4(uniform_ptr(db) + off4[u] + extra, lds_base + dst4[u]);
+    }
+  };
+  auto issue = [&](int s, St &buf) __attribute__((always_inline)) {
+    static_for<St::OPS>([&](auto J) __attribute__((always_inline)) { issue_op(s, buf, J); });
   };
 
   float acc[16];
@@ -253,59 +322,84 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   const int bsw = (lane >> 2) & 3;  // swizzle of this lane's weight run
 
-  auto compute = [&](int s, St &buf) {
-    const int kb = s * kStageBlocks;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      // scale tiles of blocks kb+2k (lanes 0-31) and kb+2k+1 (lanes 32-63)
-      const float fa = buf.sa[wm][k][lane];
-      uint32_t dwp;
-      int hi;
-      if constexpr (SEG == 1) {
-        dwp = buf.dw[wn][0][32 * k + li];
-        hi = lh;
-      } else {
-        dwp = buf.dw[wn][k][lane];
-        int64_t ub;
-        int sb;
-        locate<SEG>(kb + 2 * k + lh, ub, sb);
-        hi = sb & 1;
-      }
-      const float fb = half_bits_to_float(hi ? dwp >> 16 : dwp & 0xffffu);
-      typedef float v32f __attribute__((ext_vector_type(32)));
-      const v32f z32 = {};
-      const v32f fac = __builtin_amdgcn_mfma_f32_32x32x1f32(fa, fb, z32, 0, 0, 0);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int bb = 2 * k + j;
-        const v4i af = *(const v4i *)(buf.a[wm][bb] + lane * 16);
-        const v4i bf = *(const v4i *)(buf.b[wn] + lane * 64 + 16 * (bb ^ bsw));
-        const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, zero, 0, 0, 0);
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float dotf = (float)c[v];
-          const float f = fac[16 * j + v];
-          if (FMA) {
-            acc[v] = __builtin_fmaf(dotf, f, acc[v]);
-          } else {
-            const float contrib = dotf * f;
-            acc[v] = acc[v] + contrib;
-          }
-        }
-        // One block's MFMA results live at a time: the accumulators are
-        // pinned here (an empty asm that reads and writes them), so the
-        // epilogue cannot sink below later stages' MFMAs, which would only
-        // add registers -- the other waves of the SIMD fill MFMA latency.
-#pragma unroll
-        for (int v = 0; v < 16; ++v) asm volatile("" : "+v"(acc[v]));
-      }
+  // Scale tiles of blocks kb+2k (lanes 0-31) and kb+2k+1 (lanes 32-63).
+  typedef float v32f __attribute__((ext_vector_type(32)));
+  auto scales = [&](int kb, St &buf, int k) __attribute__((always_inline)) -> v32f {
+    const float fa = buf.sa[wm][2 * k + lh][li];
+    uint32_t h;
+    if constexpr (SEG == 1) {
+      // this lane's row n = li of column tile wn: group li/4, row li%4; the
+      // f16 pair (2k, 2k+1) of the stage's slots, half lh
+      const uint32_t pair = ((const uint32_t *)buf.dw16[wn])[(li >> 2) * 32 + (li & 3) * 8 +
+                                                              ((kb & (kPassBlocks - 1)) >> 1) + k];
+      h = lh ? pair >> 16 : pair & 0xffffu;
+    } else if constexpr (SEG == 4) {
+      // the stage's four blocks share one slot
+      const uint32_t dwp = buf.dw4[wn][k][lane];
+      int64_t ub;
+      int sb;
+      locate<SEG>(kb, ub, sb);
+      h = (sb & 1) ? dwp >> 16 : dwp & 0xffffu;
+    } else {
+      const uint32_t dwp = buf.dw4[wn][k][lane];
+      const StagePos sp = stage_pos(kb);
+      h = ((sp.slot + Seg6::wrap(sp.r, 2 * k + lh)) & 1) ? dwp >> 16 : dwp & 0xffffu;
     }
+    const float fb = half_bits_to_float(h);
+    const v32f z32 = {};
+    return __builtin_amdgcn_mfma_f32_32x32x1f32(fa, fb, z32, 0, 0, 0);
+  };
+  auto dots = [&](St &buf, int bb) __attribute__((always_inline)) -> v16i {
+    const v4i af = *(const v4i *)(buf.a[wm][bb] + lane * 16);
+    const v4i bf = *(const v4i *)(buf.b[wn] + lane * 64 + 16 * (bb ^ bsw));
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, zero, 0, 0, 0);
+  };
+  // Software-pipelined over the stage's blocks: block bb+1's MFMA (and the
+  // next pair's scale MFMA) issue before block bb's epilogue, so a wave has
+  // VALU work while its matrix ops run.
+  // The next stage's DMA ops (stage sn into buffer nbuf) are spread over
+  // the blocks, issued after each block's MFMAs: a burst of them right after
+  // the barrier would stall every wave on the load queue at once.
+  auto compute = [&](int s, St &buf, int sn, St &nbuf) __attribute__((always_inline)) {
+    const int kb = s * kStageBlocks;
+    v32f fac[2];
+    fac[0] = scales(kb, buf, 0);
+    v16i c = dots(buf, 0);
+    static_for<kStageBlocks>([&](auto BB) __attribute__((always_inline)) {
+      constexpr int bb = decltype(BB)::value;
+      v16i cn = c;
+      if constexpr (bb + 1 < kStageBlocks) cn = dots(buf, bb + 1);
+      if constexpr (bb == 0) fac[1] = scales(kb, buf, 1);
+      static_for<St::OPS>([&](auto J) __attribute__((always_inline)) {
+        if constexpr (decltype(J)::value * kStageBlocks / St::OPS == bb)
+          issue_op(sn, nbuf, J);
+      });
+      const v32f &f2 = fac[bb >> 1];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float dotf = (float)c[v];
+        const float f = f2[16 * (bb & 1) + v];
+        if (FMA) {
+          acc[v] = __builtin_fmaf(dotf, f, acc[v]);
+        } else {
+          const float contrib = dotf * f;
+          acc[v] = acc[v] + contrib;
+        }
+      }
+      // The accumulators are pinned here (an empty asm that reads and
+      // writes them), so an epilogue cannot sink below later blocks' MFMAs
+      // and pile up their results in registers.
+#pragma unroll
+      for (int v = 0; v < 16; ++v) asm volatile("" : "+v"(acc[v]));
+      c = cn;
+    });
   };
 
   // Every DMA is unconditional: a branch around one makes the compiler's
   // wait tracking merge states and wait for all loads before the next LDS
   // read.  Stages past the end reload the last stage into a buffer nobody
   // reads again (the stage count, 4 per unit, is a multiple of NST).
+  static_assert(kPassBlocks / kStageBlocks % NST == 0, "stages per unit");
   const int last = stages - 1;
 #pragma unroll
   for (int i = 0; i < NST - 1; ++i) issue(min(i, last), stage(i));
@@ -315,14 +409,10 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     for (int i = 0; i < NST; ++i) {
       const int s = s0 + i;
       // NST - 2 stages were issued after stage s
-      if constexpr (St::TOTAL % W == 0)
-        wait_vmcnt<(NST - 2) * OPS_MAX>();
-      else
-        wait_vmcnt_dyn<(NST - 2) * OPS_MAX>((NST - 2) * ops);
+      wait_vmcnt<(NST - 2) * St::OPS>();
       stage_barrier();
       // every wave is past stage s-1: its buffer takes stage s+NST-1
-      issue(min(s + NST - 1, last), stage((i + NST - 1) % NST));
-      compute(s, stage(i));
+      compute(s, stage(i), min(s + NST - 1, last), stage((i + NST - 1) % NST));
     }
   }
   // no DMA may land in LDS after the workgroup has released it
