@@ -250,13 +250,10 @@ __global__ void selftest_quant_kernel(uint32_t lo, uint32_t hi,
 }
 
 // Grid: x covers (row, padded block) in units of 8 blocks per wave.
-// tiled != 0 writes the GEMM's tiled layout (launch_quantize_tiled) and
-// ignores ldq / lds.
 __global__ void quantize_kernel(const void *__restrict__ x, int x_bf16,
                                 int64_t m, int64_t ldx, int64_t blocks,
                                 int8_t *qa, int64_t ldq, float *sa,
-                                int64_t lds, int64_t blocks_pad, int aligned,
-                                int tiled) {
+                                int64_t lds, int64_t blocks_pad, int aligned) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t blk_all = t >> 3;  // global (row, block) index
   const int lane = threadIdx.x & 63;
@@ -272,14 +269,43 @@ __global__ void quantize_kernel(const void *__restrict__ x, int x_bf16,
   float s;
   quantize_block8(v, valid, &q, &s);
   if (in_range) {
-    if (tiled) {
-      const int64_t tile = (row >> 5) * blocks_pad + blk;
-      *(int32_t *)(qa + tile * 1024 + (row & 31) * kBlock + (lane & 7) * 4) = q;
-      if ((lane & 7) == 0) sa[tile * 32 + (row & 31)] = s;
-    } else {
-      *(int32_t *)(qa + row * ldq + blk * kBlock + (lane & 7) * 4) = q;
-      if ((lane & 7) == 0) sa[row * lds + blk] = s;
-    }
+    *(int32_t *)(qa + row * ldq + blk * kBlock + (lane & 7) * 4) = q;
+    if ((lane & 7) == 0) sa[row * lds + blk] = s;
+  }
+}
+
+// Q8_1 into the GEMM's tiled layout: one wave per 32-row x 1-block tile
+// (tile index rt * blocks_pad + b), in four steps of 8 rows: lane l takes
+// values 4(l%8) .. +3 of row 32rt + 8c + l/8, so each step reads 8 rows of
+// 128 B and writes 256 contiguous bytes of the tile.  quantize_block8 does
+// the arithmetic, so the bits match the row kernel.  Rows past m and blocks
+// past `blocks` are written as zeros.
+__global__ __launch_bounds__(256) void quantize_tiles_kernel(
+    const void *__restrict__ x, int x_bf16, int64_t m, int64_t ldx,
+    int32_t blocks, int32_t blocks_pad, int64_t tiles, int8_t *__restrict__ qa,
+    float *__restrict__ sa, int aligned) {
+  const int lane = threadIdx.x & 63;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= tiles) return;  // uniform per wave
+  const int32_t rt = (int32_t)(tile / blocks_pad);
+  const int32_t b = (int32_t)(tile - (int64_t)rt * blocks_pad);
+  const int rr = lane >> 3, p = lane & 7;
+  float4 v[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int64_t row = (int64_t)rt * 32 + 8 * c + rr;
+    v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < m && b < blocks)
+      v[c] = load_act4(x, row * ldx + (int64_t)b * kBlock + 4 * p, x_bf16 != 0,
+                       aligned != 0);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    int32_t q;
+    float s;
+    quantize_block8(v[c], true, &q, &s);
+    *(int32_t *)(qa + tile * 1024 + (8 * c + rr) * kBlock + 4 * p) = q;
+    if (p == 0) sa[tile * 32 + 8 * c + rr] = s;
   }
 }
 
@@ -893,7 +919,7 @@ hipError_t launch_quantize(const void *x, bool x_bf16, int64_t m, int64_t ldx,
       ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
   hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(threads, 256)), dim3(256),
                      0, s, x, x_bf16 ? 1 : 0, m, ldx, blocks, qa, ldq, sa, lds,
-                     blocks_pad, aligned, 0);
+                     blocks_pad, aligned);
   return hipGetLastError();
 }
 
@@ -901,13 +927,14 @@ hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
                                  int64_t ldx, int64_t cols, int8_t *qa,
                                  float *sa, int64_t blocks_pad, hipStream_t s) {
   const int64_t blocks = cols / kBlock;
-  const int64_t threads = m * blocks_pad * 8;
+  const int64_t tiles = (m + 31) / 32 * blocks_pad;
   const int64_t esz = x_bf16 ? 2 : 4;
   const int aligned =
       ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(threads, 256)), dim3(256),
-                     0, s, x, x_bf16 ? 1 : 0, m, ldx, blocks, qa, (int64_t)0, sa,
-                     (int64_t)0, blocks_pad, aligned, 1);
+  hipLaunchKernelGGL(quantize_tiles_kernel, dim3((unsigned)((tiles + 3) / 4)),
+                     dim3(256), 0, s, x, x_bf16 ? 1 : 0, m, ldx,
+                     (int32_t)blocks, (int32_t)blocks_pad, tiles, qa, sa,
+                     aligned);
   return hipGetLastError();
 }
 
