@@ -172,25 +172,37 @@ __device__ __forceinline__ float div127(float m) {
   return m == __builtin_inff() ? m : s;
 }
 
-// RN(1 / s).  For s in [2^-125, 2^126] v_rcp_f32 plus one Newton step with
-// FMA is exact (checked exhaustively over that range on gfx950 by the device
-// self-test); outside it -- where 1/s is subnormal or overflows -- the IEEE
-// division sequence runs instead.
+// RN(1 / s) for s in [2^-125, 2^126]: v_rcp_f32 plus one Newton step with
+// FMA is exact there (checked exhaustively on gfx950 by the device
+// self-test).  Outside that range -- where 1/s is subnormal or overflows --
+// only IEEE division is exact; recip_in_range reports which case holds.
+__device__ __forceinline__ bool recip_in_range(float s) {
+  return s >= 0x1p-125f && s <= 0x1p126f;
+}
+__device__ __forceinline__ float recip_fast(float s) {
+  const float y = __builtin_amdgcn_rcpf(s);
+  const float e = __builtin_fmaf(-s, y, 1.0f);
+  return __builtin_fmaf(e, y, y);
+}
 __device__ __forceinline__ float recip(float s) {
-  if (s >= 0x1p-125f && s <= 0x1p126f) {
-    const float y = __builtin_amdgcn_rcpf(s);
-    const float e = __builtin_fmaf(-s, y, 1.0f);
-    return __builtin_fmaf(e, y, y);
-  }
-  return 1.0f / s;
+  return recip_in_range(s) ? recip_fast(s) : 1.0f / s;
+}
+
+// Low byte of roundeven(x) for |x| < 2^22: adding 1.5 * 2^23 rounds to an
+// integer (round to nearest even) and leaves it, two's complement, in the
+// low mantissa bits.  A NaN yields 0, as the integer conversion does.
+__device__ __forceinline__ uint32_t round_byte(float x) {
+  return __builtin_bit_cast(uint32_t, x + 12582912.0f) & 0xffu;
 }
 
 // Quantizes 8 blocks per wave instruction: 8 lanes x float4 per block.
 // Q8Decode.cpp:83-120: sa = max|x|/127; inv = max==0 ? 0 : 1/sa;
-// q = (int8)(int32)roundeven(x*inv).
-__device__ __forceinline__ void quantize_block8(float4 v, bool valid,
-                                                int32_t *q_out, float *s_out) {
-  if (!valid) v = make_float4(0.f, 0.f, 0.f, 0.f);
+// q = (int8)(int32)roundeven(x*inv).  The fast form takes the reciprocal
+// from recip_fast and returns true in lanes whose scale is outside its
+// exact range (extreme magnitudes only); such a block must be redone with
+// quantize_block8.
+__device__ __forceinline__ bool quantize_block8_fast(float4 v, int32_t *q_out,
+                                                     float *s_out) {
   float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   // max over the 8 lanes of the block with DPP (no LDS round trips): swap
   // neighbours, swap pairs, then mirror each half-row (lane i <-> 7 - i).
@@ -198,13 +210,27 @@ __device__ __forceinline__ void quantize_block8(float4 v, bool valid,
   m = fmaxf(m, dpp_f32<0x4E>(m));
   m = fmaxf(m, dpp_f32<0x141>(m));
   const float s = div127(m);
-  const float inv = m == 0.0f ? 0.0f : recip(s);
-  const int q0 = (int)rintf(v.x * inv), q1 = (int)rintf(v.y * inv);
-  const int q2 = (int)rintf(v.z * inv), q3 = (int)rintf(v.w * inv);
-  *q_out = (int32_t)((uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                     ((uint32_t)(q2 & 0xff) << 16) |
-                     ((uint32_t)(q3 & 0xff) << 24));
+  const bool zero = m == 0.0f;
+  const float inv = zero ? 0.0f : recip_fast(s);
+  *q_out = (int32_t)(round_byte(v.x * inv) | (round_byte(v.y * inv) << 8) |
+                     (round_byte(v.z * inv) << 16) | (round_byte(v.w * inv) << 24));
   *s_out = s;  // the same in all 8 lanes of the block
+  return !zero && !recip_in_range(s);
+}
+__device__ __forceinline__ void quantize_block8(float4 v, bool valid,
+                                                int32_t *q_out, float *s_out) {
+  if (!valid) v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (__builtin_amdgcn_ballot_w64(quantize_block8_fast(v, q_out, s_out))) {
+    // rare: an extreme scale somewhere in the wave
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, dpp_f32<0xB1>(m));
+    m = fmaxf(m, dpp_f32<0x4E>(m));
+    m = fmaxf(m, dpp_f32<0x141>(m));
+    const float s = div127(m);
+    const float inv = m == 0.0f ? 0.0f : recip(s);
+    *q_out = (int32_t)(round_byte(v.x * inv) | (round_byte(v.y * inv) << 8) |
+                       (round_byte(v.z * inv) << 16) | (round_byte(v.w * inv) << 24));
+  }
 }
 
 // Four consecutive activations as f32: an f32 row (one float4 when 16 B
@@ -463,21 +489,35 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     // (blocks past `blocks` become zero).
     if (kRowFirst) {
       // One basic block (no conditional store), so the rounds interleave.
-      // Blocks past `blocks` were loaded as zeros.
+      // Blocks past `blocks` were loaded as zeros.  The fast reciprocal
+      // covers every scale but extreme ones; a block with such a scale
+      // (flagged per round) is redone exactly after the rounds.
+      auto row_value = [&](int u) {
+        return XB ? make_float4(bf16_to_float(xr[u].x & 0xffffu),
+                                bf16_to_float(xr[u].x >> 16),
+                                bf16_to_float(xr[u].y & 0xffffu),
+                                bf16_to_float(xr[u].y >> 16))
+                  : __builtin_bit_cast(float4, xr[u]);
+      };
+      bool slow = false;
 #pragma unroll
       for (int u = 0; u < XR; ++u) {
         const int t = u * 64 * W + (int)threadIdx.x;
         int32_t q;
         float sq;
-        const float4 v =
-            XB ? make_float4(bf16_to_float(xr[u].x & 0xffffu),
-                                   bf16_to_float(xr[u].x >> 16),
-                                   bf16_to_float(xr[u].y & 0xffffu),
-                                   bf16_to_float(xr[u].y >> 16))
-                     : __builtin_bit_cast(float4, xr[u]);
-        quantize_block8(v, true, &q, &sq);
+        slow |= quantize_block8_fast(row_value(u), &q, &sq);
         ((int32_t *)qa_l)[t] = q;
         sa_l[t >> 3] = sq;
+      }
+      if (__builtin_amdgcn_ballot_w64(slow)) {
+#pragma unroll
+        for (int u = 0; u < XR; ++u) {
+          const int t = u * 64 * W + (int)threadIdx.x;
+          int32_t q;
+          float sq;
+          quantize_block8(row_value(u), true, &q, &sq);
+          ((int32_t *)qa_l)[t] = q;
+        }
       }
     } else {
       constexpr int U = 4;
