@@ -51,6 +51,22 @@ def test_gemm_bitwise(ctx, oracle, m, n, k, epi):
     assert close(y, oracle.linear(x, p4, n, epilogue=other))
 
 
+def test_gemm_extreme_input_scales(ctx, oracle):
+    # Blocks with subnormal, tiny and huge scales and zero blocks in
+    # different rows: the tiled quantizer's exact-reciprocal fix-up.
+    rng = np.random.default_rng(11)
+    m, n, k = 70, 264, 2560
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[3, 0:32] *= np.float32(1e-41)
+    x[5, 64:96] *= np.float32(1e-36)
+    x[40, 128:160] *= np.float32(1e37)
+    x[69, 2528:2560] *= np.float32(3e-39)
+    x[33, :] = 0.0
+    p4 = oracle.pack_q8_0_p4(w)
+    assert bits_equal(gemm(ctx, p4, n, k, x), oracle.linear(x, p4, n, epilogue="fma"))
+
+
 def test_gemm_exact_operand_boundaries(ctx, oracle):
     # run_numeric.py:690-732 prefill case: M=19, N=136, K=288, exact operands,
     # zero last block of row 0, against a float64 matmul at 1e-5 / 1e-6.

@@ -77,6 +77,27 @@ def test_gemv_matches_scalar_reference_bitwise(ctx, oracle, k):
     assert close(y, oracle.linear(x, p4, n, epilogue="fma"))
 
 
+# Input rows whose blocks have extreme scales: subnormal (the reciprocal's
+# IEEE branch inside the GEMV's in-workgroup quantizer), tiny-normal, huge,
+# zero and mixed blocks, for the unrolled (2560, 9216), segmented and runtime
+# (3072) pass counts; the M = 1024 prefill path goes through the tiled
+# quantizer with the same rows.
+@pytest.mark.parametrize("k", [2560, 3072, 9216])
+def test_gemv_extreme_input_scales(ctx, oracle, k):
+    rng = np.random.default_rng(300 + k)
+    n = 264
+    w = weights(rng, n, k)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    x[0, 0:32] *= np.float32(1e-41)     # subnormal values, subnormal scale
+    x[0, 64:96] *= np.float32(1e-36)    # scale below 2^-125
+    x[0, 65] = np.float32(-1e-36)
+    x[0, 128:160] *= np.float32(1e37)   # scale above 2^126 / 127
+    x[0, 192:224] = 0.0
+    x[0, k - 32:] *= np.float32(3e-39)
+    y, p4 = run_linear(ctx, oracle, w, x)
+    assert bits_equal(y, oracle.linear(x, p4, n, epilogue="scalar"))
+
+
 def test_gemv_exact_operands(ctx, oracle):
     # run_numeric.py:690-732 decode boundary case: N=136, K=288, exact operands,
     # last block of x zero; float64 matmul of the exact values at 1e-5 / 1e-6.
