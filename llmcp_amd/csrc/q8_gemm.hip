@@ -152,13 +152,17 @@ struct Seg6 {
 // per SIMD; 4 waves: two workgroups per CU) is declared so that the kernel
 // stays within 256 VGPRs, which keeps the MFMA results in VGPRs where the
 // epilogue reads them (no accumulation-register round trips).
+// EPI: activation code in bits 0-1, bf16 output in bit 2, the SwiGLU
+// multiply by `mul` in bit 3 (compile time: the epilogue is inlined for
+// every accumulator element).
 template <int WM, int WN, int NST, bool FMA, int SEG, int EPI>
 __global__ __launch_bounds__(64 * WM * WN)
 __attribute__((amdgpu_waves_per_eu(WM * WN >= 12 ? 3 : 2)))
 void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
                  int32_t row_tiles, int32_t nblk, const uint8_t *__restrict__ w,
                  int64_t n_rows, int64_t m_rows, int32_t passes, int32_t m_tiles,
-                 int32_t n_tiles, void *__restrict__ y, int64_t ldy) {
+                 int32_t n_tiles, void *y, int64_t ldy, const float *mul,
+                 int64_t ldg) {
   typedef GemmStage<WM, WN, SEG> St;
   static_assert(NST == 2 || NST == 4, "stage buffers");
   constexpr int W = WM * WN;
@@ -423,7 +427,13 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   for (int v = 0; v < 16; ++v) {
     const int64_t m = m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
     if (m < m_rows && n < n_rows) {
-      const float o = activate(acc[v], EPI & 3);
+      float o = activate(acc[v], EPI & 3);
+      if constexpr ((EPI & 8) != 0) {
+        // SwiGLU: times the gate's activated output (FuseSiluMul's mul)
+        const float g = mul[m * ldg + n];
+        o = (EPI & 4) != 0 ? bf16_to_float(float_to_bf16(g)) * bf16_to_float(float_to_bf16(o))
+                           : g * o;
+      }
       if constexpr ((EPI & 4) != 0)
         ((uint16_t *)y)[m * ldy + n] = float_to_bf16(o);
       else
@@ -432,38 +442,15 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   }
 }
 
-// SwiGLU multiply of the prefill path: gate (SiLU applied) and up in f32.
-// f32: h = g * u in place.  bf16 result: each linear's output rounds to
-// bf16 first, then the bf16 multiply (FuseSiluMul on bf16 tensors).
-__global__ void mul_kernel(float *__restrict__ g, const float *__restrict__ u,
-                           uint16_t *__restrict__ out_bf16, int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= count) return;
-  if (out_bf16) {
-    const float gb = bf16_to_float(float_to_bf16(g[i]));
-    const float ub = bf16_to_float(float_to_bf16(u[i]));
-    out_bf16[i] = float_to_bf16(gb * ub);
-  } else {
-    g[i] = g[i] * u[i];
-  }
-}
-
 }  // namespace
-
-hipError_t launch_mul(float *g, const float *u, uint16_t *out_bf16,
-                      int64_t count, hipStream_t s) {
-  if (count == 0) return hipSuccess;
-  hipLaunchKernelGGL(mul_kernel, dim3((unsigned)((count + 255) / 256)),
-                     dim3(256), 0, s, g, u, out_bf16, count);
-  return hipGetLastError();
-}
 
 template <int WM, int WN, int NST, bool FMA, int SEG, int EPI>
 static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
                           int32_t n_tiles, unsigned grid, hipStream_t s) {
   hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI>), dim3(grid),
                      dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
-                     l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy);
+                     l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
+                     l.mul, l.ldg);
 }
 
 template <int WM, int WN, int NST, bool FMA, int SEG>
@@ -473,6 +460,10 @@ static void launch_gemm_e(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
   // accumulator element, runtime switches bloat the kernel and slow it
 #define LLMCP_GEMM_EPI(E) \
   case E: return launch_gemm_k<WM, WN, NST, FMA, SEG, E>(l, passes, m_tiles, n_tiles, grid, s);
+  if (l.mul) {  // the SwiGLU up linear: no activation of its own
+    if (l.y_bf16) return launch_gemm_k<WM, WN, NST, FMA, SEG, 12>(l, passes, m_tiles, n_tiles, grid, s);
+    return launch_gemm_k<WM, WN, NST, FMA, SEG, 8>(l, passes, m_tiles, n_tiles, grid, s);
+  }
   switch ((l.activation & 3) | (l.y_bf16 ? 4 : 0)) {
     LLMCP_GEMM_EPI(1) LLMCP_GEMM_EPI(2) LLMCP_GEMM_EPI(3) LLMCP_GEMM_EPI(4)
     LLMCP_GEMM_EPI(5) LLMCP_GEMM_EPI(6) LLMCP_GEMM_EPI(7)

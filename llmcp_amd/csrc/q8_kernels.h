@@ -74,6 +74,11 @@ struct GemmLaunch {
   int64_t ldy = 0;
   int activation = 0;            // llmcp_q8_activation
   bool fma = true;             // epilogue: fma (SDOT GEMM) or mul+add (scalar)
+  // Non-null: the SwiGLU multiply in the epilogue, y = g * act(acc) with g
+  // f32 [m, ldg] (the gate linear's activated output; it may alias y when
+  // y is f32).  A bf16 result rounds both factors to bf16 first.
+  const float *mul = nullptr;
+  int64_t ldg = 0;
 };
 
 hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);
@@ -85,11 +90,6 @@ hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);
 hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
                                  int64_t ldx, int64_t cols, int8_t *qa,
                                  float *sa, int64_t blocks_pad, hipStream_t s);
-
-// SwiGLU multiply of the prefill path from f32 gate (SiLU applied) and up:
-// f32 h = g * u in place in g, or bf16 out = bf16(bf16(g) * bf16(u)).
-hipError_t launch_mul(float *g, const float *u, uint16_t *out_bf16,
-                      int64_t count, hipStream_t s);
 
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             const uint8_t *table, int64_t rows, int64_t cols,

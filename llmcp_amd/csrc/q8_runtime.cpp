@@ -631,8 +631,9 @@ static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
 
 // Prefill: quantize all M rows once (zero-padded to whole units), then the
 // int8-MFMA GEMM.  The activation scratch grows on first use for a larger M.
-static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
-                       const Rows &out, int activation) {
+// Q8_1 of the input rows into the context's scratch (the GEMM's tiled
+// layout).  The scratch grows on first use for a larger M.
+static int gemm_quantize(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w) {
   const int64_t m = in.rows;
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   const int64_t row_tiles = (m + 31) / 32;  // the tiled layout pads M to 32
@@ -642,10 +643,19 @@ static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
   hipError_t e = launch_quantize_tiled(in.data, in.bf16, m, in.ld, w->cols,
                                        ctx->qa, ctx->sa, nblk, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  return LLMCP_Q8_OK;
+}
+
+// int8-MFMA GEMM of the quantized rows (gemm_quantize) against w.  `mul`
+// (nullable, f32 [m, ldg]) turns the epilogue into the SwiGLU multiply.
+static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
+                       const Rows &out, int activation, const float *mul,
+                       int64_t ldg) {
+  const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   GemmLaunch g;
   g.qa = ctx->qa;
   g.sa = ctx->sa;
-  g.row_tiles = (int32_t)row_tiles;
+  g.row_tiles = (int32_t)((m + 31) / 32);
   g.nblk = (int32_t)nblk;
   g.w = w->dev;
   g.rows = w->rows;
@@ -656,9 +666,18 @@ static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
   g.ldy = out.ld;
   g.activation = activation;
   g.fma = ctx->gemm_fma;
-  e = launch_gemm(g, ctx->stream);
+  g.mul = mul;
+  g.ldg = ldg;
+  hipError_t e = launch_gemm(g, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "gemm launch");
   return LLMCP_Q8_OK;
+}
+
+static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
+                       const Rows &out, int activation) {
+  int rc = gemm_quantize(ctx, in, w);
+  if (rc) return rc;
+  return gemm_launch(ctx, in.rows, w, out, activation, nullptr, 0);
 }
 
 static int check_linear_shapes(const Rows &in, const Tensor *w,
@@ -722,31 +741,24 @@ static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if (m == 1) return gemv_common(ctx, in, wg, wu, out, LLMCP_Q8_ACT_NONE, nullptr);
   if (execution_mode == LLMCP_Q8_DECODE)
     return fail(LLMCP_Q8_DECLINED, "decode SwiGLU requires M == 1");
-  // Prefill: gate GEMM with SiLU, up GEMM, then the multiply
-  // (MulOpLowering, LowerToLinalg.cpp:377-393).  f32: gate straight into
-  // the output, up into scratch.  bf16: both in f32 scratch, the multiply
-  // rounds each to bf16 first.
-  if (out.ld != wg->rows)
-    return fail(LLMCP_Q8_DECLINED, "prefill SwiGLU output must be dense");
-  const uint64_t n = (uint64_t)(m * wg->rows);
-  rc = grow(ctx, ctx->up, ctx->up_bytes, (out.bf16 ? 2 : 1) * n * 4,
-            "prefill SwiGLU scratch");
-  if (rc) return rc;
-  Rows g = out, u = out;
-  u.data = ctx->up;
-  u.bf16 = false;
-  u.ld = wg->rows;
+  // Prefill: the input quantized once; the gate GEMM with SiLU, then the up
+  // GEMM whose epilogue does the multiply (MulOpLowering,
+  // LowerToLinalg.cpp:377-393) with the gate's output.  f32: the gate goes
+  // straight into the output and the up GEMM multiplies it in place.  bf16:
+  // the gate goes to f32 scratch and the multiply rounds both factors to
+  // bf16 first.
+  Rows g = out;
   if (out.bf16) {
-    g = u;
-    g.data = ctx->up + n;
+    rc = grow(ctx, ctx->up, ctx->up_bytes, (uint64_t)(m * wg->rows) * 4,
+              "prefill SwiGLU scratch");
+    if (rc) return rc;
+    g.data = ctx->up;
+    g.bf16 = false;
+    g.ld = wg->rows;
   }
-  if ((rc = gemm_common(ctx, in, wg, g, LLMCP_Q8_ACT_SILU))) return rc;
-  if ((rc = gemm_common(ctx, in, wu, u, LLMCP_Q8_ACT_NONE))) return rc;
-  hipError_t e = launch_mul((float *)g.data, (const float *)u.data,
-                            out.bf16 ? (uint16_t *)out.data : nullptr,
-                            (int64_t)n, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "mul launch");
-  return LLMCP_Q8_OK;
+  if ((rc = gemm_quantize(ctx, in, wg))) return rc;
+  if ((rc = gemm_launch(ctx, m, wg, g, LLMCP_Q8_ACT_SILU, nullptr, 0))) return rc;
+  return gemm_launch(ctx, m, wu, out, LLMCP_Q8_ACT_NONE, (const float *)g.data, g.ld);
 }
 
 static int lm_head_impl(llmcp_q8_ctx *ctx, const Rows &in,
