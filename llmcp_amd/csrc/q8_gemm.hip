@@ -324,6 +324,20 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
 #pragma unroll
   for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  // SwiGLU: this lane's 16 gate values, loaded at the start of the last
+  // group of stages so that their latency hides behind it (indices clamped,
+  // no branch: a branch around a load would disturb the DMA wait tracking).
+  float gpre[16];
+  auto prefetch_gate = [&]() __attribute__((always_inline)) {
+    if constexpr ((EPI & 8) != 0) {
+      const int64_t nc = min(n0 + 32 * wn + li, n_rows - 1);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t mc = min(m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3), m_rows - 1);
+        gpre[v] = mul[mc * ldg + nc];
+      }
+    }
+  };
   const int bsw = (lane >> 2) & 3;  // swizzle of this lane's weight run
 
   // Scale tiles of blocks kb+2k (lanes 0-31) and kb+2k+1 (lanes 32-63).
@@ -408,7 +422,10 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
 #pragma unroll
   for (int i = 0; i < NST - 1; ++i) issue(min(i, last), stage(i));
 
-  for (int s0 = 0; s0 < stages; s0 += NST) {
+  // One group of NST stages (static buffer indices).  With the SwiGLU
+  // multiply the last group is peeled off: it also prefetches the gate values.
+  auto group = [&](int s0, auto LAST) __attribute__((always_inline)) {
+    if constexpr (decltype(LAST)::value) prefetch_gate();
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
       const int s = s0 + i;
@@ -418,6 +435,12 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
       // every wave is past stage s-1: its buffer takes stage s+NST-1
       compute(s, stage(i), min(s + NST - 1, last), stage((i + NST - 1) % NST));
     }
+  };
+  if constexpr ((EPI & 8) != 0) {
+    for (int s0 = 0; s0 < stages - NST; s0 += NST) group(s0, std::false_type{});
+    group(stages - NST, std::true_type{});
+  } else {
+    for (int s0 = 0; s0 < stages; s0 += NST) group(s0, std::false_type{});
   }
   // no DMA may land in LDS after the workgroup has released it
   wait_vmcnt<0>();
@@ -430,7 +453,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
       float o = activate(acc[v], EPI & 3);
       if constexpr ((EPI & 8) != 0) {
         // SwiGLU: times the gate's activated output (FuseSiluMul's mul)
-        const float g = mul[m * ldg + n];
+        const float g = gpre[v];
         o = (EPI & 4) != 0 ? bf16_to_float(float_to_bf16(g)) * bf16_to_float(float_to_bf16(o))
                            : g * o;
       }
