@@ -44,9 +44,9 @@ struct GemvLaunch {
   int64_t cols = 0;              // K
   int nmat = 1;                  // 2 = fused SwiGLU (gate, up)
   int activation = 0;            // llmcp_q8_activation (nmat == 1 only)
-  unsigned long long *keys = nullptr;  // non-null: fused argmax partials,
-  int64_t *argmax_out = nullptr;       // gemv_workgroups(rows) entries
-};
+  unsigned long long *keys = nullptr;  // non-null: fused argmax into these
+  int64_t *argmax_out = nullptr;       // kArgmaxSlots slots, zero on entry
+};                                     // and left zero
 
 // One-matrix GEMVs with at most this many lane groups quantize the input
 // row inside the kernel (once per workgroup); wider ones (every workgroup
@@ -56,7 +56,15 @@ constexpr int64_t kInLoopQuantMaxGroups = 4096;
 bool gemv_quantizes_input(int64_t rows, int nmat);
 
 hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s);
-int64_t gemv_workgroups(int64_t rows);
+
+// The argmax GEMV folds each workgroup's (value, index) key into one of
+// kArgmaxSlots slots with an atomic max; the reduce kernel swaps them back
+// to zero.  More slots than this left same-address atomics contending.
+constexpr int kArgmaxSlots = 2048;
+// Reduces the slots into *out (the first maximum's index) and clears them;
+// out == nullptr only clears.
+hipError_t launch_argmax_reduce(unsigned long long *slots, int64_t *out,
+                                hipStream_t s);
 
 // Prefill GEMM on int8 MFMA.  qa/sa: Q8_1 activations [m, ldq] / [m, lds],
 // zero-padded to passes*16 blocks (launch_quantize with blocks_pad).

@@ -368,6 +368,47 @@ __device__ __forceinline__ unsigned long long argmax_key(float v,
          (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
+__device__ __forceinline__ unsigned long long max_u64(unsigned long long a,
+                                                      unsigned long long b) {
+  return a > b ? a : b;
+}
+
+// DPP move of a 64-bit value (both halves with the same control; lanes with
+// no source read 0, the identity of an unsigned max).
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(
+      0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(
+      0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+// Maximum over the wave, returned in every lane: quad swaps, row shifts by
+// 4 and 8 (lane 15 of each row holds the row's maximum), then row_bcast:15
+// and row_bcast:31 carry it into lane 63.
+__device__ __forceinline__ unsigned long long wave_max_u64(
+    unsigned long long v) {
+  v = max_u64(v, dpp_u64<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = max_u64(v, dpp_u64<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = max_u64(v, dpp_u64<0x114>(v));  // row_shr:4
+  v = max_u64(v, dpp_u64<0x118>(v));  // row_shr:8
+  v = max_u64(v, dpp_u64<0x142>(v));  // row_bcast:15
+  v = max_u64(v, dpp_u64<0x143>(v));  // row_bcast:31
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), 63);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+// Folds a workgroup's best key into slot blockIdx mod kArgmaxSlots.  The
+// atomic returns nothing and orders nothing: the reduce kernel that reads
+// the slots runs after this kernel has completed.
+__device__ __forceinline__ void argmax_fold(unsigned long long *slots,
+                                            unsigned long long key) {
+  (void)__hip_atomic_fetch_max(slots + (blockIdx.x & (kArgmaxSlots - 1)), key,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Waves per workgroup of an IN_WG GEMV with a compile-time pass count.  The
 // workgroup quantizes the input row once (pc * 16 blocks, 8 lanes per block,
 // row_rounds float4 loads per lane), so wider workgroups share that work.
@@ -713,7 +754,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
       key = other > key ? other : key;
     }
     if (W == 1) {
-      if (lane == 0) a.keys[blockIdx.x] = key;
+      if (lane == 0) argmax_fold(a.keys, key);
     } else {
       if (lane == 0) key_l[wave] = key;
       __syncthreads();
@@ -721,40 +762,33 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         unsigned long long best = key_l[0];
 #pragma unroll
         for (int w = 1; w < W; ++w) best = key_l[w] > best ? key_l[w] : best;
-        a.keys[blockIdx.x] = best;
+        argmax_fold(a.keys, best);
       }
     }
   }
 }
 
-// Second stage of the fused argmax: one workgroup reduces the per-workgroup
-// keys and writes the index of the first maximum.  Loads are issued 16 deep
-// per thread so the pass costs one memory latency.
+// Second stage of the fused argmax: one workgroup of 1024 threads takes the
+// kArgmaxSlots slots (swapping in 0, so the slots are clear for the next
+// call without a memset) and writes the index of the first maximum.  With
+// out == nullptr it only clears the slots.
 __global__ __launch_bounds__(1024) void argmax_reduce_kernel(
-    const unsigned long long *__restrict__ keys, int64_t n, int64_t *out) {
+    unsigned long long *slots, int64_t *out) {
+  static_assert(kArgmaxSlots % 1024 == 0, "slots per thread");
   __shared__ unsigned long long part[16];
   unsigned long long best = 0ull;
-  for (int64_t i0 = 0; i0 < n; i0 += 16 * 1024) {
-    unsigned long long k[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int64_t i = i0 + u * 1024 + threadIdx.x;
-      k[u] = i < n ? keys[i] : 0ull;
-    }
-#pragma unroll
-    for (int u = 0; u < 16; ++u) best = k[u] > best ? k[u] : best;
-  }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const unsigned long long other = __shfl_xor(best, off);
-    best = other > best ? other : best;
-  }
+  for (int u = 0; u < kArgmaxSlots / 1024; ++u)
+    best = max_u64(best, __hip_atomic_exchange(slots + u * 1024 + threadIdx.x,
+                                               0ull, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT));
+  best = wave_max_u64(best);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = best;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
-      best = part[w] > best ? part[w] : best;
-    *out = (int64_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+  if (threadIdx.x < 64) {
+    best = wave_max_u64(threadIdx.x < 16 ? part[threadIdx.x] : 0ull);
+    if (threadIdx.x == 0 && out)
+      *out = (int64_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
   }
 }
 
@@ -899,19 +933,6 @@ hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t s) {
   }
 }
 
-// Workgroup width of a launch (as launch_gemv_w picks it).
-static int gemv_waves(int64_t passes, int in, int nmat) {
-  if (in == IN_WG) {
-    switch (passes) {
-      case 1: case 2: case 3: case 5: case 8: case 18:
-        return wg_waves(nmat, (int)passes);
-      default:
-        return wg_waves(nmat, 0);
-    }
-  }
-  return 4;
-}
-
 }  // namespace
 
 hipError_t launch_repack(const uint8_t *p4, uint8_t *out, int64_t rows,
@@ -982,9 +1003,6 @@ bool gemv_quantizes_input(int64_t rows, int nmat) {
   return nmat == 2 || rows / kLanes <= kInLoopQuantMaxGroups;
 }
 
-int64_t gemv_workgroups(int64_t rows) {
-  return rows / kLanes;  // one wave per workgroup is the widest grid
-}
 
 // The compile-time variants the C ABI needs (V bits as in gemv_kernel):
 // SwiGLU f32 or bf16 in and out; the argmax GEMV (lm_head) with f32 logits
@@ -1040,13 +1058,16 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
   a.act = l.activation;
   const int in = l.x ? IN_WG : IN_PRE;
   if (l.x && (uintptr_t)l.x % (l.x_bf16 ? 8 : 16)) return hipErrorInvalidValue;
-  const int waves = gemv_waves(a.passes, in, l.nmat);
   hipError_t e = in == IN_WG ? launch_gemv_in<IN_WG>(a, l, s)
                              : launch_gemv_in<IN_PRE>(a, l, s);
   if (e != hipSuccess || !l.keys) return e;
-  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(1024), 0, s,
-                     (const unsigned long long *)l.keys,
-                     (a.groups + waves - 1) / waves, l.argmax_out);
+  return launch_argmax_reduce(l.keys, l.argmax_out, s);
+}
+
+hipError_t launch_argmax_reduce(unsigned long long *slots, int64_t *out,
+                                hipStream_t s) {
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(1024), 0, s, slots,
+                     out);
   return hipGetLastError();
 }
 

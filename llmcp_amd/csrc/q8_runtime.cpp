@@ -71,13 +71,14 @@ struct llmcp_q8_ctx {
   int32_t *err_flag = nullptr;
   // Workspace, sized when weights are registered so that decode-time calls
   // (and graph capture) never allocate: the quantized input row, its scales
-  // and the per-workgroup argmax keys of the lm_head.
+  // and the lm_head's argmax slots (kArgmaxSlots, zero between calls;
+  // keys_dirty when a call may have left them otherwise).
   int8_t *qa = nullptr;
   float *sa = nullptr;
   unsigned long long *keys = nullptr;
+  bool keys_dirty = false;
   uint64_t qa_bytes = 0;
   uint64_t sa_bytes = 0;
-  uint64_t keys_bytes = 0;
   // Fused MLP: the SwiGLU output h when the caller passes no buffer for it.
   float *hf = nullptr;
   float *up = nullptr;  // prefill SwiGLU: the up projection
@@ -160,20 +161,32 @@ int grow(llmcp_q8_ctx *ctx, T *&ptr, uint64_t &have, uint64_t need,
   return LLMCP_Q8_OK;
 }
 
-int ensure_scratch(llmcp_q8_ctx *ctx, uint64_t qa_bytes, uint64_t sa_bytes,
-                   uint64_t keys_bytes = 0) {
+int ensure_scratch(llmcp_q8_ctx *ctx, uint64_t qa_bytes, uint64_t sa_bytes) {
   int rc = grow(ctx, ctx->qa, ctx->qa_bytes, qa_bytes, "activation scratch");
   if (!rc) rc = grow(ctx, ctx->sa, ctx->sa_bytes, sa_bytes, "scale scratch");
-  if (!rc) rc = grow(ctx, ctx->keys, ctx->keys_bytes, keys_bytes, "argmax keys");
   return rc;
+}
+
+// The argmax slots, allocated and zeroed once (before any graph capture).
+int ensure_argmax_slots(llmcp_q8_ctx *ctx) {
+  if (ctx->keys) return LLMCP_Q8_OK;
+  const size_t bytes = (size_t)kArgmaxSlots * sizeof(unsigned long long);
+  if (hipMalloc((void **)&ctx->keys, bytes) != hipSuccess) {
+    ctx->keys = nullptr;
+    return fail(LLMCP_Q8_ENOMEM, "argmax slots of %llu bytes",
+                (unsigned long long)bytes);
+  }
+  HIP_TRY(hipMemsetAsync(ctx->keys, 0, bytes, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return LLMCP_Q8_OK;
 }
 
 // Workspace a one-row call against a [rows, cols] weight needs, including
 // the f32 buffer for h should its output feed the fused MLP's down GEMV.
 int ensure_decode_scratch(llmcp_q8_ctx *ctx, int64_t rows, int64_t cols) {
   const uint64_t nblk = (uint64_t)passes_for(cols) * kPassBlocks;
-  int rc = ensure_scratch(ctx, nblk * kBlock, nblk * 4,
-                          (uint64_t)gemv_workgroups(rows) * 8u);
+  int rc = ensure_scratch(ctx, nblk * kBlock, nblk * 4);
+  if (!rc) rc = ensure_argmax_slots(ctx);
   if (rc || rows % kBlock) return rc;
   return grow(ctx, ctx->hf, ctx->hf_bytes, (uint64_t)rows * 4, "mlp hidden");
 }
@@ -623,9 +636,18 @@ static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
   if (argmax_dev) {
     l.keys = ctx->keys;
     l.argmax_out = argmax_dev;
+    // a failed call may have folded keys without the reduce that clears them
+    if (ctx->keys_dirty) {
+      hipError_t e = launch_argmax_reduce(ctx->keys, nullptr, ctx->stream);
+      if (e != hipSuccess) return hip_fail(e, "argmax clear launch");
+      ctx->keys_dirty = false;
+    }
   }
   hipError_t e = launch_gemv(l, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "gemv launch");
+  if (e != hipSuccess) {
+    if (argmax_dev) ctx->keys_dirty = true;
+    return hip_fail(e, "gemv launch");
+  }
   return LLMCP_Q8_OK;
 }
 

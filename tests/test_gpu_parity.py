@@ -262,6 +262,29 @@ def test_lm_head_argmax_and_ties(ctx, oracle):
         ctx.release(t)
 
 
+def test_lm_head_argmax_back_to_back(ctx, oracle):
+    # Calls queued without a sync in between, alternating two rows whose
+    # maxima differ by ~100x: a key left over from one call would win the
+    # next one.  4096 x 2560 folds 1024 workgroups into the slots; 248320 rows
+    # (test_lm_head_full_vocab) put several workgroups on each slot.
+    rng = np.random.default_rng(15)
+    v, k = 4096, 2560
+    p4 = oracle.pack_q8_0_p4(weights(rng, v, k))
+    t = ctx.upload_p4(p4, v, k)
+    x1 = rng.standard_normal((1, k)).astype(np.float32)
+    x2 = (-0.01 * x1).astype(np.float32)
+    xs = [ctx.to_device(x1), ctx.to_device(x2)]
+    expect = [oracle.argmax(oracle.linear(x, p4, v)) for x in (x1, x2)]
+    assert expect[0] != expect[1]
+    ld = ctx.alloc(v * 4)
+    ams = [ctx.alloc(8) for _ in range(6)]
+    for i, am in enumerate(ams):
+        ctx.lm_head(xs[i % 2], t, ld, 1, argmax=am)
+    got = [int(ctx.to_host(am, (1,), np.int64)[0]) for am in ams]
+    assert got == [expect[i % 2] for i in range(6)]
+    ctx.release(t)
+
+
 def test_lm_head_full_vocab(ctx, oracle):
     # Config 3: tied 248320 x 2560 table (0.67 GB of Q8_0), device-synthesized.
     v, k = 248320, 2560
