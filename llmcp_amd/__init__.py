@@ -411,6 +411,9 @@ class Context:
     def graph_launch(self, g):
         check(lib().llmcp_q8_graph_launch(self.handle, g))
 
+    def graph_destroy(self, g):
+        check(lib().llmcp_q8_graph_destroy(g))
+
 
 def pack_p4_host(w):
     """Host llmcp-pack (quantizeTensorQ8_0Packed) of an f32 [N,K] matrix."""

@@ -285,6 +285,44 @@ def test_lm_head_argmax_back_to_back(ctx, oracle):
     ctx.release(t)
 
 
+def test_device_resident_token_loop(ctx, oracle):
+    # The decode loop's tail on the device: the embedding gather reads the
+    # token id the previous lm_head's argmax wrote, with no host round trip
+    # between steps (the 1 MB of logits and the id stay in HBM).  Separate
+    # embedding and head tables so the ids keep moving.  Run eagerly, then as
+    # one captured step replayed, checking every id against the oracle chain.
+    rng = np.random.default_rng(16)
+    v, k = 4096, 2560
+    pe = oracle.pack_q8_0_p4(weights(rng, v, k))
+    pw = oracle.pack_q8_0_p4(weights(rng, v, k))
+    te, tw = ctx.upload_p4(pe, v, k), ctx.upload_p4(pw, v, k)
+    chain = [7]
+    for _ in range(6):
+        x = oracle.embedding(np.array(chain[-1:], np.int64), pe, k)
+        chain.append(int(oracle.argmax(oracle.linear(x, pw, v))))
+    assert len(set(chain)) == len(chain)
+    xd, ld = ctx.alloc(k * 4), ctx.alloc(v * 4)
+    ids = [ctx.to_device(np.array([chain[0]], np.int64))]
+    ids += [ctx.alloc(8) for _ in range(6)]
+    for i in range(6):
+        ctx.embedding(ids[i], 1, te, xd)
+        ctx.lm_head(xd, tw, ld, 1, argmax=ids[i + 1])
+    got = [int(ctx.to_host(t, (1,), np.int64)[0]) for t in ids]
+    assert got == chain
+    am = ctx.to_device(np.array([chain[0]], np.int64))
+    ctx.graph_begin()
+    ctx.embedding(am, 1, te, xd)
+    ctx.lm_head(xd, tw, ld, 1, argmax=am)
+    g = ctx.graph_end()
+    for i in range(6):
+        ctx.graph_launch(g)
+        assert int(ctx.to_host(am, (1,), np.int64)[0]) == chain[i + 1]
+    ctx.graph_destroy(g)
+    assert ctx.check_flag() == 0
+    ctx.release(te)
+    ctx.release(tw)
+
+
 def test_lm_head_full_vocab(ctx, oracle):
     # Config 3: tied 248320 x 2560 table (0.67 GB of Q8_0), device-synthesized.
     v, k = 248320, 2560
