@@ -275,6 +275,22 @@ int llmcp_q8_ctx_check(llmcp_q8_ctx *ctx, int32_t *flag);
  * from IEEE division (0 expected).  Synchronous; about 4e9 evaluations. */
 int llmcp_q8_selftest_quantizer(llmcp_q8_ctx *ctx, uint64_t *mismatches);
 
+/* Device self-test of the f32 exp inside the silu / sigmoid / softplus
+ * epilogues (no counterpart in the reference; it lets a host pin that exp
+ * against its own over every float input).  The device evaluates exp for
+ * every non-NaN float v.  An exp accurate to 2^-46 can round differently from
+ * the correctly rounded value only where exp(v) lies within 2^-46 of a change
+ * of float rounding; counts[0] is the number of such inputs, and the first
+ * `cap` of them are written to inputs[] with the library's result bits in
+ * results[] (*stored of them).  counts[1] is the number of inputs where the
+ * library's exp differs from the device math library's exp(double) rounded
+ * to float, counts[2] those of them outside the listed set (0 expected), and
+ * counts[3] the largest difference between the library's f64 exp and the
+ * device math library's, in units in the last place of the latter, over
+ * |v| <= 100.  Host buffers; synchronous; about 4e9 evaluations. */
+int llmcp_q8_selftest_exp(llmcp_q8_ctx *ctx, uint64_t counts[4], float *inputs,
+                          uint32_t *results, int64_t cap, int64_t *stored);
+
 /* ---------------------------------------------------- offline packing -- */
 
 /* quantizeTensorQ8_0Packed (lib/Model/Quantization.cpp:165-214) on the host:

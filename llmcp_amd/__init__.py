@@ -69,7 +69,7 @@ EXPORTS = [
     "llmcp_q8_event_destroy", "llmcp_q8_event_record",
     "llmcp_q8_event_elapsed_ms", "llmcp_q8_graph_begin", "llmcp_q8_graph_end",
     "llmcp_q8_graph_launch", "llmcp_q8_graph_destroy",
-    "llmcp_q8_device_bytes", "llmcp_q8_selftest_quantizer",
+    "llmcp_q8_device_bytes", "llmcp_q8_selftest_quantizer", "llmcp_q8_selftest_exp",
     "llmcp_q8_linear_bf16", "llmcp_q8_swiglu_bf16", "llmcp_q8_mlp_bf16",
     "llmcp_q8_lm_head_bf16", "llmcp_q8_embedding_bf16",
     "_mlir_ciface_llmcp_q8_linear_bf16", "_mlir_ciface_llmcp_q8_swiglu_bf16",
@@ -135,6 +135,8 @@ def lib():
         "llmcp_q8_graph_destroy": (I, [P]),
         "llmcp_q8_device_bytes": (U64, [P, P]),
         "llmcp_q8_selftest_quantizer": (I, [P, ctypes.POINTER(U64)]),
+        "llmcp_q8_selftest_exp": (I, [P, ctypes.POINTER(U64), P, P, ctypes.c_int64,
+                                      ctypes.POINTER(ctypes.c_int64)]),
         "llmcp_q8_linear_bf16": (I, [P, P, P, P, I32, I32]),
         "llmcp_q8_swiglu_bf16": (I, [P, P, P, P, P, I32]),
         "llmcp_q8_mlp_bf16": (I, [P, P, P, P, P, P, P, I32]),
@@ -384,6 +386,20 @@ class Context:
         n = ctypes.c_uint64(0)
         check(lib().llmcp_q8_selftest_quantizer(self.handle, ctypes.byref(n)))
         return n.value
+
+    def selftest_exp(self, cap=1 << 16):
+        """Exhaustive device check of the epilogues' f32 exp: returns
+        (counts, inputs, result_bits) -- counts = (inputs near a float
+        rounding change, differences from the device math library's
+        exp(double), those differences outside the listed inputs, largest
+        f64 difference from that library's exp in its ulps)."""
+        counts = (ctypes.c_uint64 * 4)()
+        xs = np.zeros(cap, np.float32)
+        rs = np.zeros(cap, np.uint32)
+        k = ctypes.c_int64(0)
+        check(lib().llmcp_q8_selftest_exp(self.handle, counts, xs.ctypes.data,
+                                          rs.ctypes.data, cap, ctypes.byref(k)))
+        return tuple(int(c) for c in counts), xs[:k.value], rs[:k.value]
 
     # ---- timing
     def event(self):

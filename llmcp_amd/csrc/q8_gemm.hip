@@ -446,11 +446,14 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   wait_vmcnt<0>();
 
   const int64_t n = n0 + 32 * wn + li;
+  // the activation over all 16 values (rows or columns past the end too,
+  // whose results are not stored): one straight-line sequence
+  activate_array(acc, EPI & 3);
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int64_t m = m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
     if (m < m_rows && n < n_rows) {
-      float o = activate(acc[v], EPI & 3);
+      float o = acc[v];
       if constexpr ((EPI & 8) != 0) {
         // SwiGLU: times the gate's activated output (FuseSiluMul's mul)
         const float g = gpre[v];

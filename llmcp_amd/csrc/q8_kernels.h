@@ -31,6 +31,8 @@ hipError_t launch_quantize(const void *x, bool x_bf16, int64_t m, int64_t ldx,
 // Exhaustive device check of the quantizer's division identities; adds the
 // number of mismatching inputs to *bad.
 hipError_t launch_selftest_quantizer(unsigned long long *bad, hipStream_t s);
+hipError_t launch_selftest_exp(unsigned long long *out, float *inputs,
+                               uint32_t *results, uint32_t cap, hipStream_t s);
 
 struct GemvLaunch {
   const void *x = nullptr;       // input row (f32 16 B / bf16 8 B aligned),

@@ -172,18 +172,7 @@ __device__ __forceinline__ float div127(float m) {
   return m == __builtin_inff() ? m : s;
 }
 
-// RN(1 / s) for s in [2^-125, 2^126]: v_rcp_f32 plus one Newton step with
-// FMA is exact there (checked exhaustively on gfx950 by the device
-// self-test).  Outside that range -- where 1/s is subnormal or overflows --
-// only IEEE division is exact; recip_in_range reports which case holds.
-__device__ __forceinline__ bool recip_in_range(float s) {
-  return s >= 0x1p-125f && s <= 0x1p126f;
-}
-__device__ __forceinline__ float recip_fast(float s) {
-  const float y = __builtin_amdgcn_rcpf(s);
-  const float e = __builtin_fmaf(-s, y, 1.0f);
-  return __builtin_fmaf(e, y, y);
-}
+// recip_in_range / recip_fast (RN(1 / s) on [2^-125, 2^126]): q8_device.h.
 __device__ __forceinline__ float recip(float s) {
   return recip_in_range(s) ? recip_fast(s) : 1.0f / s;
 }
@@ -273,6 +262,56 @@ __global__ void selftest_quant_kernel(uint32_t lo, uint32_t hi,
   const unsigned long long mask = __ballot(miss);
   if ((threadIdx.x & 63) == 0 && mask)
     atomicAdd(bad, (unsigned long long)__popcll(mask));
+}
+
+// Exhaustive check of exp_f32 over the float bit patterns [lo, hi) (NaN
+// inputs skipped).  out[0] counts inputs whose exp y lies within 2^-46
+// (relative) of a change of float rounding -- y(1-2^-46) and y(1+2^-46)
+// round to different floats -- and the first `cap` of them are stored with
+// exp_f32's result bits (out[3] is the append cursor); out[1] counts inputs
+// where exp_f32 differs from the math library's exp(double) rounded to
+// float, and out[2] those of them outside the first set; out[4] is the
+// largest difference between exp_f32's f64 value and the library's
+// exp(double), in units of the latter's last place (|v| <= 100).
+__global__ void selftest_exp_kernel(uint32_t lo, uint32_t hi,
+                                    unsigned long long *out, float *inputs,
+                                    uint32_t *results, uint32_t cap) {
+  const uint32_t i = lo + blockIdx.x * blockDim.x + threadIdx.x;
+  bool near = false, differ = false;
+  float v = 0.0f, got = 0.0f;
+  if (i < hi) {
+    v = __builtin_bit_cast(float, i);
+    if (v == v) {
+      got = exp_f32(v);
+      const float lib = (float)exp((double)v);
+      differ = __builtin_bit_cast(uint32_t, got) != __builtin_bit_cast(uint32_t, lib);
+      const double y =
+          exp_f64_reduced((double)(v > 100.0f ? 100.0f : (v < -110.0f ? -110.0f : v)));
+      const float fa = (float)(y * (1.0 - 0x1p-46)), fb = (float)(y * (1.0 + 0x1p-46));
+      near = __builtin_bit_cast(uint32_t, fa) != __builtin_bit_cast(uint32_t, fb);
+      if (v >= -100.0f && v <= 100.0f) {
+        const double yl = exp((double)v);
+        int e2;
+        (void)frexp(yl, &e2);
+        const double ulps = fabs(y - yl) / ldexp(1.0, e2 - 53);
+        atomicMax(out + 4, (unsigned long long)ceil(ulps));
+      }
+    }
+  }
+  const unsigned long long mn = __ballot(near), md = __ballot(differ),
+                           mo = __ballot(differ && !near);
+  if ((threadIdx.x & 63) == 0) {
+    if (mn) atomicAdd(out, (unsigned long long)__popcll(mn));
+    if (md) atomicAdd(out + 1, (unsigned long long)__popcll(md));
+    if (mo) atomicAdd(out + 2, (unsigned long long)__popcll(mo));
+  }
+  if (near) {
+    const unsigned long long slot = atomicAdd(out + 3, 1ull);
+    if (slot < cap) {
+      inputs[slot] = v;
+      results[slot] = __builtin_bit_cast(uint32_t, got);
+    }
+  }
 }
 
 // Grid: x covers (row, padded block) in units of 8 blocks per wave.
@@ -968,6 +1007,21 @@ hipError_t launch_selftest_quantizer(unsigned long long *bad, hipStream_t s) {
                      dim3(grid_for((int64_t)(hi - lo), 256)), dim3(256), 0, s,
                      lo, hi, bad);
   return hipGetLastError();
+}
+
+hipError_t launch_selftest_exp(unsigned long long *out, float *inputs,
+                               uint32_t *results, uint32_t cap, hipStream_t s) {
+  // all bit patterns in two halves (the last one, 0xffffffff, is a NaN)
+  const uint32_t bounds[3] = {0u, 0x80000000u, 0xffffffffu};
+  for (int h = 0; h < 2; ++h) {
+    hipLaunchKernelGGL(selftest_exp_kernel,
+                       dim3(grid_for((int64_t)(bounds[h + 1] - bounds[h]), 256)),
+                       dim3(256), 0, s, bounds[h], bounds[h + 1], out, inputs,
+                       results, cap);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_quantize(const void *x, bool x_bf16, int64_t m, int64_t ldx,

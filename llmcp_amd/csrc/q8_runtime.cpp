@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 #include <omp.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -404,6 +405,47 @@ int llmcp_q8_selftest_quantizer(llmcp_q8_ctx *ctx, uint64_t *mismatches) {
   (void)hipFree(bad);
   if (e != hipSuccess) return hip_fail(e, "quantizer self-test");
   *mismatches = host;
+  return LLMCP_Q8_OK;
+}
+
+int llmcp_q8_selftest_exp(llmcp_q8_ctx *ctx, uint64_t counts[4], float *inputs,
+                          uint32_t *results, int64_t cap, int64_t *stored) {
+  if (!ctx || !counts || !stored || cap < 0 || (cap > 0 && (!inputs || !results)))
+    return fail(LLMCP_Q8_EINVAL, "null argument or negative capacity");
+  if (cap > (int64_t)1 << 24) return fail(LLMCP_Q8_EINVAL, "capacity above 2^24");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  unsigned long long *out = nullptr;
+  float *din = nullptr;
+  uint32_t *dres = nullptr;
+  const size_t n = cap > 0 ? (size_t)cap : 1;
+  if (hipMalloc(&out, 5 * sizeof(*out)) != hipSuccess ||
+      hipMalloc(&din, n * sizeof(float)) != hipSuccess ||
+      hipMalloc(&dres, n * sizeof(uint32_t)) != hipSuccess) {
+    (void)hipFree(out);
+    (void)hipFree(din);
+    (void)hipFree(dres);
+    return fail(LLMCP_Q8_ENOMEM, "exp self-test buffers");
+  }
+  unsigned long long host[5] = {0, 0, 0, 0, 0};
+  hipError_t e = hipMemsetAsync(out, 0, sizeof(host), ctx->stream);
+  if (e == hipSuccess)
+    e = launch_selftest_exp(out, din, dres, (uint32_t)cap, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(host, out, sizeof(host), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  const int64_t k = e == hipSuccess ? (int64_t)std::min<unsigned long long>(host[3], (unsigned long long)cap) : 0;
+  if (e == hipSuccess && k > 0)
+    e = hipMemcpy(inputs, din, (size_t)k * sizeof(float), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && k > 0)
+    e = hipMemcpy(results, dres, (size_t)k * sizeof(uint32_t), hipMemcpyDeviceToHost);
+  (void)hipFree(out);
+  (void)hipFree(din);
+  (void)hipFree(dres);
+  if (e != hipSuccess) return hip_fail(e, "exp self-test");
+  for (int i = 0; i < 3; ++i) counts[i] = host[i];
+  counts[3] = host[4];
+  *stored = k;
   return LLMCP_Q8_OK;
 }
 

@@ -162,6 +162,10 @@ def _scalar_map(name, v):
     return np.array([f(float(a)) for a in v.ravel()], np.float32).reshape(v.shape)
 
 
+def expf(v):
+    return _scalar_map("oracle_expf", v)
+
+
 def silu(v):
     return _scalar_map("oracle_silu", v)
 

@@ -392,6 +392,23 @@ def test_quantizer_division_identities(ctx):
     assert ctx.selftest_quantizer() == 0
 
 
+def test_exp_pinned_over_all_floats(ctx, oracle):
+    """The epilogues' exp (f64 Taylor evaluation rounded to f32) against the
+    oracle's (host libm exp(double) rounded to f32) over every float input.
+    The device lists every input whose exp lies within 2^-46 of a change of
+    float rounding; both evaluations are far more accurate than that (the
+    device's is measured against the device library's below), so they can
+    only disagree on the listed inputs, which are compared one by one."""
+    (near, differ, outside, max_ulps), xs, got = ctx.selftest_exp()
+    assert outside == 0
+    assert max_ulps <= 8  # f64 ulps: the device exp is accurate to ~2^-49
+    assert 0 < near == xs.size  # every listed input was returned
+    ref = oracle.expf(xs).view(np.uint32)
+    bad = np.nonzero(ref != got)[0]
+    assert bad.size == 0, (xs[bad][:8], got[bad][:8], ref[bad][:8])
+    assert differ <= near
+
+
 @pytest.mark.parametrize("k", [1056, 3872, 8864])
 def test_block_dots_exact(ctx, oracle, k):
     rng = np.random.default_rng(16 + k)
