@@ -18,6 +18,8 @@
 
 #include <stddef.h>
 
+#include <algorithm>
+
 #include <utility>
 
 #include "q8_device.h"
@@ -155,7 +157,7 @@ struct Seg6 {
 // EPI: activation code in bits 0-1, bf16 output in bit 2, the SwiGLU
 // multiply by `mul` in bit 3 (compile time: the epilogue is inlined for
 // every accumulator element).
-template <int WM, int WN, int NST, bool FMA, int SEG, int EPI>
+template <int WM, int WN, int NST, bool FMA, int SEG, int EPI, bool PERSIST>
 __global__ __launch_bounds__(64 * WM * WN)
 __attribute__((amdgpu_waves_per_eu(WM * WN >= 12 ? 3 : 2)))
 void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
@@ -176,15 +178,30 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
 
   // XCD-aware tile order: ids with the same (id % 8) share an XCD; each XCD
   // takes whole N-tiles (all their M-tiles), so a weight tile is fetched
-  // into that XCD's L2 once.
-  const int id = blockIdx.x;
-  const int xcd = id & 7;
-  const int kk = id >> 3;
-  const int n_tile = (kk / m_tiles) * 8 + xcd;
-  const int m_tile = kk % m_tiles;
-  if (n_tile >= n_tiles) return;  // uniform per workgroup
-  const int64_t m0 = (int64_t)m_tile * BM;
-  const int64_t n0 = (int64_t)n_tile * BN;
+  // into that XCD's L2 once.  Workgroups are persistent: workgroup g takes
+  // ids g, g + G, g + 2G, ... (G = gridDim.x, a multiple of 8, so all on one
+  // XCD); ids of the padding N-tiles (n_tile >= n_tiles) are skipped.
+  const int total = (n_tiles + 7) / 8 * 8 * m_tiles;
+  const int G = gridDim.x;
+  auto tile_of = [&](int id, int &mt, int &nt) __attribute__((always_inline)) {
+    const int kk = id >> 3;
+    nt = (kk / m_tiles) * 8 + (id & 7);
+    mt = kk % m_tiles;
+  };
+  auto next_tile = [&](int id) __attribute__((always_inline)) {
+    for (; id < total; id += G) {
+      int mt, nt;
+      tile_of(id, mt, nt);
+      if (nt < n_tiles) break;
+    }
+    return id;
+  };
+  int id = next_tile(blockIdx.x);
+  if (id >= total) return;  // uniform per workgroup
+  int m_tile, n_tile;
+  tile_of(id, m_tile, n_tile);
+  int64_t m0 = (int64_t)m_tile * BM;
+  int64_t n0 = (int64_t)n_tile * BN;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -194,17 +211,18 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   const int stages = passes * (kPassBlocks / kStageBlocks);
   const int64_t wrow = (int64_t)passes * kPassBytes;  // bytes per lane group
 
-  // This wave's DMA ops.  Per op: a loop-invariant per-lane byte offset (a
-  // tensor is below 4 GiB), its kind and LDS destination (wave-uniform);
-  // the per-stage part of each address is wave-uniform too (plus, for
-  // S = 6, a per-lane block offset).
+  // This wave's DMA ops.  Per op: a per-lane byte offset that depends on the
+  // tile (a tensor is below 4 GiB), its kind and LDS destination (wave-
+  // uniform); the per-stage part of each address is wave-uniform too (plus,
+  // for S = 6, a per-lane block offset).
   enum { K_A = 0, K_B = 1, K_SA = 2, K_DW = 3 };
-  uint32_t off16[St::S16], off4[St::S4 > 0 ? St::S4 : 1];
+  constexpr int S4N = St::S4 > 0 ? St::S4 : 1;
   int kind[St::S16], abb[St::S16], dst16[St::S16], piece16[St::S16];
-  int dst4[St::S4 > 0 ? St::S4 : 1], piece4[St::S4 > 0 ? St::S4 : 1];
+  int dst4[S4N], piece4[S4N];
   // S = 6: per-lane block offsets for r = 0, 2, 4 (Seg6), in three arrays
   // indexed only at compile time (a runtime index would put them in scratch)
   uint32_t x16r0[St::S16], x16r2[St::S16], x16r4[St::S16];
+  const int q4 = lane >> 2;
 #pragma unroll
   for (int u = 0; u < St::S16; ++u) {
     int o = wave + u * W;
@@ -213,34 +231,18 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     piece16[u] = 0;
     if (o < St::CA) {
       kind[u] = K_A;
-      const int64_t rt = min((int64_t)m_tile * WM + o / kStageBlocks, (int64_t)row_tiles - 1);
-      off16[u] = (uint32_t)(rt * nblk * 1024 + li * 32 + lh * 16);
       dst16[u] = (int)offsetof(St, a) + o * 1024;
     } else if (o < St::CA + St::CB) {
       kind[u] = K_B;
       const int c = o - St::CA;
-      const int q = lane >> 2;
-      const int ri = 16 * (c & 3) + q;
-      const int64_t n = min(n0 + 32 * (c >> 2) + (ri & 31), n_rows - 1);
-      const int piece = (lane & 3) ^ ((q >> 2) & 3);
-      piece16[u] = piece;
-      off16[u] = (uint32_t)((n >> 2) * wrow + (ri >> 5) * 1024 + (n & 3) * 256 +
-                            (SEG == 1 ? piece * 16 : SEG == 4 ? piece * kPassBytes : 0));
+      piece16[u] = (lane & 3) ^ ((q4 >> 2) & 3);
       dst16[u] = (int)offsetof(St, b) + c * 1024;
     } else if (o < St::CA + St::CB + St::CS) {
       kind[u] = K_SA;
-      // lanes 0-31: row tile 2c, lanes 32-63: row tile 2c+1 (512 B each)
-      const int c = o - St::CA - St::CB;
-      const int64_t rt = min((int64_t)m_tile * WM + 2 * c + lh, (int64_t)row_tiles - 1);
-      off16[u] = (uint32_t)(rt * nblk * 128 + li * 16);
-      dst16[u] = (int)offsetof(St, sa) + c * 1024;
+      dst16[u] = (int)offsetof(St, sa) + (o - St::CA - St::CB) * 1024;
     } else {
       kind[u] = K_DW;
-      // column tile c: lane l takes 16 B of group l/8's 128 B scale block
-      const int c = o - St::CA - St::CB - St::CS;
-      const int64_t ng = min(n0 + 32 * c + 4 * (lane >> 3), n_rows - 4);
-      off16[u] = (uint32_t)((ng >> 2) * wrow + kPassQs + (lane & 7) * 16);
-      dst16[u] = (int)offsetof(St, dw16) + c * 1024;
+      dst16[u] = (int)offsetof(St, dw16) + (o - St::CA - St::CB - St::CS) * 1024;
     }
   }
 #pragma unroll
@@ -249,14 +251,9 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     if (o >= St::T4) o -= St::T4;
     // S > 1, column tile o/2, block 2(o%2) + lh of the stage, one f16 per
     // dword
-    const int64_t n = min(n0 + 32 * (o / 2) + li, n_rows - 1);
-    const int j = o % 2;
-    piece4[u] = 2 * j + lh;
-    off4[u] = (uint32_t)((n >> 2) * wrow + kPassQs + 32 * (n & 3) +
-                         (SEG == 4 ? (2 * j + lh) * kPassBytes : 0));
+    piece4[u] = 2 * (o % 2) + lh;
     dst4[u] = (int)offsetof(St, dw4) + o * 256;
   }
-
 #pragma unroll
   for (int u = 0; u < St::S16; ++u) {
     const bool seg = SEG == 6 && kind[u] == K_B;
@@ -264,6 +261,50 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     x16r2[u] = seg ? Seg6::qs(2, piece16[u]) : 0u;
     x16r4[u] = seg ? Seg6::qs(4, piece16[u]) : 0u;
   }
+
+  // The tile-dependent per-lane offsets of this wave's ops for the tile at
+  // (mt, nn0).
+  struct Offsets {
+    uint32_t o16[St::S16], o4[S4N];
+  };
+  auto tile_offsets = [&](int mt, int64_t nn0) __attribute__((always_inline)) {
+    Offsets of;
+#pragma unroll
+    for (int u = 0; u < St::S16; ++u) {
+      int o = wave + u * W;
+      if (o >= St::T16) o -= St::T16;
+      if (kind[u] == K_A) {
+        const int64_t rt = min((int64_t)mt * WM + o / kStageBlocks, (int64_t)row_tiles - 1);
+        of.o16[u] = (uint32_t)(rt * nblk * 1024 + li * 32 + lh * 16);
+      } else if (kind[u] == K_B) {
+        const int c = o - St::CA;
+        const int ri = 16 * (c & 3) + q4;
+        const int64_t n = min(nn0 + 32 * (c >> 2) + (ri & 31), n_rows - 1);
+        const int piece = piece16[u];
+        of.o16[u] = (uint32_t)((n >> 2) * wrow + (ri >> 5) * 1024 + (n & 3) * 256 +
+                               (SEG == 1 ? piece * 16 : SEG == 4 ? piece * kPassBytes : 0));
+      } else if (kind[u] == K_SA) {
+        // lanes 0-31: row tile 2c, lanes 32-63: row tile 2c+1 (512 B each)
+        const int c = o - St::CA - St::CB;
+        const int64_t rt = min((int64_t)mt * WM + 2 * c + lh, (int64_t)row_tiles - 1);
+        of.o16[u] = (uint32_t)(rt * nblk * 128 + li * 16);
+      } else {
+        // column tile c: lane l takes 16 B of group l/8's 128 B scale block
+        const int c = o - St::CA - St::CB - St::CS;
+        const int64_t ng = min(nn0 + 32 * c + 4 * (lane >> 3), n_rows - 4);
+        of.o16[u] = (uint32_t)((ng >> 2) * wrow + kPassQs + (lane & 7) * 16);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < St::S4; ++u) {
+      int o = wave + u * W;
+      if (o >= St::T4) o -= St::T4;
+      const int64_t n = min(nn0 + 32 * (o / 2) + li, n_rows - 1);
+      of.o4[u] = (uint32_t)((n >> 2) * wrow + kPassQs + 32 * (n & 3) +
+                            (SEG == 4 ? piece4[u] * kPassBytes : 0));
+    }
+    return of;
+  };
 
   // Wave-uniform position of a stage's first block in the unit layout:
   // S = 1, 4: its unit and slot; S = 6: unit 6P, slot q and r (Seg6).
@@ -287,7 +328,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
 
   // Issue DMA op j (j < S16: 16 B class, else 4 B class) of stage s into
   // buffer `buf`: branch-free, the same instruction sequence in every wave.
-  auto issue_op = [&](int s, St &buf, auto J) __attribute__((always_inline)) {
+  auto issue_op = [&](int s, St &buf, auto J, const Offsets &of) __attribute__((always_inline)) {
     constexpr int j = decltype(J)::value;
     const int kb = s * kStageBlocks;  // first block of the stage
     const StagePos sp = stage_pos(kb);
@@ -307,22 +348,20 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
         const uint32_t m0 = sp.r == 0 ? ~0u : 0u, m2 = sp.r == 2 ? ~0u : 0u;
         extra = (x16r0[u] & m0) | (x16r2[u] & m2) | (x16r4[u] & ~(m0 | m2));
       }
-      dma16(uniform_ptr(base) + off16[u] + extra, lds_base + dst16[u]);
+      dma16(uniform_ptr(base) + of.o16[u] + extra, lds_base + dst16[u]);
     } else {
       const int u = j - St::S16;
       const uint8_t *db = w + sp.unit * kPassBytes + 2 * (sp.slot & ~1);
       uint32_t extra = 0;
       if constexpr (SEG == 6) extra = Seg6::scale(sp.r, sp.slot, piece4[u]);
-      dma4(uniform_ptr(db) + off4[u] + extra, lds_base + dst4[u]);
+      dma4(uniform_ptr(db) + of.o4[u] + extra, lds_base + dst4[u]);
     }
   };
-  auto issue = [&](int s, St &buf) __attribute__((always_inline)) {
-    static_for<St::OPS>([&](auto J) __attribute__((always_inline)) { issue_op(s, buf, J); });
+  auto issue = [&](int s, St &buf, const Offsets &of) __attribute__((always_inline)) {
+    static_for<St::OPS>([&](auto J) __attribute__((always_inline)) { issue_op(s, buf, J, of); });
   };
 
   float acc[16];
-#pragma unroll
-  for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   // SwiGLU: this lane's 16 gate values, loaded at the start of the last
   // group of stages so that their latency hides behind it (indices clamped,
@@ -378,7 +417,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   // The next stage's DMA ops (stage sn into buffer nbuf) are spread over
   // the blocks, issued after each block's MFMAs: a burst of them right after
   // the barrier would stall every wave on the load queue at once.
-  auto compute = [&](int s, St &buf, int sn, St &nbuf) __attribute__((always_inline)) {
+  auto compute = [&](int s, St &buf, int sn, St &nbuf, const Offsets &of) __attribute__((always_inline)) {
     const int kb = s * kStageBlocks;
     v32f fac[2];
     fac[0] = scales(kb, buf, 0);
@@ -390,7 +429,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
       if constexpr (bb == 0) fac[1] = scales(kb, buf, 1);
       static_for<St::OPS>([&](auto J) __attribute__((always_inline)) {
         if constexpr (decltype(J)::value * kStageBlocks / St::OPS == bb)
-          issue_op(sn, nbuf, J);
+          issue_op(sn, nbuf, J, of);
       });
       const v32f &f2 = fac[bb >> 1];
 #pragma unroll
@@ -415,57 +454,89 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
 
   // Every DMA is unconditional: a branch around one makes the compiler's
   // wait tracking merge states and wait for all loads before the next LDS
-  // read.  Stages past the end reload the last stage into a buffer nobody
-  // reads again (the stage count, 4 per unit, is a multiple of NST).
+  // read.  The DMA stream runs on across tiles: the last group of stages
+  // issues the next tile's first NST - 1 stages, so their latency hides
+  // behind that group and this tile's epilogue.  After the last tile they
+  // reload the tile's own first stages into buffers nobody reads again.
   static_assert(kPassBlocks / kStageBlocks % NST == 0, "stages per unit");
   const int last = stages - 1;
+  Offsets cur = tile_offsets(m_tile, n0);
 #pragma unroll
-  for (int i = 0; i < NST - 1; ++i) issue(min(i, last), stage(i));
+  for (int i = 0; i < NST - 1; ++i) issue(min(i, last), stage(i), cur);
 
-  // One group of NST stages (static buffer indices).  With the SwiGLU
-  // multiply the last group is peeled off: it also prefetches the gate values.
-  auto group = [&](int s0, auto LAST) __attribute__((always_inline)) {
-    if constexpr (decltype(LAST)::value) prefetch_gate();
+  for (;;) {
+    const int id_next = PERSIST ? next_tile(id + G) : total;
+    const bool more = PERSIST && id_next < total;
+    int m_next = m_tile, n_next = n_tile;
+    if (more) tile_of(id_next, m_next, n_next);
+    Offsets nxt;
 #pragma unroll
-    for (int i = 0; i < NST; ++i) {
-      const int s = s0 + i;
-      // NST - 2 stages were issued after stage s
-      wait_vmcnt<(NST - 2) * St::OPS>();
-      stage_barrier();
-      // every wave is past stage s-1: its buffer takes stage s+NST-1
-      compute(s, stage(i), min(s + NST - 1, last), stage((i + NST - 1) % NST));
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+
+    // One group of NST stages (static buffer indices).  The last group is
+    // peeled off when it differs: with PERSIST its stages s + NST - 1 past
+    // the end are the next tile's, and with the SwiGLU multiply it
+    // prefetches the gate values.  Without PERSIST (one tile per
+    // workgroup) those stages reload the tile's last stage into buffers
+    // nobody reads again.
+    auto group = [&](int s0, auto LAST) __attribute__((always_inline)) {
+      constexpr bool is_last = decltype(LAST)::value;
+      if constexpr (is_last) {
+        prefetch_gate();
+        if constexpr (PERSIST) nxt = tile_offsets(m_next, (int64_t)n_next * BN);
+      }
+#pragma unroll
+      for (int i = 0; i < NST; ++i) {
+        const int s = s0 + i;
+        // NST - 2 stages were issued after stage s
+        wait_vmcnt<(NST - 2) * St::OPS>();
+        stage_barrier();
+        // every wave is past stage s-1: its buffer takes stage s+NST-1
+        St &nbuf = stage((i + NST - 1) % NST);
+        if (PERSIST && is_last && i > 0)
+          compute(s, stage(i), i - 1, nbuf, nxt);
+        else
+          compute(s, stage(i), min(s + NST - 1, last), nbuf, cur);
+      }
+    };
+    if constexpr (PERSIST || (EPI & 8) != 0) {
+      for (int s0 = 0; s0 < stages - NST; s0 += NST) group(s0, std::false_type{});
+      group(stages - NST, std::true_type{});
+    } else {
+      for (int s0 = 0; s0 < stages; s0 += NST) group(s0, std::false_type{});
     }
-  };
-  if constexpr ((EPI & 8) != 0) {
-    for (int s0 = 0; s0 < stages - NST; s0 += NST) group(s0, std::false_type{});
-    group(stages - NST, std::true_type{});
-  } else {
-    for (int s0 = 0; s0 < stages; s0 += NST) group(s0, std::false_type{});
+
+    const int64_t n = n0 + 32 * wn + li;
+    // the activation over all 16 values (rows or columns past the end too,
+    // whose results are not stored): one straight-line sequence
+    activate_array(acc, EPI & 3);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t m = m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
+      if (m < m_rows && n < n_rows) {
+        float o = acc[v];
+        if constexpr ((EPI & 8) != 0) {
+          // SwiGLU: times the gate's activated output (FuseSiluMul's mul)
+          const float g = gpre[v];
+          o = (EPI & 4) != 0 ? bf16_to_float(float_to_bf16(g)) * bf16_to_float(float_to_bf16(o))
+                             : g * o;
+        }
+        if constexpr ((EPI & 4) != 0)
+          ((uint16_t *)y)[m * ldy + n] = float_to_bf16(o);
+        else
+          ((float *)y)[m * ldy + n] = o;
+      }
+    }
+    if (!more) break;
+    id = id_next;
+    m_tile = m_next;
+    n_tile = n_next;
+    m0 = (int64_t)m_tile * BM;
+    n0 = (int64_t)n_tile * BN;
+    cur = nxt;
   }
   // no DMA may land in LDS after the workgroup has released it
   wait_vmcnt<0>();
-
-  const int64_t n = n0 + 32 * wn + li;
-  // the activation over all 16 values (rows or columns past the end too,
-  // whose results are not stored): one straight-line sequence
-  activate_array(acc, EPI & 3);
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int64_t m = m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
-    if (m < m_rows && n < n_rows) {
-      float o = acc[v];
-      if constexpr ((EPI & 8) != 0) {
-        // SwiGLU: times the gate's activated output (FuseSiluMul's mul)
-        const float g = gpre[v];
-        o = (EPI & 4) != 0 ? bf16_to_float(float_to_bf16(g)) * bf16_to_float(float_to_bf16(o))
-                           : g * o;
-      }
-      if constexpr ((EPI & 4) != 0)
-        ((uint16_t *)y)[m * ldy + n] = float_to_bf16(o);
-      else
-        ((float *)y)[m * ldy + n] = o;
-    }
-  }
 }
 
 }  // namespace
@@ -473,10 +544,21 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
 template <int WM, int WN, int NST, bool FMA, int SEG, int EPI>
 static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
                           int32_t n_tiles, unsigned grid, hipStream_t s) {
-  hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI>), dim3(grid),
-                     dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
-                     l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
-                     l.mul, l.ldg);
+  // persistent (several tiles per workgroup) only when the tiles outnumber
+  // the resident workgroups, and only for the 12-wave shape and S = 1 or 4
+  // (with S = 6 the next tile's offsets spill registers)
+  constexpr bool kPersist = WM * WN >= 12 && SEG != 6;
+  const unsigned total = (unsigned)((n_tiles + 7) / 8 * 8 * m_tiles);
+  if (kPersist && grid < total)
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, kPersist>), dim3(grid),
+                       dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
+                       l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
+                       l.mul, l.ldg);
+  else
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, false>), dim3(total),
+                       dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
+                       l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
+                       l.mul, l.ldg);
 }
 
 template <int WM, int WN, int NST, bool FMA, int SEG>
@@ -498,13 +580,32 @@ static void launch_gemm_e(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
 #undef LLMCP_GEMM_EPI
 }
 
+// Compute units of the current device (cached per device).
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int WM, int WN, int NST, bool FMA>
 static hipError_t launch_gemm_t(const GemmLaunch &l, hipStream_t s) {
   const int32_t passes = (int32_t)passes_for(l.cols);
   const int32_t m_tiles = (int32_t)((l.m + 32 * WM - 1) / (32 * WM));
   const int32_t n_tiles = (int32_t)((l.rows + 32 * WN - 1) / (32 * WN));
   const int32_t n_tiles8 = (n_tiles + 7) / 8 * 8;
-  const unsigned grid = (unsigned)(n_tiles8 * m_tiles);
+  // persistent workgroups: at most as many as are resident at once (one or
+  // two per CU, by LDS), a multiple of 8 so that each stays on its XCD
+  const int64_t resident = (int64_t)cu_count() * (WM * WN >= 12 ? 1 : 2) / 8 * 8;
+  const unsigned grid =
+      (unsigned)std::min<int64_t>((int64_t)n_tiles8 * m_tiles, std::max<int64_t>(8, resident));
   // the weight's unit layout is fixed at registration (seg_for)
   switch (seg_for(passes)) {
     case 6: launch_gemm_e<WM, WN, NST, FMA, 6>(l, passes, m_tiles, n_tiles, grid, s); break;

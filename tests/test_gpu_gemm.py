@@ -130,3 +130,43 @@ def test_prefill_swiglu(ctx, oracle):
     assert bits_equal(h, oracle.swiglu(x, pg, pu, n, epilogue="fma"))
     ctx.release(tg)
     ctx.release(tu)
+
+
+def _sampled_rows(rng, m, count=32):
+    return np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, count - 2)]))
+
+
+# More tiles than resident workgroups: with K = 288 and 3872 (1 and 4 blocks
+# per lane slot; 288 is a single group of stages) each workgroup runs several
+# tiles back to back, its DMA stream crossing from one tile into the next;
+# K = 9216 (6 blocks per slot) takes one tile per workgroup in two rounds.
+# N = 3720 is 39 column tiles (the schedule's padding ids to 40 are
+# skipped).  Every column of 32 sampled rows is checked, which touches each
+# column tile in most row tiles.
+@pytest.mark.parametrize("k", [288, 3872, 9216])
+def test_gemm_persistent_tiles(ctx, oracle, k):
+    m, n = 1024, 3720
+    rng = np.random.default_rng(900 + k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    p4 = oracle.pack_q8_0_p4(w)
+    y = gemm(ctx, p4, n, k, x)
+    rows = _sampled_rows(rng, m)
+    assert bits_equal(y[rows], oracle.linear(x[rows], p4, n, epilogue="fma"))
+
+
+def test_prefill_swiglu_persistent_tiles(ctx, oracle):
+    m, n, k = 1024, 3720, 512
+    rng = np.random.default_rng(950)
+    wg = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wu = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    pg, pu = oracle.pack_q8_0_p4(wg), oracle.pack_q8_0_p4(wu)
+    tg, tu = ctx.upload_p4(pg, n, k), ctx.upload_p4(pu, n, k)
+    xd, hd = ctx.to_device(x), ctx.alloc(m * n * 4)
+    ctx.swiglu(xd, tg, tu, hd, m, mode="prefill")
+    h = ctx.to_host(hd, (m, n), np.float32)
+    rows = _sampled_rows(rng, m)
+    assert bits_equal(h[rows], oracle.swiglu(x[rows], pg, pu, n, epilogue="fma"))
+    ctx.release(tg)
+    ctx.release(tu)
