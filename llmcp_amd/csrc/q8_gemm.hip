@@ -169,7 +169,6 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   static_assert(NST == 2 || NST == 4, "stage buffers");
   constexpr int W = WM * WN;
   constexpr int BM = 32 * WM, BN = 32 * WN;
-  constexpr int UNIT_S4 = SEG == 4;  // blocks of a stage: one slot, 4 units
   // one LDS object per stage buffer (see above)
   __shared__ St st0, st1, st2, st3, st4;
   auto stage = [&](int i) __attribute__((always_inline)) -> St & {

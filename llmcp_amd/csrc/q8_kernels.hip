@@ -452,7 +452,7 @@ __device__ __forceinline__ void argmax_fold(unsigned long long *slots,
 // workgroup quantizes the input row once (pc * 16 blocks, 8 lanes per block,
 // row_rounds float4 loads per lane), so wider workgroups share that work.
 __host__ __device__ constexpr int wg_waves(int nmat, int pc) {
-  return nmat == 2 ? 3 : (pc <= 5 ? 2 : 4);
+  return nmat == 2 ? 4 : (pc <= 5 ? 2 : 4);
 }
 __host__ __device__ constexpr int row_rounds(int pc, int w) {
   return (2 * pc + w - 1) / w;

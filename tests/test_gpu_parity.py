@@ -189,10 +189,10 @@ def test_decode_mlp_end_to_end(ctx, oracle):
 
 
 def test_fused_mlp_matches_separate_ops(ctx, oracle):
-    # llmcp_q8_mlp: gate/up GEMV quantizes h for the down GEMV in its own
-    # epilogue (ticketed); the result must equal swiglu -> linear bit for bit,
-    # over repeated calls (tickets reset) and for a width that leaves a
-    # partial last pass (ffn = 1056 -> 33 blocks).
+    # llmcp_q8_mlp: the gate/up GEMV writes h, the down GEMV quantizes it per
+    # workgroup; the result must equal swiglu -> linear bit for bit, over
+    # repeated calls, with the caller's h buffer or the context's, and for a
+    # width that leaves a partial last pass (ffn = 1056 -> 33 blocks).
     rng = np.random.default_rng(21)
     for hidden, ffn in ((2560, 9216), (512, 1056)):
         wg, wu, wd = weights(rng, ffn, hidden), weights(rng, ffn, hidden), weights(rng, hidden, ffn)
