@@ -241,6 +241,26 @@ __device__ __forceinline__ float4 load_act4(const void *p, int64_t i,
   return make_float4(f[0], f[1], f[2], f[3]);
 }
 
+// load_act4 with the row type and alignment fixed at compile time: one
+// straight-line load, so several of them stay in flight together.
+template <bool BF16, bool ALIGNED>
+__device__ __forceinline__ float4 load_act4_t(const void *p, int64_t i) {
+  if constexpr (BF16) {
+    const uint16_t *h = (const uint16_t *)p + i;
+    if constexpr (ALIGNED) {
+      const uint2 w = *(const uint2 *)h;
+      return make_float4(bf16_to_float(w.x & 0xffffu), bf16_to_float(w.x >> 16),
+                         bf16_to_float(w.y & 0xffffu), bf16_to_float(w.y >> 16));
+    }
+    return make_float4(bf16_to_float(h[0]), bf16_to_float(h[1]),
+                       bf16_to_float(h[2]), bf16_to_float(h[3]));
+  } else {
+    const float *f = (const float *)p + i;
+    if constexpr (ALIGNED) return *(const float4 *)f;
+    return make_float4(f[0], f[1], f[2], f[3]);
+  }
+}
+
 // Exhaustive check of div127 and recip against IEEE division over the
 // float bit patterns [lo, hi): one pattern per thread, mismatches counted
 // per wave.
@@ -345,24 +365,31 @@ __global__ void quantize_kernel(const void *__restrict__ x, int x_bf16,
 // 128 B and writes 256 contiguous bytes of the tile.  quantize_block8 does
 // the arithmetic, so the bits match the row kernel.  Rows past m and blocks
 // past `blocks` are written as zeros.
+template <bool XB, bool AL>
 __global__ __launch_bounds__(256) void quantize_tiles_kernel(
-    const void *__restrict__ x, int x_bf16, int64_t m, int64_t ldx,
-    int32_t blocks, int32_t blocks_pad, int64_t tiles, int8_t *__restrict__ qa,
-    float *__restrict__ sa, int aligned) {
+    const void *__restrict__ x, int64_t m, int64_t ldx, int32_t blocks,
+    int32_t blocks_pad, int64_t tiles, int8_t *__restrict__ qa,
+    float *__restrict__ sa) {
   const int lane = threadIdx.x & 63;
   const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tile >= tiles) return;  // uniform per wave
   const int32_t rt = (int32_t)(tile / blocks_pad);
   const int32_t b = (int32_t)(tile - (int64_t)rt * blocks_pad);
   const int rr = lane >> 3, p = lane & 7;
+  // The four loads go out unconditionally (rows past m and padded blocks
+  // read a clamped address) and are zeroed only once all are in flight.
+  const int32_t bc = b < blocks ? b : blocks - 1;
   float4 v[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int64_t row = (int64_t)rt * 32 + 8 * c + rr;
-    v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (row < m && b < blocks)
-      v[c] = load_act4(x, row * ldx + (int64_t)b * kBlock + 4 * p, x_bf16 != 0,
-                       aligned != 0);
+    const int64_t rc = row < m ? row : m - 1;
+    v[c] = load_act4_t<XB, AL>(x, rc * ldx + (int64_t)bc * kBlock + 4 * p);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int64_t row = (int64_t)rt * 32 + 8 * c + rr;
+    if (!(row < m && b < blocks)) v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -1046,10 +1073,19 @@ hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
   const int64_t esz = x_bf16 ? 2 : 4;
   const int aligned =
       ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(quantize_tiles_kernel, dim3((unsigned)((tiles + 3) / 4)),
-                     dim3(256), 0, s, x, x_bf16 ? 1 : 0, m, ldx,
-                     (int32_t)blocks, (int32_t)blocks_pad, tiles, qa, sa,
-                     aligned);
+  const dim3 grid((unsigned)((tiles + 3) / 4));
+  const int32_t nb = (int32_t)blocks, np = (int32_t)blocks_pad;
+  if (x_bf16) {
+    if (aligned)
+      hipLaunchKernelGGL((quantize_tiles_kernel<true, true>), grid, dim3(256), 0, s, x, m, ldx, nb, np, tiles, qa, sa);
+    else
+      hipLaunchKernelGGL((quantize_tiles_kernel<true, false>), grid, dim3(256), 0, s, x, m, ldx, nb, np, tiles, qa, sa);
+  } else {
+    if (aligned)
+      hipLaunchKernelGGL((quantize_tiles_kernel<false, true>), grid, dim3(256), 0, s, x, m, ldx, nb, np, tiles, qa, sa);
+    else
+      hipLaunchKernelGGL((quantize_tiles_kernel<false, false>), grid, dim3(256), 0, s, x, m, ldx, nb, np, tiles, qa, sa);
+  }
   return hipGetLastError();
 }
 
