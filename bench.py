@@ -367,6 +367,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration)")
+    ap.add_argument("--gemm-only", type=int, default=0, metavar="M",
+                    help="time only config 4's prefill GEMM at M rows and print "
+                         "its figures (a short run for counter collection)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the Q8_0 linear path runs on a single "
@@ -377,6 +380,10 @@ def main():
     ctx = q8.Context(0)
     if args.copy_calibration:
         copy_calibration(ctx)
+    if args.gemm_only:
+        r = bench_gemm(ctx, args.gemm_only)
+        print(json.dumps({"gemm_m%d_n9216_k2560" % args.gemm_only: r}), flush=True)
+        return
     res = bench_decode_mlp(ctx, q8, args.steps, args.warmup)
     extra = {}
     if not args.no_extra:
