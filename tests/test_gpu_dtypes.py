@@ -161,3 +161,43 @@ def test_embedding_bf16(ctx, oracle, k):
     assert bits_equal(out, to_bf16(oracle, oracle.embedding(tokens, p4, k)))
     assert ctx.check_flag() == 0
     ctx.release(t)
+
+
+# bf16 through the persistent GEMM schedule (more tiles than resident
+# workgroups: M = 1024, N = 3720, K = 2560), checked on 32 sampled rows.
+def _rows(rng, m):
+    return np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, 30)]))
+
+
+def test_linear_bf16_persistent_tiles(ctx, oracle):
+    rng = np.random.default_rng(360)
+    m, n, k = 1024, 3720, 2560
+    w = weights(rng, n, k)
+    xb = to_bf16(oracle, rng.standard_normal((m, k)))
+    p4 = oracle.pack_q8_0_p4(w)
+    t = ctx.upload_p4(p4, n, k)
+    xd, yd = ctx.to_device(xb), ctx.alloc(m * n * 2)
+    ctx.linear(xd, t, yd, m, activation="silu", mode="prefill", dtype="bf16")
+    y = ctx.to_host(yd, (m, n), np.uint16)
+    rows = _rows(rng, m)
+    ref = oracle.linear(oracle.bf16_bits_to_f32(xb[rows]), p4, n, activation="silu",
+                        epilogue="fma")
+    assert bits_equal(y[rows], to_bf16(oracle, ref))
+    ctx.release(t)
+
+
+def test_swiglu_bf16_persistent_tiles(ctx, oracle):
+    rng = np.random.default_rng(361)
+    m, n, k = 1024, 3720, 512
+    wg, wu = weights(rng, n, k, 0.05), weights(rng, n, k, 0.05)
+    xb = to_bf16(oracle, rng.standard_normal((m, k)))
+    p4g, p4u = oracle.pack_q8_0_p4(wg), oracle.pack_q8_0_p4(wu)
+    tg, tu = ctx.upload_p4(p4g, n, k), ctx.upload_p4(p4u, n, k)
+    xd, hd = ctx.to_device(xb), ctx.alloc(m * n * 2)
+    ctx.swiglu(xd, tg, tu, hd, m, mode="prefill", dtype="bf16")
+    h = ctx.to_host(hd, (m, n), np.uint16)
+    rows = _rows(rng, m)
+    ref = swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb[rows]), p4g, p4u, n)
+    assert bits_equal(h[rows], ref)
+    ctx.release(tg)
+    ctx.release(tu)
