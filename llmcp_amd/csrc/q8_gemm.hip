@@ -19,7 +19,6 @@
 #include <stddef.h>
 
 #include <algorithm>
-
 #include <utility>
 
 #include "q8_device.h"
@@ -51,6 +50,8 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // tiles.  Each stage buffer is its own LDS object, so the compiler's wait
 // for a wave's own DMA into one buffer does not drain the others; the
 // cross-wave hand-off is an explicit vmcnt wait plus s_barrier.
+// When the tiles outnumber the resident workgroups, workgroups are
+// persistent and the ring runs on from one tile into the next (PERSIST).
 constexpr int kStageBlocks = 4;
 
 template <int WM, int WN, int SEG>
