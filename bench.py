@@ -324,6 +324,20 @@ def cpu_baseline(res, budget_s=12.0):
         if time.perf_counter() - t0 > budget_s / 2 or m >= 200:
             break
     dt_col = (time.perf_counter() - t0) / m
+    # Config 4's GEMM on the same path: the scalar GEMM is row-parallel over
+    # M (Q8Scalar.cpp:84,127), so a 64-row sample on all threads gives its
+    # per-row rate, which holds for M = 1024.
+    rows = 64
+    xg = np.random.default_rng(4).standard_normal((rows, hidden)).astype(np.float32)
+    t0 = time.perf_counter()
+    k = 0
+    while True:
+        o.linear(xg, pg, ffn)
+        k += 1
+        if time.perf_counter() - t0 > budget_s / 4 or k >= 50:
+            break
+    dt_g = (time.perf_counter() - t0) / k
+    gemm_ops = 2.0 * rows * ffn * hidden
     return dict(value=res["step_bytes"] / dt / 1e9, unit="GB/s", cores=1,
                 kind="port",
                 sample="%d decode-MLP steps (2560->9216 x2 SwiGLU, 9216->2560) on one "
@@ -331,7 +345,11 @@ def cpu_baseline(res, budget_s=12.0):
                        "Q8Scalar.cpp:84,127 (M=1 -> 1 thread); %.1f ms/step" % (n, dt * 1e3),
                 colpar_value=res["step_bytes"] / dt_col / 1e9,
                 colpar_threads=o.max_threads(),
-                colpar_ms_per_step=dt_col * 1e3)
+                colpar_ms_per_step=dt_col * 1e3,
+                gemm={"TOPS": round(gemm_ops / dt_g / 1e12, 4), "threads": o.max_threads(),
+                      "sample": "%d-row samples of config 4 (K=2560 -> N=9216), scalar "
+                                "epilogue, row-parallel OpenMP; %d calls" % (rows, k),
+                      "ms_per_m1024_call": round(dt_g * 1024 / rows * 1e3, 1)})
 
 
 def copy_calibration(ctx, nbytes=256 << 20, reps=10):
