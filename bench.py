@@ -198,8 +198,11 @@ def bench_lm_head(ctx, v=248320, k=2560, iters=20):
 
 
 def bench_gemm(ctx, m, n=9216, k=2560, iters=30):
-    """Config 4: prefill GEMM, activation quantization included ("op") and
-    the quantize kernel alone, over a rotating pool of weight copies."""
+    """Config 4: the prefill linear as a caller sees it ("op": the tiled Q8_1
+    quantizer plus the GEMM kernel) over a rotating pool of weight copies;
+    the rates are over the whole op.  The C ABI's dense-layout quantizer is
+    timed beside it for reference (the GEMM kernel alone is in the rocprofv3
+    summaries)."""
     per = p4_bytes(n, k)
     copies = max(2, -(-int(1.6 * MALL_BYTES) // per)) if m <= 256 else 2
     ws = []
@@ -231,12 +234,10 @@ def bench_gemm(ctx, m, n=9216, k=2560, iters=30):
         ctx.release(w)
         p4d.free()
     ops = 2.0 * m * n * k
-    kern = max(us - q_us, 1e-3)
-    return {"op_us": round(us, 2), "quantize_us": round(q_us, 2),
-            "gemm_us": round(kern, 2),
+    return {"op_us": round(us, 2),
             "op_TOPS": round(ops / (us * 1e-6) / 1e12, 1),
-            "gemm_TOPS": round(ops / (kern * 1e-6) / 1e12, 1),
-            "frac_int8_peak": round(ops / (kern * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+            "frac_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+            "quantize_dense_us": round(q_us, 2),
             "bytes": per + m * k * 4 + m * n * 4}
 
 
