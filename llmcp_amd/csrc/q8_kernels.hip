@@ -860,16 +860,18 @@ __global__ __launch_bounds__(1024) void argmax_reduce_kernel(
 
 // ---------------------------------------------------------- embedding -- //
 
-// One thread per (token, 16 columns) -- LowerToLinalg.cpp:435-531 gathered
-// from the pass layout.  out = f32(q) * f32(d), exact.
+// One thread per (token, 16 columns), a flat grid over tokens x chunks so
+// that every lane has work -- LowerToLinalg.cpp:435-531 gathered from the
+// pass layout.  out = f32(q) * f32(d), exact.
 __global__ void embedding_kernel(const int64_t *__restrict__ tokens,
                                  int64_t count, const uint8_t *__restrict__ t,
                                  int64_t rows, int64_t passes, int64_t chunks,
                                  void *__restrict__ out, int out_bf16,
                                  int64_t ldo, int32_t *err, int aligned) {
-  const int64_t c16 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t ti = blockIdx.y;
-  if (c16 >= chunks || ti >= count) return;
+  const int64_t th = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t ti = th / chunks;
+  const int64_t c16 = th - ti * chunks;
+  if (ti >= count) return;
   const int64_t tok = tokens[ti];
   float v[16];
   if (tok < 0 || tok >= rows) {
@@ -1171,7 +1173,7 @@ hipError_t launch_embedding(const int64_t *tokens, int64_t count,
       ? ((uintptr_t)out % 16 == 0) && (ldo % 8 == 0)
       : ((uintptr_t)out % 16 == 0) && (ldo % 4 == 0);
   hipLaunchKernelGGL(embedding_kernel,
-                     dim3(grid_for(chunks, 256), (unsigned)count), dim3(256),
+                     dim3(grid_for(chunks * count, 256)), dim3(256),
                      0, s, tokens, count, table, rows, passes_for(cols),
                      chunks, out, out_bf16 ? 1 : 0, ldo, err_flag,
                      aligned ? 1 : 0);
