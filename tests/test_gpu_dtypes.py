@@ -201,3 +201,25 @@ def test_swiglu_bf16_persistent_tiles(ctx, oracle):
     assert bits_equal(h[rows], ref)
     ctx.release(tg)
     ctx.release(tu)
+
+
+# llmcp-matmul-benchmark's Q8 self-check (llmcp-matmul-benchmark.cpp:280-289,
+# :331-335; registered as a test at tests/CMakeLists.txt:162-165): every
+# record holds scales 0x2008 and q = 127, activations are bf16 1.0, and the
+# first bf16 output must equal K.  Run at the registered shape (M = N = K = 64,
+# prefill) and on the decode path, for the fixture's K values.
+@pytest.mark.parametrize("m,k", [(64, 64), (1, 64), (64, 2560), (1, 2560)])
+def test_matmul_benchmark_all_ones_fixture(ctx, oracle, m, k):
+    n = 64
+    rec = np.array([0x08, 0x20] * 4 + [0x7F] * 128, np.uint8)
+    p4 = np.tile(rec, n // 4 * (k // 32))
+    t = ctx.upload_p4(p4, n, k)
+    xb = np.full((m, k), 0x3F80, np.uint16)  # bf16 1.0
+    xd, yd = ctx.to_device(xb), ctx.alloc(m * n * 2)
+    ctx.linear(xd, t, yd, m, mode="decode" if m == 1 else "prefill", dtype="bf16")
+    y = ctx.to_host(yd, (m, n), np.uint16)
+    assert np.all(oracle.bf16_bits_to_f32(y) == np.float32(k))  # first == K
+    ref = oracle.linear(np.ones((m, k), np.float32), p4, n,
+                        epilogue="scalar" if m == 1 else "fma")
+    assert bits_equal(y, to_bf16(oracle, ref))
+    ctx.release(t)
