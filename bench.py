@@ -304,6 +304,78 @@ def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320
     return out
 
 
+def bench_arena(ctx, q8, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320):
+    """The whole config-5 model from one LLMCPWGT arena file, as the AOT
+    runtime loads it: written once (synthetic weights of the sequence's
+    shapes), mapped, uploaded by llmcp_q8_upload_arena (validation, host ->
+    HBM copies, device repack), then one decode step run through weight
+    descriptors that point into the mapping."""
+    import struct
+    import tempfile
+    shapes = [("gate", ffn, hidden), ("up", ffn, hidden), ("down", hidden, ffn),
+              ("qkv", qkv, hidden), ("o", hidden, hidden), ("a", hidden, hidden),
+              ("b", hidden, hidden)]
+    tensors = []
+    for li in range(layers):
+        for j, (name, n, k) in enumerate(shapes):
+            p4d, _ = ctx.synthesize_p4(seed=200000 + 16 * li + j, rows=n, cols=k)
+            tensors.append(("model.layers.%d.%s.weight" % (li, name), n, k,
+                            ctx.to_host(p4d, (p4d.nbytes,), np.uint8)))
+            p4d.free()
+    p4d, _ = ctx.synthesize_p4(seed=199, rows=vocab, cols=hidden)
+    tensors.append(("model.embed_tokens.weight", vocab, hidden,
+                    ctx.to_host(p4d, (p4d.nbytes,), np.uint8)))
+    p4d.free()
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    path = os.path.join(d, "llmcp_q8_bench_arena_%d.bin" % os.getpid())
+    try:
+        t0 = time.perf_counter()
+        q8.write_arena(path, tensors)
+        write_s = time.perf_counter() - t0
+        del tensors
+        f = np.memmap(path, dtype=np.uint8, mode="r")
+        ctx.sync()
+        t0 = time.perf_counter()
+        count = ctx.upload_arena(f)
+        ctx.sync()
+        upload_s = time.perf_counter() - t0
+        arena = struct.unpack_from("<Q", f, 16)[0]
+        entries = json.loads(bytes(f[arena:]).decode())["tensors"]
+        w = {e["name"]: q8.Weight(ctx, f.ctypes.data + e["offset"], e["shape"][0],
+                                  e["shape"][1], owner=f) for e in entries}
+        rng = np.random.default_rng(6)
+        x = ctx.to_device(rng.standard_normal((1, hidden)).astype(np.float32))
+        yq, yh = ctx.alloc(qkv * 4), ctx.alloc(ffn * 4)
+        y, logits, am = ctx.alloc(hidden * 4), ctx.alloc(vocab * 4), ctx.alloc(8)
+
+        def step():
+            for li in range(layers):
+                pre = "model.layers.%d." % li
+                ctx.linear(x, w[pre + "qkv.weight"], yq, 1)
+                for nm in ("o", "a", "b"):
+                    ctx.linear(x, w[pre + nm + ".weight"], y, 1)
+                ctx.mlp(x, w[pre + "gate.weight"], w[pre + "up.weight"],
+                        w[pre + "down.weight"], y, h=yh)
+            ctx.lm_head(x, w["model.embed_tokens.weight"], logits, 1, argmax=am)
+
+        step()
+        ctx.sync()
+        timer = Timer(ctx)
+        g = graph_of(ctx, step)
+        run_graph(ctx, timer, g, 1)
+        step_us = run_graph(ctx, timer, g, 5) * 1e3 / 5
+        for wt in w.values():
+            ctx.release(wt)
+        nbytes = int(f.nbytes)
+        del w, f
+    finally:
+        if os.path.exists(path):
+            os.unlink(path)
+    return {"file_bytes": nbytes, "q8_tensors": count, "write_s": round(write_s, 2),
+            "upload_s": round(upload_s, 3), "upload_GB/s": round(nbytes / upload_s / 1e9, 2),
+            "decode_step_us": round(step_us, 1)}
+
+
 def cpu_baseline(res, budget_s=12.0):
     """Reference x86 scalar Q8 path (oracle restatement) on the host cores."""
     from oracle import q8_oracle as o
@@ -390,6 +462,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration)")
+    ap.add_argument("--arena", action="store_true",
+                    help="also load the 32-layer model from a 4.4 GB arena "
+                         "file (written to /dev/shm) and time the upload")
     ap.add_argument("--gemm-only", type=int, default=0, metavar="M",
                     help="time only config 4's prefill GEMM at M rows and print "
                          "its figures (a short run for counter collection)")
@@ -422,6 +497,8 @@ def main():
         for m in (64, 256, 1024):
             extra["gemm_m%d_n9216_k2560" % m] = bench_gemm(ctx, m)
         extra["sequence_32_layers"] = bench_sequence(ctx)
+    if args.arena:
+        extra["arena_32_layers"] = bench_arena(ctx, q8)
     cpu = None if args.no_cpu else cpu_baseline(res)
     line = {
         "metric": "Q8_0 linear: M=1 GEMV HBM GB/s (% peak); M=1024 GEMM int8 TOPS (% peak)",
