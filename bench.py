@@ -143,8 +143,10 @@ def bench_decode_mlp(ctx, q8, steps, warmup, hidden=2560, ffn=9216):
     return res
 
 
-def bench_gemv(ctx, n, k, iters=200):
-    """Config 1: a single Q8_0 GEMV (K = N = 2560) over a rotating pool."""
+def bench_gemv(ctx, n, k, iters=200, residual=False):
+    """Config 1: a single Q8_0 GEMV (K = N = 2560) over a rotating pool;
+    with `residual`, the same GEMV with the residual add fused
+    (llmcp_q8_linear_add, in place on the output row)."""
     per = p4_bytes(n, k)
     copies = max(2, -(-int(1.6 * MALL_BYTES) // per))
     ws = []
@@ -156,7 +158,10 @@ def bench_gemv(ctx, n, k, iters=200):
 
     def rot():
         for w, _ in ws:
-            ctx.linear(xd, w, yd, 1)
+            if residual:
+                ctx.linear_add(xd, w, yd, yd, 1)
+            else:
+                ctx.linear(xd, w, yd, 1)
 
     timer = Timer(ctx)
     g = graph_of(ctx, rot)
@@ -488,6 +493,8 @@ def main():
         c1 = bench_gemv(ctx, 2560, 2560)
         extra["gemv_2560x2560"] = {"us": round(c1["us"], 3), "GB/s": round(c1["gb_s"], 1),
                                    "frac_hbm": round(c1["gb_s"] / HBM_PEAK_GBS, 4)}
+        c1a = bench_gemv(ctx, 2560, 2560, residual=True)
+        extra["gemv_2560x2560_residual_add"] = {"us": round(c1a["us"], 3)}
         c3 = bench_lm_head(ctx)
         extra["lm_head_248320x2560_argmax"] = {
             "us": round(c3["us"], 2), "GB/s": round(c3["gb_s"], 1),

@@ -39,10 +39,11 @@
 extern "C" {
 #endif
 
-/* Version of this C ABI.  The model ABI of the AOT library
+/* Version of this C ABI (1: f32 entries; 2: bf16 twins and all four
+ * activations; 3: linear + residual add).  The model ABI of the AOT library
  * (llmcp_model_abi_version() == 2, include/llmcp/Support/AotAbi.h:12) is not
  * changed by this library. */
-#define LLMCP_Q8_ABI_VERSION 2
+#define LLMCP_Q8_ABI_VERSION 3
 
 enum llmcp_q8_status {
   LLMCP_Q8_OK = 0,
@@ -183,6 +184,28 @@ int llmcp_q8_linear_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
                          const llmcp_memref_i8_1d *weight,
                          llmcp_memref_bf16_2d *output, int32_t activation,
                          int32_t execution_mode);
+
+/* llmcp.linear followed by llmcp.add of a residual, the pair the model
+ * builder emits after out_proj and after the MLP's down projection
+ * (ModelBuilder.cpp:271, :275; AddOpLowering, LowerToLinalg.cpp:359-375):
+ * y[M,N] = r[M,N] + x[M,K] . W[N,K]^T.  The linear's result is formed exactly
+ * as llmcp_q8_linear forms it (no activation: the pattern has none), then one
+ * f32 addition.  `residual` may be the same memory as `output` (in place);
+ * it is a row-major [M, N] device buffer of the output's element type. */
+int llmcp_q8_linear_add(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                        const llmcp_memref_i8_1d *weight,
+                        const llmcp_memref_f32_2d *residual,
+                        llmcp_memref_f32_2d *output, int32_t execution_mode);
+
+/* bf16 in, residual and out: the linear's result is rounded to bf16 first,
+ * then the bf16 add as arith.addf on bf16 lowers it (both operands widened to
+ * f32, added, rounded to bf16 to nearest even). */
+int llmcp_q8_linear_add_bf16(llmcp_q8_ctx *ctx,
+                             const llmcp_memref_bf16_2d *input,
+                             const llmcp_memref_i8_1d *weight,
+                             const llmcp_memref_bf16_2d *residual,
+                             llmcp_memref_bf16_2d *output,
+                             int32_t execution_mode);
 
 /* Fused SwiGLU hidden: h = silu(x . Wg^T) * (x . Wu^T), the pair
  * `linear{activation=silu}` + `mul` that FuseSiluMul produces
@@ -325,6 +348,16 @@ int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
                                      llmcp_memref_i8_1d *w_up,
                                      llmcp_memref_f32_2d *output,
                                      int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_linear_add(llmcp_memref_f32_2d *input,
+                                         llmcp_memref_i8_1d *weight,
+                                         llmcp_memref_f32_2d *residual,
+                                         llmcp_memref_f32_2d *output,
+                                         int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_linear_add_bf16(llmcp_memref_bf16_2d *input,
+                                              llmcp_memref_i8_1d *weight,
+                                              llmcp_memref_bf16_2d *residual,
+                                              llmcp_memref_bf16_2d *output,
+                                              int32_t execution_mode);
 int32_t _mlir_ciface_llmcp_q8_lm_head(llmcp_memref_f32_2d *hidden,
                                       llmcp_memref_i8_1d *table,
                                       llmcp_memref_f32_2d *logits,

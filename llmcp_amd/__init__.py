@@ -74,6 +74,8 @@ EXPORTS = [
     "llmcp_q8_lm_head_bf16", "llmcp_q8_embedding_bf16",
     "_mlir_ciface_llmcp_q8_linear_bf16", "_mlir_ciface_llmcp_q8_swiglu_bf16",
     "_mlir_ciface_llmcp_q8_lm_head_bf16", "_mlir_ciface_llmcp_q8_embedding_bf16",
+    "llmcp_q8_linear_add", "llmcp_q8_linear_add_bf16",
+    "_mlir_ciface_llmcp_q8_linear_add", "_mlir_ciface_llmcp_q8_linear_add_bf16",
 ]
 
 
@@ -146,6 +148,10 @@ def lib():
         "_mlir_ciface_llmcp_q8_swiglu_bf16": (I32, [P, P, P, P, I32]),
         "_mlir_ciface_llmcp_q8_lm_head_bf16": (I32, [P, P, P, P, I32]),
         "_mlir_ciface_llmcp_q8_embedding_bf16": (I32, [P, P, P]),
+        "llmcp_q8_linear_add": (I, [P, P, P, P, P, I32]),
+        "llmcp_q8_linear_add_bf16": (I, [P, P, P, P, P, I32]),
+        "_mlir_ciface_llmcp_q8_linear_add": (I32, [P, P, P, P, I32]),
+        "_mlir_ciface_llmcp_q8_linear_add_bf16": (I32, [P, P, P, P, I32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -326,6 +332,16 @@ class Context:
         if dtype not in DTYPES:
             raise ValueError("dtype must be one of %r" % (DTYPES,))
         return getattr(lib(), name + ("_bf16" if dtype == "bf16" else ""))
+
+    def linear_add(self, x, w, r, y, m, mode="decode", dtype="f32"):
+        """y = r + linear(x): the residual add in the linear's epilogue
+        (r and y [m, w.rows], same element type; r may be y)."""
+        xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, w.cols)
+        ri = f32_memref(r.ptr if hasattr(r, "ptr") else r, m, w.rows)
+        yo = f32_memref(y.ptr if hasattr(y, "ptr") else y, m, w.rows)
+        check(self._entry("llmcp_q8_linear_add", dtype)(
+            self.handle, ctypes.byref(xi), ctypes.byref(w.memref()),
+            ctypes.byref(ri), ctypes.byref(yo), MODE[mode]))
 
     def linear(self, x, w, y, m, activation="none", mode="decode", dtype="f32"):
         xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, w.cols)

@@ -156,7 +156,8 @@ struct Seg6 {
 // stays within 256 VGPRs, which keeps the MFMA results in VGPRs where the
 // epilogue reads them (no accumulation-register round trips).
 // EPI: activation code in bits 0-1, bf16 output in bit 2, the SwiGLU
-// multiply by `mul` in bit 3 (compile time: the epilogue is inlined for
+// multiply by `mul` (f32) in bit 3, the residual add of `mul` (y's element
+// type, no activation) in bit 4 (compile time: the epilogue is inlined for
 // every accumulator element).
 template <int WM, int WN, int NST, bool FMA, int SEG, int EPI, bool PERSIST>
 __global__ __launch_bounds__(64 * WM * WN)
@@ -164,7 +165,7 @@ __attribute__((amdgpu_waves_per_eu(WM * WN >= 12 ? 3 : 2)))
 void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
                  int32_t row_tiles, int32_t nblk, const uint8_t *__restrict__ w,
                  int64_t n_rows, int64_t m_rows, int32_t passes, int32_t m_tiles,
-                 int32_t n_tiles, void *y, int64_t ldy, const float *mul,
+                 int32_t n_tiles, void *y, int64_t ldy, const void *mul,
                  int64_t ldg) {
   typedef GemmStage<WM, WN, SEG> St;
   static_assert(NST == 2 || NST == 4, "stage buffers");
@@ -363,17 +364,21 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
 
   float acc[16];
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  // SwiGLU: this lane's 16 gate values, loaded at the start of the last
-  // group of stages so that their latency hides behind it (indices clamped,
-  // no branch: a branch around a load would disturb the DMA wait tracking).
+  // SwiGLU gate values or residuals: this lane's 16, loaded at the start of
+  // the last group of stages so that their latency hides behind it (indices
+  // clamped, no branch: a branch around a load would disturb the DMA wait
+  // tracking).  bf16 residuals are widened exactly.
   float gpre[16];
   auto prefetch_gate = [&]() __attribute__((always_inline)) {
-    if constexpr ((EPI & 8) != 0) {
+    if constexpr ((EPI & 24) != 0) {
       const int64_t nc = min(n0 + 32 * wn + li, n_rows - 1);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t mc = min(m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3), m_rows - 1);
-        gpre[v] = mul[mc * ldg + nc];
+        if constexpr ((EPI & 16) != 0 && (EPI & 4) != 0)
+          gpre[v] = bf16_to_float(((const uint16_t *)mul)[mc * ldg + nc]);
+        else
+          gpre[v] = ((const float *)mul)[mc * ldg + nc];
       }
     }
   };
@@ -499,7 +504,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
           compute(s, stage(i), min(s + NST - 1, last), nbuf, cur);
       }
     };
-    if constexpr (PERSIST || (EPI & 8) != 0) {
+    if constexpr (PERSIST || (EPI & 24) != 0) {
       for (int s0 = 0; s0 < stages - NST; s0 += NST) group(s0, std::false_type{});
       group(stages - NST, std::true_type{});
     } else {
@@ -520,6 +525,10 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
           const float g = gpre[v];
           o = (EPI & 4) != 0 ? bf16_to_float(float_to_bf16(g)) * bf16_to_float(float_to_bf16(o))
                              : g * o;
+        }
+        if constexpr ((EPI & 16) != 0) {
+          // residual add (AddOpLowering): the result as stored, plus r, in f32
+          o = (EPI & 4) != 0 ? bf16_to_float(float_to_bf16(o)) + gpre[v] : o + gpre[v];
         }
         if constexpr ((EPI & 4) != 0)
           ((uint16_t *)y)[m * ldy + n] = float_to_bf16(o);
@@ -549,16 +558,19 @@ static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
   // (with S = 6 the next tile's offsets spill registers)
   constexpr bool kPersist = WM * WN >= 12 && SEG != 6;
   const unsigned total = (unsigned)((n_tiles + 7) / 8 * 8 * m_tiles);
+  // the epilogue's second operand: the SwiGLU gate or the residual
+  const void *mp = (EPI & 16) != 0 ? l.add : (const void *)l.mul;
+  const int64_t ld = (EPI & 16) != 0 ? l.ldr : l.ldg;
   if (kPersist && grid < total)
     hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, kPersist>), dim3(grid),
                        dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
                        l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
-                       l.mul, l.ldg);
+                       mp, ld);
   else
     hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, false>), dim3(total),
                        dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
                        l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
-                       l.mul, l.ldg);
+                       mp, ld);
 }
 
 template <int WM, int WN, int NST, bool FMA, int SEG>
@@ -571,6 +583,10 @@ static void launch_gemm_e(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
   if (l.mul) {  // the SwiGLU up linear: no activation of its own
     if (l.y_bf16) return launch_gemm_k<WM, WN, NST, FMA, SEG, 12>(l, passes, m_tiles, n_tiles, grid, s);
     return launch_gemm_k<WM, WN, NST, FMA, SEG, 8>(l, passes, m_tiles, n_tiles, grid, s);
+  }
+  if (l.add) {  // linear + residual add: no activation
+    if (l.y_bf16) return launch_gemm_k<WM, WN, NST, FMA, SEG, 20>(l, passes, m_tiles, n_tiles, grid, s);
+    return launch_gemm_k<WM, WN, NST, FMA, SEG, 16>(l, passes, m_tiles, n_tiles, grid, s);
   }
   switch ((l.activation & 3) | (l.y_bf16 ? 4 : 0)) {
     LLMCP_GEMM_EPI(1) LLMCP_GEMM_EPI(2) LLMCP_GEMM_EPI(3) LLMCP_GEMM_EPI(4)

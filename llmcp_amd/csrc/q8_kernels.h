@@ -46,6 +46,9 @@ struct GemvLaunch {
   int64_t cols = 0;              // K
   int nmat = 1;                  // 2 = fused SwiGLU (gate, up)
   int activation = 0;            // llmcp_q8_activation (nmat == 1 only)
+  const void *residual = nullptr;      // non-null (one matrix, no activation,
+                                       // no argmax): y = r + acc, r [rows] of
+                                       // y's element type (may alias y)
   unsigned long long *keys = nullptr;  // non-null: fused argmax into these
   int64_t *argmax_out = nullptr;       // kArgmaxSlots slots, zero on entry
 };                                     // and left zero
@@ -89,6 +92,11 @@ struct GemmLaunch {
   // y is f32).  A bf16 result rounds both factors to bf16 first.
   const float *mul = nullptr;
   int64_t ldg = 0;
+  // Non-null (no activation, no mul): the residual add in the epilogue,
+  // y = r + acc with r [m, ldr] of y's element type (it may alias y); a bf16
+  // result rounds acc to bf16 first and adds in f32.
+  const void *add = nullptr;
+  int64_t ldr = 0;
 };
 
 hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);

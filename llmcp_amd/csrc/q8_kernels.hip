@@ -410,7 +410,8 @@ struct GemvArgs {
   const uint8_t *w0;
   const uint8_t *w1;
   void *y;           // output row, f32 or bf16
-  unsigned long long *keys;  // ARGMAX: one (value, index) key per workgroup
+  const void *r;     // V bit 3: the residual row (y's element type)
+  unsigned long long *keys;  // ARGMAX: kArgmaxSlots slots folded into
   int64_t groups;
   int32_t blocks;
   int32_t passes;
@@ -502,12 +503,15 @@ __host__ __device__ constexpr int row_slots(int pc, int w) {
 // them in block order; the next pass's prepare() is scheduled together with
 // the current chain(), so the dots overlap the serial DPP additions.
 // V packs the compile-time variant: bit 0 the input row is bf16 (IN_WG),
-// bit 1 the output is bf16, bit 2 a one-matrix GEMV applies a.act.
+// bit 1 the output is bf16, bit 2 a one-matrix GEMV applies a.act, bit 3 a
+// one-matrix GEMV adds the residual row a.r to its (rounded) result.
 template <int NMAT, bool ARGMAX, int IN, int W, int D, int PC, int V>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   constexpr bool XB = (V & 1) != 0;
   constexpr bool YB = (V & 2) != 0;
   constexpr bool ACTV = (V & 4) != 0;
+  constexpr bool ADD = (V & 8) != 0;
+  static_assert(!ADD || (NMAT == 1 && !ARGMAX && !ACTV), "residual add variants");
   extern __shared__ __align__(16) unsigned char lds[];  // IN_WG input row
   __shared__ unsigned long long key_l[W];
   const int passes = PC > 0 ? PC : a.passes;
@@ -804,6 +808,14 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   }
   const bool owner = active && j == 15;
   if (owner) {
+    // residual add (AddOpLowering, LowerToLinalg.cpp:359-375): the linear's
+    // result as stored, plus r, in f32; bf16 rounds once more
+    if constexpr (ADD) {
+      if constexpr (YB)
+        y = bf16_to_float(float_to_bf16(y)) + bf16_to_float(((const uint16_t *)a.r)[row]);
+      else
+        y = y + ((const float *)a.r)[row];
+    }
     if constexpr (YB)
       ((uint16_t *)a.y)[row] = float_to_bf16(y);
     else
@@ -1106,7 +1118,9 @@ static hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
   const int xb = (IN == IN_WG && l.x_bf16) ? 1 : 0;
   const int yb = l.y_bf16 ? 2 : 0;
   const int av = (l.nmat == 1 && !l.keys && l.activation != 0) ? 4 : 0;
-  const int v = xb | yb | av;
+  const int ad = l.residual ? 8 : 0;
+  if (ad && (l.nmat != 1 || l.keys || av)) return hipErrorInvalidValue;
+  const int v = xb | yb | av | ad;
   if (l.nmat == 2) {
     if (v == 0) return launch_gemv_t<2, false, IN, 0>(a, s);
     if (v == (IN == IN_WG ? 3 : 2)) return launch_gemv_t<2, false, IN, IN == IN_WG ? 3 : 2>(a, s);
@@ -1123,6 +1137,8 @@ static hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
       case 3: return launch_gemv_t<1, false, IN, 3>(a, s);
       case 4: return launch_gemv_t<1, false, IN, 4>(a, s);
       case 7: return launch_gemv_t<1, false, IN, 7>(a, s);
+      case 8: return launch_gemv_t<1, false, IN, 8>(a, s);
+      case 11: return launch_gemv_t<1, false, IN, 11>(a, s);
       default: return hipErrorInvalidValue;
     }
   }
@@ -1131,6 +1147,8 @@ static hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
     case 2: return launch_gemv_t<1, false, IN, 2>(a, s);
     case 4: return launch_gemv_t<1, false, IN, 4>(a, s);
     case 6: return launch_gemv_t<1, false, IN, 6>(a, s);
+    case 8: return launch_gemv_t<1, false, IN, 8>(a, s);
+    case 10: return launch_gemv_t<1, false, IN, 10>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1143,6 +1161,7 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
   a.w0 = l.w[0];
   a.w1 = l.w[1] ? l.w[1] : l.w[0];
   a.y = l.y;
+  a.r = l.residual;
   a.keys = l.keys;
   a.groups = l.rows / kLanes;
   a.blocks = (int32_t)(l.cols / kBlock);

@@ -649,7 +649,7 @@ int llmcp_q8_upload_arena(llmcp_q8_ctx *ctx, const void *file,
 // the input inside the GEMV; wide ones (lm_head) quantize it once first.
 static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
                        const Tensor *w1, const Rows &y, int activation,
-                       int64_t *argmax_dev) {
+                       int64_t *argmax_dev, const Rows *residual = nullptr) {
   int rc = ensure_decode_scratch(ctx, w0->rows, w0->cols);
   if (rc) return rc;
   GemvLaunch l;
@@ -675,6 +675,7 @@ static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
   l.cols = w0->cols;
   l.nmat = w1 ? 2 : 1;
   l.activation = activation;
+  if (residual) l.residual = residual->data;
   if (argmax_dev) {
     l.keys = ctx->keys;
     l.argmax_out = argmax_dev;
@@ -714,7 +715,7 @@ static int gemm_quantize(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w) {
 // (nullable, f32 [m, ldg]) turns the epilogue into the SwiGLU multiply.
 static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
                        const Rows &out, int activation, const float *mul,
-                       int64_t ldg) {
+                       int64_t ldg, const Rows *residual = nullptr) {
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   GemmLaunch g;
   g.qa = ctx->qa;
@@ -732,6 +733,10 @@ static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
   g.fma = ctx->gemm_fma;
   g.mul = mul;
   g.ldg = ldg;
+  if (residual) {
+    g.add = residual->data;
+    g.ldr = residual->ld;
+  }
   hipError_t e = launch_gemm(g, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "gemm launch");
   return LLMCP_Q8_OK;
@@ -785,6 +790,30 @@ static int linear_impl(llmcp_q8_ctx *ctx, const Rows &in,
   // the GEMV (scalar epilogue) beats a 1/128-full GEMM tile.
   if (m == 1) return gemv_common(ctx, in, w, nullptr, out, activation, nullptr);
   return gemm_common(ctx, in, w, out, activation);
+}
+
+// llmcp.linear + llmcp.add (ModelBuilder.cpp:271, :275): the residual add
+// in the GEMV's or GEMM's epilogue.
+static int linear_add_impl(llmcp_q8_ctx *ctx, const Rows &in,
+                           const llmcp_memref_i8_1d *weight, const Rows &res,
+                           const Rows &out, int32_t execution_mode) {
+  const Tensor *w = nullptr;
+  int rc = resolve_weight(ctx, weight, &w);
+  if (rc) return rc;
+  if ((rc = check_linear_shapes(in, w, out))) return rc;
+  if (res.rows != out.rows || res.cols != out.cols)
+    return fail(LLMCP_Q8_DECLINED, "residual must be [M, N] like the output");
+  if ((rc = check_mode(execution_mode))) return rc;
+  const int64_t m = in.rows;
+  if (m == 0) return LLMCP_Q8_OK;
+  if ((rc = set_device(ctx))) return rc;
+  if (execution_mode == LLMCP_Q8_DECODE && m != 1)
+    return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
+                (long long)m);
+  if (m == 1)
+    return gemv_common(ctx, in, w, nullptr, out, LLMCP_Q8_ACT_NONE, nullptr, &res);
+  if ((rc = gemm_quantize(ctx, in, w))) return rc;
+  return gemm_launch(ctx, m, w, out, LLMCP_Q8_ACT_NONE, nullptr, 0, &res);
 }
 
 static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
@@ -926,6 +955,32 @@ int llmcp_q8_linear_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
   if (!view_of(input, true, in) || !view_of(output, true, out))
     return fail(LLMCP_Q8_DECLINED, kDenseMsg);
   return linear_impl(ctx, in, weight, out, activation, execution_mode);
+}
+
+int llmcp_q8_linear_add(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                        const llmcp_memref_i8_1d *weight,
+                        const llmcp_memref_f32_2d *residual,
+                        llmcp_memref_f32_2d *output, int32_t execution_mode) {
+  if (!ctx || !residual) return fail(LLMCP_Q8_EINVAL, "null argument");
+  Rows in, res, out;
+  if (!view_of(input, false, in) || !view_of(residual, false, res) ||
+      !view_of(output, false, out))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return linear_add_impl(ctx, in, weight, res, out, execution_mode);
+}
+
+int llmcp_q8_linear_add_bf16(llmcp_q8_ctx *ctx,
+                             const llmcp_memref_bf16_2d *input,
+                             const llmcp_memref_i8_1d *weight,
+                             const llmcp_memref_bf16_2d *residual,
+                             llmcp_memref_bf16_2d *output,
+                             int32_t execution_mode) {
+  if (!ctx || !residual) return fail(LLMCP_Q8_EINVAL, "null argument");
+  Rows in, res, out;
+  if (!view_of(input, true, in) || !view_of(residual, true, res) ||
+      !view_of(output, true, out))
+    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+  return linear_add_impl(ctx, in, weight, res, out, execution_mode);
 }
 
 int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
@@ -1203,6 +1258,26 @@ int32_t _mlir_ciface_llmcp_q8_linear(llmcp_memref_f32_2d *input,
   if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
   return llmcp_q8_linear(g_default_ctx, input, weight, output, activation,
                          execution_mode);
+}
+
+int32_t _mlir_ciface_llmcp_q8_linear_add(llmcp_memref_f32_2d *input,
+                                         llmcp_memref_i8_1d *weight,
+                                         llmcp_memref_f32_2d *residual,
+                                         llmcp_memref_f32_2d *output,
+                                         int32_t execution_mode) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  return llmcp_q8_linear_add(g_default_ctx, input, weight, residual, output,
+                             execution_mode);
+}
+
+int32_t _mlir_ciface_llmcp_q8_linear_add_bf16(llmcp_memref_bf16_2d *input,
+                                              llmcp_memref_i8_1d *weight,
+                                              llmcp_memref_bf16_2d *residual,
+                                              llmcp_memref_bf16_2d *output,
+                                              int32_t execution_mode) {
+  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+  return llmcp_q8_linear_add_bf16(g_default_ctx, input, weight, residual,
+                                  output, execution_mode);
 }
 
 int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
