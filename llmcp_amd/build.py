@@ -15,6 +15,10 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["q8_kernels.hip", "q8_gemm.hip", "q8_runtime.cpp"]
 
+ROOT = os.path.dirname(HERE)
+CONSUMER_SRC = os.path.join(ROOT, "tests", "c_consumer", "q8_consumer.cpp")
+CONSUMER = os.path.join(ROOT, "tests", "c_consumer", "q8_consumer")
+
 COMMON = [
     "--offload-arch=gfx950",
     "-O3",
@@ -54,6 +58,25 @@ def build(verbose=False):
     return LIB
 
 
+def build_consumer(verbose=False):
+    """Links the C++17 test host of the C ABI against the built library with
+    the plain host compiler, as an AOT runtime would: only include/ and
+    -lllmcp_q8, no HIP headers."""
+    tmp = CONSUMER + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra",
+           "-I", os.path.join(ROOT, "include"), CONSUMER_SRC,
+           "-L", HERE, "-lllmcp_q8",
+           "-Wl,-rpath,$ORIGIN/../../llmcp_amd",
+           "-Wl,-rpath-link,/opt/rocm/lib", "-Wl,-rpath-link,/opt/rocm/llvm/lib",
+           "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, CONSUMER)
+    return CONSUMER
+
+
 if __name__ == "__main__":
     build(verbose="-v" in sys.argv)
+    build_consumer(verbose="-v" in sys.argv)
     print(LIB)

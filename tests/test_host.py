@@ -132,3 +132,22 @@ def test_arena_accepts_mixed_dtypes(q8, tmp_path, oracle):
                              "dtype": "F32", "shape": [4]})
     f2 = _rewrite_manifest(f, add_f32)
     assert q8.arena_inspect(f2) == (2, 1)
+
+
+def consumer_binary():
+    from llmcp_amd import build as b
+    if not os.path.exists(b.CONSUMER):
+        b.build_consumer()
+    return b.CONSUMER
+
+
+def test_cpp_consumer_host_part(q8, tmp_path):
+    """A C++17 program that includes only llmcp_q8.h and links -lllmcp_q8
+    (tests/c_consumer/q8_consumer.cpp) packs the matmul benchmark's all-ones
+    rows, writes, maps and inspects an arena, and finds its tensors through
+    the manifest, with no device touched."""
+    import subprocess
+    r = subprocess.run([consumer_binary(), "--cpu", str(tmp_path)],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "host part ok" in r.stdout
