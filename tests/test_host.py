@@ -151,3 +151,92 @@ def test_cpp_consumer_host_part(q8, tmp_path):
                        capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "host part ok" in r.stdout
+
+
+# Property tests of the arena validator on corrupted files: whatever the
+# bytes, llmcp_q8_arena_inspect returns OK or LLMCP_Q8_EFORMAT and never
+# reads outside the buffer it was given (each case runs on a copy cut to its
+# exact length, so an over-read past the end would touch unmapped memory or
+# garbage, not the original file's tail).
+from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import strategies as st  # noqa: E402
+
+
+def _inspect_outcome(q8, f):
+    try:
+        n, nq = q8.arena_inspect(f)
+    except q8.Q8Error as e:
+        assert e.code == q8.EFORMAT, e
+        return None
+    assert 0 <= nq <= n
+    return n, nq
+
+
+@pytest.fixture(scope="module")
+def fuzz_arena(q8, oracle, tmp_path_factory):
+    rng = np.random.default_rng(5)
+    a = oracle.pack_q8_0_p4((rng.standard_normal((16, 64)) * 0.02).astype(np.float32))
+    b = oracle.pack_q8_0_p4((rng.standard_normal((8, 96)) * 0.02).astype(np.float32))
+    path = str(tmp_path_factory.mktemp("fuzz") / "w.bin")
+    q8.write_arena(path, [("model.a.weight", 16, 64, a), ("model.b.weight", 8, 96, b)])
+    return np.fromfile(path, dtype=np.uint8)
+
+
+_SETTINGS = settings(max_examples=400, deadline=None, derandomize=True,
+                     suppress_health_check=[HealthCheck.function_scoped_fixture])
+
+
+@_SETTINGS
+@given(data=st.data())
+def test_arena_fuzz_byte_mutations(q8, fuzz_arena, data):
+    f = fuzz_arena.copy()
+    edits = data.draw(st.lists(st.tuples(st.integers(0, f.size - 1), st.integers(0, 255)),
+                               min_size=1, max_size=8))
+    for pos, val in edits:
+        f[pos] = val
+    cut = data.draw(st.integers(0, f.size))
+    _inspect_outcome(q8, np.array(f[:cut]))
+
+
+@_SETTINGS
+@given(data=st.data())
+def test_arena_fuzz_manifest_text(q8, fuzz_arena, data):
+    arena = struct.unpack_from("<Q", fuzz_arena, 16)[0]
+    text = bytearray(fuzz_arena[arena:].tobytes())
+    for _ in range(data.draw(st.integers(1, 4))):
+        op = data.draw(st.sampled_from(["replace", "insert", "delete"]))
+        pos = data.draw(st.integers(0, len(text) - 1))
+        ch = data.draw(st.sampled_from(list(b'{}[]":,0123456789-.eE \\tnulfas') + [0, 0xff]))
+        if op == "replace":
+            text[pos] = ch
+        elif op == "insert":
+            text.insert(pos, ch)
+        elif len(text) > 1:
+            del text[pos]
+    out = np.concatenate([fuzz_arena[:arena], np.frombuffer(bytes(text), np.uint8)])
+    struct.pack_into("<Q", out, 32, len(text))
+    _inspect_outcome(q8, out)
+
+
+@_SETTINGS
+@given(field=st.sampled_from(["offset", "size", "shape0", "shape1", "total_bytes",
+                              "arena_offset", "manifest_bytes"]),
+       value=st.one_of(st.integers(-2 ** 63, 2 ** 64 - 1),
+                       st.sampled_from([2 ** 63 - 1, 2 ** 63, 2 ** 64 - 1, -1, 2 ** 32,
+                                        2 ** 62, 3 * 2 ** 61])))
+def test_arena_fuzz_numeric_extremes(q8, fuzz_arena, field, value):
+    f = fuzz_arena.copy()
+    if field in ("arena_offset", "manifest_bytes"):
+        struct.pack_into("<Q", f, 16 if field == "arena_offset" else 32, value % 2 ** 64)
+        _inspect_outcome(q8, f)
+        return
+
+    def edit(m):
+        t = m["tensors"][1]
+        if field == "total_bytes":
+            m["total_bytes"] = value
+        elif field.startswith("shape"):
+            t["shape"][int(field[-1])] = value
+        else:
+            t[field] = value
+    _inspect_outcome(q8, _rewrite_manifest(f, edit))
