@@ -531,7 +531,7 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": (load_traffic() or {}).get("hbm_bytes_per_launch"),
-                     "kernel": "gemv_kernel<2,false,IN_WG,4,5,5,0> (fused gate/up "
+                     "kernel": "gemv_kernel<2,false,IN_WG,4,4,5,0> (fused gate/up "
                                "SwiGLU, 4-wave workgroups, input row quantized "
                                "per workgroup; timed alone via llmcp_q8_swiglu)",
                      "launch_us": round(res["gu_launch_us"], 3),
