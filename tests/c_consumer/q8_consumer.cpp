@@ -182,6 +182,49 @@ int main(int argc, char **argv) {
                   (double)yf[0]);
     }
   }
+  // One device-resident decode step through the C interface: the token id
+  // lives in HBM, the embedding gathers its row of the 256 x 2560 table, the
+  // tied lm_head scores every row and writes the first-maximum id back in
+  // HBM (llmcp-benchmark.cpp:93-101 does the argmax on the host).  On the
+  // fixture every row dequantizes to 127 * f16(0x2008) = 131064 / 131072
+  // exactly, all logits are equal, and the first maximum is row 0.
+  {
+    const int64_t v = rows[1], hdim = cols[1];
+    MemRef<int8_t, 1> table{(int8_t *)(file + off[1]), (int8_t *)(file + off[1]), 0,
+                            {v * (hdim + hdim / 16)}, {1}};
+    void *tok = nullptr, *hid = nullptr, *lg = nullptr, *am = nullptr;
+    if (llmcp_q8_dev_alloc(ctx, 8, &tok) || llmcp_q8_dev_alloc(ctx, (uint64_t)hdim * 4, &hid) ||
+        llmcp_q8_dev_alloc(ctx, (uint64_t)v * 4, &lg) || llmcp_q8_dev_alloc(ctx, 8, &am))
+      return fail("alloc");
+    const int64_t token = 5, sentinel = -1;
+    llmcp_q8_memcpy_h2d(ctx, tok, &token, 8);
+    llmcp_q8_memcpy_h2d(ctx, am, &sentinel, 8);
+    MemRef<int64_t, 1> tm{(int64_t *)tok, (int64_t *)tok, 0, {1}, {1}};
+    MemRef<float, 2> hm{(float *)hid, (float *)hid, 0, {1, hdim}, {hdim, 1}};
+    MemRef<float, 2> lm{(float *)lg, (float *)lg, 0, {1, v}, {v, 1}};
+    MemRef<int64_t, 1> amm{(int64_t *)am, (int64_t *)am, 0, {1}, {1}};
+    if (_mlir_ciface_llmcp_q8_embedding((llmcp_memref_i64_1d *)&tm, (llmcp_memref_i8_1d *)&table,
+                                        (llmcp_memref_f32_2d *)&hm))
+      return fail("embedding");
+    if (_mlir_ciface_llmcp_q8_lm_head((llmcp_memref_f32_2d *)&hm, (llmcp_memref_i8_1d *)&table,
+                                      (llmcp_memref_f32_2d *)&lm, (llmcp_memref_i64_1d *)&amm,
+                                      LLMCP_Q8_DECODE))
+      return fail("lm_head");
+    std::vector<float> hv(hdim), lv(v);
+    int64_t best = -2;
+    llmcp_q8_memcpy_d2h(ctx, hv.data(), hid, (uint64_t)hdim * 4);
+    llmcp_q8_memcpy_d2h(ctx, lv.data(), lg, (uint64_t)v * 4);
+    llmcp_q8_memcpy_d2h(ctx, &best, am, 8);
+    const float row_value = 131064.0f / 131072.0f;
+    for (int64_t i = 0; i < hdim; ++i) bad += hv[i] != row_value;
+    for (int64_t i = 0; i < v; ++i) bad += lv[i] != lv[0];
+    bad += best != 0;
+    int32_t flag = -1;
+    if (llmcp_q8_ctx_check(ctx, &flag) || flag != 0) return fail("device error flag");
+    std::printf("q8_consumer: decode step: token %lld -> row value %.9g, logit %.6g, argmax %lld\n",
+                (long long)token, (double)hv[0], (double)lv[0], (long long)best);
+    for (void *p : {tok, hid, lg, am}) llmcp_q8_dev_free(ctx, p);
+  }
   llmcp_q8_ctx_destroy(ctx);
   munmap(map, fsize);
   if (bad) {

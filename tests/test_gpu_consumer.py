@@ -5,7 +5,9 @@ _mlir_ciface_ entries are called with MemRef descriptors whose weight data
 points into the mapping.  The data is llmcp-matmul-benchmark's Q8 fixture
 (llmcp-matmul-benchmark.cpp:280-289, check :331-335: first == K), at its
 registered 64x64x64 shape (tests/CMakeLists.txt:162-165) and on a decode-sized
-256x2560 tensor, for M = 1 (decode GEMV) and M = 64 (prefill GEMM)."""
+256x2560 tensor, for M = 1 (decode GEMV) and M = 64 (prefill GEMM); then one
+device-resident decode step (token id in HBM -> embedding -> lm_head -> argmax
+id in HBM), where every logit ties and the first maximum must be row 0."""
 import os
 import subprocess
 import sys
@@ -27,3 +29,4 @@ def test_cpp_consumer_arena_to_mlir_ciface(q8, tmp_path):
     assert r.returncode == 0, r.stdout + r.stderr
     assert "device part ok" in r.stdout
     assert r.stdout.count("first") == 4
+    assert "argmax 0" in r.stdout
