@@ -245,7 +245,9 @@ int llmcp_q8_mlp_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
 /* llmcp.lm_head (LowerToLinalg.cpp:729-765): f32 logits [M,V] over the tied
  * table, plus the first-maximum index of the last row written to
  * `argmax_dev` (device int64, nullable) -- the host std::max_element of
- * llmcp-benchmark.cpp:51-54 fused into the kernel. */
+ * llmcp-benchmark.cpp:51-54 on the device: fused into the GEMV for M == 1;
+ * for M > 1 (prefill only; decode declines it, as for llmcp_q8_linear) the
+ * GEMM writes all rows and a reduction reads the last one. */
 int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
                      const llmcp_memref_i8_1d *table,
                      llmcp_memref_f32_2d *logits, int64_t *argmax_dev,

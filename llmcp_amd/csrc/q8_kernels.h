@@ -71,6 +71,11 @@ constexpr int kArgmaxSlots = 2048;
 hipError_t launch_argmax_reduce(unsigned long long *slots, int64_t *out,
                                 hipStream_t s);
 
+// First-maximum index of the f32 row v[0..n) into *out, through the zeroed
+// slots (left zeroed); n < 2^32.
+hipError_t launch_argmax_row(const float *v, int64_t n, int64_t *out,
+                             unsigned long long *slots, hipStream_t s);
+
 // Prefill GEMM on int8 MFMA.  qa/sa: Q8_1 activations [m, ldq] / [m, lds],
 // zero-padded to passes*16 blocks (launch_quantize with blocks_pad).
 struct GemmLaunch {

@@ -14,6 +14,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 #include "q8_device.h"
 
 namespace llmcp_q8 {
@@ -846,6 +848,25 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// First-maximum argmax of one f32 row already in HBM (the last row of a
+// prefill lm_head's logits): the same keys as the GEMV's fused argmax,
+// folded into the same slots, so argmax_reduce_kernel finishes it.  A grid
+// stride loop over the row, one key per workgroup.
+__global__ __launch_bounds__(256) void argmax_row_kernel(
+    const float *__restrict__ v, int64_t n, unsigned long long *slots) {
+  __shared__ unsigned long long part[4];
+  unsigned long long key = 0ull;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256)
+    key = max_u64(key, argmax_key(v[i], i));
+  key = wave_max_u64(key);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = key;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    argmax_fold(slots,
+                max_u64(max_u64(part[0], part[1]), max_u64(part[2], part[3])));
+}
+
 // Second stage of the fused argmax: one workgroup of 1024 threads takes the
 // kArgmaxSlots slots (swapping in 0, so the slots are clear for the next
 // call without a memset) and writes the index of the first maximum.  With
@@ -1175,6 +1196,17 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
                              : launch_gemv_in<IN_PRE>(a, l, s);
   if (e != hipSuccess || !l.keys) return e;
   return launch_argmax_reduce(l.keys, l.argmax_out, s);
+}
+
+hipError_t launch_argmax_row(const float *v, int64_t n, int64_t *out,
+                             unsigned long long *slots, hipStream_t s) {
+  if (n <= 0 || n > 0xFFFFFFFFll) return hipErrorInvalidValue;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(argmax_row_kernel, dim3(grid), dim3(256), 0, s, v, n,
+                     slots);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_argmax_reduce(slots, out, s);
 }
 
 hipError_t launch_argmax_reduce(unsigned long long *slots, int64_t *out,

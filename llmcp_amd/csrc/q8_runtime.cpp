@@ -865,10 +865,29 @@ static int lm_head_impl(llmcp_q8_ctx *ctx, const Rows &in,
   const int64_t m = in.rows;
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
-  if (m != 1)
-    return fail(LLMCP_Q8_DECLINED, "lm_head for M > 1 not available");
-  return gemv_common(ctx, in, w, nullptr, logits, LLMCP_Q8_ACT_NONE,
-                     argmax_dev);
+  if (m == 1)
+    return gemv_common(ctx, in, w, nullptr, logits, LLMCP_Q8_ACT_NONE,
+                       argmax_dev);
+  // Several rows (prefill; decode takes one): the GEMM writes every row's
+  // logits, then the first maximum of the last row is reduced from HBM.
+  if (execution_mode == LLMCP_Q8_DECODE)
+    return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
+                (long long)m);
+  if ((rc = gemm_common(ctx, in, w, logits, LLMCP_Q8_ACT_NONE))) return rc;
+  if (!argmax_dev) return LLMCP_Q8_OK;
+  if ((rc = ensure_argmax_slots(ctx))) return rc;
+  if (ctx->keys_dirty) {
+    hipError_t e = launch_argmax_reduce(ctx->keys, nullptr, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "argmax clear launch");
+    ctx->keys_dirty = false;
+  }
+  hipError_t e = launch_argmax_row((const float *)logits.data + (m - 1) * logits.ld,
+                                   logits.cols, argmax_dev, ctx->keys, ctx->stream);
+  if (e != hipSuccess) {
+    ctx->keys_dirty = true;
+    return hip_fail(e, "argmax launch");
+  }
+  return LLMCP_Q8_OK;
 }
 
 static int mlp_impl(llmcp_q8_ctx *ctx, const Rows &in,
