@@ -70,7 +70,8 @@ enum llmcp_q8_activation {
 /* Per-block epilogue of the prefill GEMM.  Both are the reference's math:
  * FMA    acc = fma(f32(I), sa*dw, acc)  -- the SDOT GEMM, Q8Matmul.cpp:204-223
  * SCALAR acc = acc + f32(I)*(sa*dw)     -- the x86 scalar path, Q8Scalar.cpp:192-199
- * The decode GEMV always computes the SCALAR form. */
+ * The decode path (GEMV, or the GEMM for several rows in DECODE mode)
+ * always computes the SCALAR form. */
 enum llmcp_q8_epilogue { LLMCP_Q8_EPI_SCALAR = 0, LLMCP_Q8_EPI_FMA = 1 };
 
 /* llmcp.execution_mode (LowerToLinalg.cpp:40-52). */
@@ -168,9 +169,11 @@ int llmcp_q8_arena_inspect(const void *file, uint64_t file_bytes,
 
 /* llmcp.linear with weight_format q8_0_p4 (LowerToLinalg.cpp:143-209):
  * y[M,N] = act(x[M,K] . W[N,K]^T), x quantized per call to Q8_1 blocks.
- * execution_mode DECODE requires M == 1 and runs the GEMV; PREFILL runs the
- * int8-MFMA GEMM for M > 1 (its epilogue: llmcp_q8_set_gemm_epilogue) and
- * the GEMV for M == 1.  activation: llmcp_q8_activation. */
+ * M == 1 runs the GEMV (scalar epilogue) in either mode.  M > 1 runs the
+ * int8-MFMA GEMM: PREFILL with the epilogue llmcp_q8_set_gemm_epilogue
+ * selects, DECODE (which the reference's decode emitter accepts for any M,
+ * Q8Decode.cpp:236-256) always with the scalar one.  activation:
+ * llmcp_q8_activation. */
 int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                     const llmcp_memref_i8_1d *weight,
                     llmcp_memref_f32_2d *output, int32_t activation,
@@ -246,8 +249,8 @@ int llmcp_q8_mlp_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
  * table, plus the first-maximum index of the last row written to
  * `argmax_dev` (device int64, nullable) -- the host std::max_element of
  * llmcp-benchmark.cpp:51-54 on the device: fused into the GEMV for M == 1;
- * for M > 1 (prefill only; decode declines it, as for llmcp_q8_linear) the
- * GEMM writes all rows and a reduction reads the last one. */
+ * for M > 1 the GEMM writes all rows (epilogue as for llmcp_q8_linear) and
+ * a reduction reads the last one. */
 int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
                      const llmcp_memref_i8_1d *table,
                      llmcp_memref_f32_2d *logits, int64_t *argmax_dev,

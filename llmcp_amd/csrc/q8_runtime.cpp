@@ -713,9 +713,12 @@ static int gemm_quantize(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w) {
 
 // int8-MFMA GEMM of the quantized rows (gemm_quantize) against w.  `mul`
 // (nullable, f32 [m, ldg]) turns the epilogue into the SwiGLU multiply.
+// Decode-mode calls take the scalar epilogue whatever the prefill variant
+// (the decode path computes the x86 scalar form for every M, like the GEMV).
 static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
                        const Rows &out, int activation, const float *mul,
-                       int64_t ldg, const Rows *residual = nullptr) {
+                       int64_t ldg, bool decode,
+                       const Rows *residual = nullptr) {
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   GemmLaunch g;
   g.qa = ctx->qa;
@@ -730,7 +733,7 @@ static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
   g.y_bf16 = out.bf16;
   g.ldy = out.ld;
   g.activation = activation;
-  g.fma = ctx->gemm_fma;
+  g.fma = ctx->gemm_fma && !decode;
   g.mul = mul;
   g.ldg = ldg;
   if (residual) {
@@ -743,10 +746,10 @@ static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
 }
 
 static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
-                       const Rows &out, int activation) {
+                       const Rows &out, int activation, bool decode) {
   int rc = gemm_quantize(ctx, in, w);
   if (rc) return rc;
-  return gemm_launch(ctx, in.rows, w, out, activation, nullptr, 0);
+  return gemm_launch(ctx, in.rows, w, out, activation, nullptr, 0, decode);
 }
 
 static int check_linear_shapes(const Rows &in, const Tensor *w,
@@ -783,13 +786,13 @@ static int linear_impl(llmcp_q8_ctx *ctx, const Rows &in,
   const int64_t m = in.rows;
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
-  if (execution_mode == LLMCP_Q8_DECODE && m != 1)
-    return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
-                (long long)m);
   // One row (decode, or a one-row prefill such as the last-row lm_head):
-  // the GEMV (scalar epilogue) beats a 1/128-full GEMM tile.
+  // the GEMV (scalar epilogue) beats a 1/128-full GEMM tile.  Several rows:
+  // the GEMM (decode ones with the scalar epilogue, as Q8Decode.cpp:236-256
+  // accepts any M).
   if (m == 1) return gemv_common(ctx, in, w, nullptr, out, activation, nullptr);
-  return gemm_common(ctx, in, w, out, activation);
+  return gemm_common(ctx, in, w, out, activation,
+                     execution_mode == LLMCP_Q8_DECODE);
 }
 
 // llmcp.linear + llmcp.add (ModelBuilder.cpp:271, :275): the residual add
@@ -807,13 +810,11 @@ static int linear_add_impl(llmcp_q8_ctx *ctx, const Rows &in,
   const int64_t m = in.rows;
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
-  if (execution_mode == LLMCP_Q8_DECODE && m != 1)
-    return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
-                (long long)m);
   if (m == 1)
     return gemv_common(ctx, in, w, nullptr, out, LLMCP_Q8_ACT_NONE, nullptr, &res);
   if ((rc = gemm_quantize(ctx, in, w))) return rc;
-  return gemm_launch(ctx, m, w, out, LLMCP_Q8_ACT_NONE, nullptr, 0, &res);
+  return gemm_launch(ctx, m, w, out, LLMCP_Q8_ACT_NONE, nullptr, 0,
+                     execution_mode == LLMCP_Q8_DECODE, &res);
 }
 
 static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
@@ -832,9 +833,8 @@ static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
   if (m == 1) return gemv_common(ctx, in, wg, wu, out, LLMCP_Q8_ACT_NONE, nullptr);
-  if (execution_mode == LLMCP_Q8_DECODE)
-    return fail(LLMCP_Q8_DECLINED, "decode SwiGLU requires M == 1");
-  // Prefill: the input quantized once; the gate GEMM with SiLU, then the up
+  const bool decode = execution_mode == LLMCP_Q8_DECODE;
+  // Several rows: the input quantized once; the gate GEMM with SiLU, then the up
   // GEMM whose epilogue does the multiply (MulOpLowering,
   // LowerToLinalg.cpp:377-393) with the gate's output.  f32: the gate goes
   // straight into the output and the up GEMM multiplies it in place.  bf16:
@@ -850,8 +850,10 @@ static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
     g.ld = wg->rows;
   }
   if ((rc = gemm_quantize(ctx, in, wg))) return rc;
-  if ((rc = gemm_launch(ctx, m, wg, g, LLMCP_Q8_ACT_SILU, nullptr, 0))) return rc;
-  return gemm_launch(ctx, m, wu, out, LLMCP_Q8_ACT_NONE, (const float *)g.data, g.ld);
+  if ((rc = gemm_launch(ctx, m, wg, g, LLMCP_Q8_ACT_SILU, nullptr, 0, decode)))
+    return rc;
+  return gemm_launch(ctx, m, wu, out, LLMCP_Q8_ACT_NONE, (const float *)g.data,
+                     g.ld, decode);
 }
 
 static int lm_head_impl(llmcp_q8_ctx *ctx, const Rows &in,
@@ -868,12 +870,11 @@ static int lm_head_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if (m == 1)
     return gemv_common(ctx, in, w, nullptr, logits, LLMCP_Q8_ACT_NONE,
                        argmax_dev);
-  // Several rows (prefill; decode takes one): the GEMM writes every row's
-  // logits, then the first maximum of the last row is reduced from HBM.
-  if (execution_mode == LLMCP_Q8_DECODE)
-    return fail(LLMCP_Q8_DECLINED, "decode GEMV requires M == 1 (got %lld)",
-                (long long)m);
-  if ((rc = gemm_common(ctx, in, w, logits, LLMCP_Q8_ACT_NONE))) return rc;
+  // Several rows: the GEMM writes every row's logits, then the first
+  // maximum of the last row is reduced from HBM.
+  if ((rc = gemm_common(ctx, in, w, logits, LLMCP_Q8_ACT_NONE,
+                        execution_mode == LLMCP_Q8_DECODE)))
+    return rc;
   if (!argmax_dev) return LLMCP_Q8_OK;
   if ((rc = ensure_argmax_slots(ctx))) return rc;
   if (ctx->keys_dirty) {

@@ -135,11 +135,24 @@ def test_prefill_single_row_uses_same_math(ctx, oracle):
     assert bits_equal(y, oracle.linear(x, p4, 128))
 
 
-def test_decode_declines_multi_row(ctx, oracle, q8):
+def test_decode_several_rows_use_the_scalar_epilogue(ctx, oracle, q8):
+    # The reference's decode emitter takes any M (Q8Decode.cpp:236-256); on
+    # x86 it lowers to the scalar path, so decode rows use the scalar
+    # epilogue even while the prefill GEMM is set to FMA (the default).
     rng = np.random.default_rng(9)
-    w = weights(rng, 64, 256)
-    with pytest.raises(q8.Declined):
-        run_linear(ctx, oracle, w, rng.standard_normal((2, 256)).astype(np.float32))
+    for m, n, k in ((2, 64, 256), (37, 264, 2560), (70, 1032, 9216)):
+        w = weights(rng, n, k)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        p4 = oracle.pack_q8_0_p4(w)
+        t = ctx.upload_p4(p4, n, k)
+        xd, yd = ctx.to_device(x), ctx.alloc(m * n * 4)
+        ctx.linear(xd, t, yd, m, mode="decode")
+        y = ctx.to_host(yd, (m, n), np.float32)
+        assert bits_equal(y, oracle.linear(x, p4, n, epilogue="scalar")), (m, n, k)
+        ctx.linear(xd, t, yd, m, mode="prefill")
+        assert bits_equal(ctx.to_host(yd, (m, n), np.float32),
+                          oracle.linear(x, p4, n, epilogue="fma")), (m, n, k)
+        ctx.release(t)
 
 
 def test_unregistered_weight_is_not_found(ctx, q8):

@@ -1,7 +1,8 @@
 """A seeded random sweep of the linear entry points against the oracle, bit
 for bit: shapes (N a multiple of 8, K a multiple of 32, including the
 unrolled pass counts, the segmented K = 4096 / 9216 layouts and runtime pass
-counts), decode (M = 1) and prefill (M = 1 takes the GEMV, M > 1 the GEMM
+counts), decode (M = 1 the GEMV; M > 1 the GEMM with the scalar epilogue,
+Q8Scalar.cpp:192-199) and prefill (M = 1 takes the GEMV, M > 1 the GEMM
 with the default FMA epilogue, Q8Matmul.cpp:204-223), f32 and bf16 tensors,
 the four activations (MatmulLoweringCommon.cpp:78-103) and the residual add
 (LowerToLinalg.cpp:359-375).  Each case prints its parameters, so a failure
@@ -23,9 +24,11 @@ def make_cases(count=120, seed=2026):
         k = int(rng.choice(K_CHOICES)) if rng.random() < 0.7 else 32 * int(rng.integers(1, 321))
         n = 8 * int(rng.integers(1, 513))
         r = rng.random()
-        if r < 0.4:
+        if r < 0.35:
             mode, m = "decode", 1
-        elif r < 0.5:
+        elif r < 0.45:
+            mode, m = "decode", int(rng.integers(2, 65))
+        elif r < 0.55:
             mode, m = "prefill", 1
         else:
             mode, m = "prefill", int(rng.integers(2, 301))
@@ -50,7 +53,7 @@ def test_random_linear_case(ctx, oracle, case):
     x = (rng.standard_normal((m, k)) * scale).astype(np.float32)
     if m > 2:
         x[m // 2] = 0.0  # an all-zero row: zero scales, zero dots
-    epi = "scalar" if m == 1 else "fma"
+    epi = "scalar" if m == 1 or mode == "decode" else "fma"
     t = ctx.upload_p4(p4, n, k)
     try:
         if dtype == "f32":

@@ -24,7 +24,9 @@ def swiglu_cases(count=40, seed=77):
     while len(out) < count:
         k = int(rng.choice(K_CHOICES))
         n = 8 * int(rng.integers(1, 400))
-        mode, m = ("decode", 1) if rng.random() < 0.5 else ("prefill", int(rng.integers(1, 200)))
+        r = rng.random()
+        mode, m = (("decode", 1) if r < 0.4 else ("decode", int(rng.integers(2, 40))) if r < 0.5
+                   else ("prefill", int(rng.integers(1, 200))))
         if m * n * k * 2 > 2e8:
             continue
         out.append((len(out), m, n, k, mode, "bf16" if rng.random() < 0.4 else "f32"))
@@ -39,7 +41,7 @@ def test_random_swiglu_case(ctx, oracle, case):
     pg = oracle.pack_q8_0_p4((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
     pu = oracle.pack_q8_0_p4((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
     x = rng.standard_normal((m, k)).astype(np.float32)
-    epi = "scalar" if m == 1 else "fma"
+    epi = "scalar" if m == 1 or mode == "decode" else "fma"
     tg, tu = ctx.upload_p4(pg, n, k), ctx.upload_p4(pu, n, k)
     try:
         if dtype == "f32":
@@ -66,7 +68,9 @@ def lm_cases(count=24, seed=78):
     while len(out) < count:
         k = int(rng.choice([512, 1056, 2560, 4096]))
         v = 8 * int(rng.integers(16, 6000))
-        mode, m = ("decode", 1) if rng.random() < 0.6 else ("prefill", int(rng.integers(1, 40)))
+        r = rng.random()
+        mode, m = (("decode", 1) if r < 0.5 else ("decode", int(rng.integers(2, 12))) if r < 0.6
+                   else ("prefill", int(rng.integers(1, 40))))
         if m * v * k > 2.5e8:
             continue
         out.append((len(out), m, v, k, mode, "bf16" if rng.random() < 0.4 else "f32",
@@ -83,7 +87,7 @@ def test_random_lm_head_case(ctx, oracle, case):
     x = rng.standard_normal((m, k)).astype(np.float32)
     xh = x if dtype == "f32" else oracle.f32_to_bf16_bits(x)
     xf = x if dtype == "f32" else oracle.bf16_bits_to_f32(xh)
-    epi = "scalar" if m == 1 else "fma"
+    epi = "scalar" if m == 1 or mode == "decode" else "fma"
     if tie:
         # copy the winning row to an earlier index: both logits are then
         # bit-identical and the first maximum is the copy
@@ -134,7 +138,7 @@ def test_random_embedding_case(ctx, oracle, case):
 def test_lm_head_several_rows(ctx, oracle, q8):
     # prefill with M = 8: every row's logits from the GEMM (FMA epilogue),
     # the argmax of the last row reduced from HBM, with a planted tie; the
-    # same shape in decode mode is declined like a multi-row decode linear
+    # same shape in decode mode with the scalar epilogue
     rng = np.random.default_rng(8100)
     m, v, k = 8, 40000, 1024
     w = (rng.standard_normal((v, k)) * 0.02).astype(np.float32)
@@ -151,7 +155,10 @@ def test_lm_head_several_rows(ctx, oracle, q8):
             ctx.lm_head(xd, t, ld, m, argmax=am, mode="prefill")
             assert np.array_equal(bits(ctx.to_host(ld, (m, v), np.float32)), bits(ref))
             assert int(ctx.to_host(am, (1,), np.int64)[0]) == oracle.argmax(ref[-1])
-        with pytest.raises(q8.Declined):
-            ctx.lm_head(xd, t, ld, m, argmax=am, mode="decode")
+        # decode rows: the scalar epilogue
+        ref_d = oracle.linear(x, p4, v, epilogue="scalar")
+        ctx.lm_head(xd, t, ld, m, argmax=am, mode="decode")
+        assert np.array_equal(bits(ctx.to_host(ld, (m, v), np.float32)), bits(ref_d))
+        assert int(ctx.to_host(am, (1,), np.int64)[0]) == oracle.argmax(ref_d[-1])
     finally:
         ctx.release(t)
