@@ -942,8 +942,12 @@ static int embedding_impl(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
     return fail(LLMCP_Q8_DECLINED, "tokens must be contiguous");
   if (out.cols != w->cols || out.rows != tokens->sizes[0])
     return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
-  if (tokens->sizes[0] > 65535)
-    return fail(LLMCP_Q8_DECLINED, "at most 65535 tokens per call");
+  // one thread per (token, 16 columns) on a one-dimensional grid of
+  // 256-thread workgroups, which allows 2^32 - 1 of them
+  if (tokens->sizes[0] > (1ll << 40) ||
+      (tokens->sizes[0] * (w->cols / 16) + 255) / 256 > 0xFFFFFFFFll)
+    return fail(LLMCP_Q8_DECLINED, "too many tokens for one launch (%lld)",
+                (long long)tokens->sizes[0]);
   if ((rc = set_device(ctx))) return rc;
   hipError_t e = launch_embedding(tokens->data + tokens->offset,
                                   tokens->sizes[0], w->dev, w->rows, w->cols,

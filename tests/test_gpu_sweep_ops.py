@@ -162,3 +162,24 @@ def test_lm_head_several_rows(ctx, oracle, q8):
         assert int(ctx.to_host(am, (1,), np.int64)[0]) == oracle.argmax(ref_d[-1])
     finally:
         ctx.release(t)
+
+
+def test_embedding_many_tokens(ctx, oracle):
+    # more ids than a 16-bit grid dimension would hold, f32 and bf16 rows
+    rng = np.random.default_rng(8200)
+    v, k, count = 512, 64, 70000
+    p4 = oracle.pack_q8_0_p4((rng.standard_normal((v, k)) * 0.02).astype(np.float32))
+    tokens = rng.integers(0, v, count).astype(np.int64)
+    ref = oracle.embedding(tokens, p4, k)
+    t = ctx.upload_p4(p4, v, k)
+    try:
+        td = ctx.to_device(tokens)
+        od = ctx.alloc(count * k * 4)
+        ctx.embedding(td, count, t, od)
+        assert np.array_equal(bits(ctx.to_host(od, (count, k), np.float32)), bits(ref))
+        ctx.embedding(td, count, t, od, dtype="bf16")
+        assert np.array_equal(bits(ctx.to_host(od, (count, k), np.uint16)),
+                              bits(oracle.f32_to_bf16_bits(ref)))
+        assert ctx.check_flag() == 0
+    finally:
+        ctx.release(t)
