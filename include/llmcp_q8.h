@@ -226,11 +226,12 @@ int llmcp_q8_swiglu_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
                          const llmcp_memref_i8_1d *w_up,
                          llmcp_memref_bf16_2d *output, int32_t execution_mode);
 
-/* Decode MLP of one layer, ModelBuilder.cpp:205-216 with FuseSiluMul:
- * h = silu(x . Wg^T) * (x . Wu^T), y = h . Wd^T, for M == 1.  Two kernels:
- * the fused gate/up GEMV, then the down GEMV (which quantizes h once per
- * workgroup).  `hidden` (nullable) receives h.  Results equal
- * llmcp_q8_swiglu followed by llmcp_q8_linear. */
+/* MLP of one layer, ModelBuilder.cpp:205-216 with FuseSiluMul:
+ * h = silu(x . Wg^T) * (x . Wu^T), y = h . Wd^T.  M == 1: two kernels, the
+ * fused gate/up GEMV, then the down GEMV (which quantizes h once per
+ * workgroup).  M > 1: the SwiGLU GEMMs, then the down GEMM.  `hidden`
+ * (nullable) receives h.  Results equal llmcp_q8_swiglu followed by
+ * llmcp_q8_linear in the same execution mode. */
 int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                  const llmcp_memref_i8_1d *w_gate,
                  const llmcp_memref_i8_1d *w_up,

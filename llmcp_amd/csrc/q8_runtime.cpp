@@ -913,8 +913,41 @@ static int mlp_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if ((rc = check_mode(execution_mode))) return rc;
   const int64_t m = in.rows;
   if (m == 0) return LLMCP_Q8_OK;
-  if (m != 1) return fail(LLMCP_Q8_DECLINED, "fused MLP needs M == 1");
   if ((rc = set_device(ctx))) return rc;
+  if (m > 1) {
+    // Several rows: the SwiGLU GEMMs of llmcp_q8_swiglu (gate with SiLU,
+    // then up with the multiply in its epilogue) into h, then the GEMM of h,
+    // with llmcp_q8_linear's epilogue choice (scalar in decode mode).
+    const bool decode = execution_mode == LLMCP_Q8_DECODE;
+    const int64_t f = wg->rows;
+    Rows h;
+    if (hidden) {
+      h = *hidden;
+    } else {
+      const uint64_t bytes = (uint64_t)(m * f) * (out.bf16 ? 2 : 4);
+      if ((rc = grow(ctx, ctx->hf, ctx->hf_bytes, bytes, "mlp hidden"))) return rc;
+      h.data = ctx->hf;
+      h.rows = m;
+      h.cols = h.ld = f;
+      h.bf16 = out.bf16;
+    }
+    Rows g = h;  // the gate's output: h itself (f32) or f32 scratch (bf16)
+    if (h.bf16) {
+      if ((rc = grow(ctx, ctx->up, ctx->up_bytes, (uint64_t)(m * f) * 4,
+                     "prefill SwiGLU scratch")))
+        return rc;
+      g.data = ctx->up;
+      g.bf16 = false;
+      g.ld = f;
+    }
+    if ((rc = gemm_quantize(ctx, in, wg))) return rc;
+    if ((rc = gemm_launch(ctx, m, wg, g, LLMCP_Q8_ACT_SILU, nullptr, 0, decode)))
+      return rc;
+    if ((rc = gemm_launch(ctx, m, wu, h, LLMCP_Q8_ACT_NONE, (const float *)g.data,
+                          g.ld, decode)))
+      return rc;
+    return gemm_common(ctx, h, wd, out, LLMCP_Q8_ACT_NONE, decode);
+  }
   if ((rc = ensure_decode_scratch(ctx, wg->rows, wg->cols))) return rc;
   // Gate/up with the SwiGLU epilogue into h, then the down GEMV, which
   // quantizes h per workgroup (Q8Decode.cpp:83-120) as its input.  h has

@@ -4,7 +4,8 @@ oracle (swiglu then linear, ModelBuilder.cpp:205-216 with FuseSiluMul) bit
 for bit: on consecutive calls with new inputs (a stale h would differ), on
 24 calls queued back to back without a host synchronization, and on replays
 of a captured graph with new inputs copied in between and eager calls on the
-same buffers between the replays."""
+same buffers between the replays; and for several rows (the SwiGLU GEMMs and
+the down GEMM) in both execution modes and dtypes."""
 import numpy as np
 import pytest
 
@@ -103,3 +104,41 @@ def test_mlp_in_a_captured_graph(ctx, oracle, mlp_weights, q8):
     finally:
         ctx.graph_destroy(g)
     assert ctx.check_flag() == 0
+
+
+@pytest.mark.parametrize("mode,dtype", [("prefill", "f32"), ("decode", "f32"),
+                                        ("prefill", "bf16"), ("decode", "bf16")])
+def test_mlp_several_rows(ctx, oracle, mlp_weights, mode, dtype):
+    # M = 24: the SwiGLU GEMMs and the down GEMM, prefill with the FMA
+    # epilogue, decode with the scalar one; equal to llmcp_q8_swiglu then
+    # llmcp_q8_linear and to the oracle, with and without a caller h
+    p4, (tg, tu, td) = mlp_weights
+    m = 24
+    rng = np.random.default_rng(12 if dtype == "f32" else 13)
+    x = rng.standard_normal((m, HIDDEN)).astype(np.float32)
+    epi = "fma" if mode == "prefill" else "scalar"
+    esz, et = (4, np.float32) if dtype == "f32" else (2, np.uint16)
+    if dtype == "f32":
+        xh = x
+        h_ref = oracle.swiglu(x, p4[0], p4[1], FFN, epilogue=epi)
+        y_ref = oracle.linear(h_ref, p4[2], HIDDEN, epilogue=epi)
+    else:
+        xh = oracle.f32_to_bf16_bits(x)
+        xf = oracle.bf16_bits_to_f32(xh)
+        g = oracle.f32_to_bf16_bits(oracle.linear(xf, p4[0], FFN, activation="silu", epilogue=epi))
+        u = oracle.f32_to_bf16_bits(oracle.linear(xf, p4[1], FFN, epilogue=epi))
+        h_ref = oracle.f32_to_bf16_bits(
+            (oracle.bf16_bits_to_f32(g) * oracle.bf16_bits_to_f32(u)).astype(np.float32))
+        y_ref = oracle.f32_to_bf16_bits(
+            oracle.linear(oracle.bf16_bits_to_f32(h_ref), p4[2], HIDDEN, epilogue=epi))
+    xd, hd = ctx.to_device(xh), ctx.alloc(m * FFN * esz)
+    y1, y2, y3 = (ctx.alloc(m * HIDDEN * esz) for _ in range(3))
+    ctx.mlp(xd, tg, tu, td, y1, h=hd, m=m, mode=mode, dtype=dtype)
+    assert bits_equal(ctx.to_host(hd, (m, FFN), et), h_ref)
+    assert bits_equal(ctx.to_host(y1, (m, HIDDEN), et), y_ref)
+    ctx.mlp(xd, tg, tu, td, y2, m=m, mode=mode, dtype=dtype)
+    assert bits_equal(ctx.to_host(y2, (m, HIDDEN), et), y_ref)
+    h2 = ctx.alloc(m * FFN * esz)
+    ctx.swiglu(xd, tg, tu, h2, m, mode=mode, dtype=dtype)
+    ctx.linear(h2, td, y3, m, mode=mode, dtype=dtype)
+    assert bits_equal(ctx.to_host(y3, (m, HIDDEN), et), y_ref)
