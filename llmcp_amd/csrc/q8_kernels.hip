@@ -988,17 +988,18 @@ inline unsigned grid_for(int64_t threads, int block) {
 
 // Ring depth: passes in flight per wave.  Two matrices: 4 (72 VGPRs; at
 // K = 2560 the fifth pass is issued as the first one is consumed, which
-// measured about 1 % faster on the decode MLP than all 5 at once); one
-// matrix from LDS: 13 (117 VGPRs; at K = 9216 the down GEMV measured 7.46 us
-// against 8.05 with all 18 passes in flight, 7.74 with 12 and 7.65-7.82
-// with 14-16); one matrix with a pre-quantized row: 12 passes of weights +
-// input.
+// measured about 1 % faster on the decode MLP than all 5 at once).  One
+// matrix from LDS: 4 up to K = 2560 (the 2560 x 2560 GEMV: 3.71 us against
+// 3.86 with all 5), else 13 (117 VGPRs; at K = 9216 the down GEMV measured
+// 7.46 us against 8.05 with all 18 passes in flight, 7.74 with 12 and
+// 7.65-7.82 with 14-16).  One matrix with a pre-quantized row: 12 passes of
+// weights + input.
 template <int NMAT, int IN, int PC>
 constexpr int ring_depth() {
   // at least two passes of units, so the next pass is in flight while the
   // current one chains
   constexpr int two = 2 * seg_for(PC);
-  constexpr int base = NMAT == 2 ? 4 : (IN == IN_WG ? 13 : 12);
+  constexpr int base = NMAT == 2 ? 4 : (IN == IN_WG ? (PC <= 5 ? 4 : 13) : 12);
   constexpr int dmax = base > two ? base : two;
   return PC > 0 ? (PC < dmax ? PC : dmax) : (NMAT == 2 ? 4 : 8);
 }
