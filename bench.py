@@ -473,6 +473,9 @@ def main():
     ap.add_argument("--gemm-only", type=int, default=0, metavar="M",
                     help="time only config 4's prefill GEMM at M rows and print "
                          "its figures (a short run for counter collection)")
+    ap.add_argument("--platform", choices=("aarch64", "x86"), default="aarch64",
+                    help="reference arithmetic to reproduce: the SDOT paths' "
+                         "fma epilogue (default) or the x86 scalar path's")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the Q8_0 linear path runs on a single "
@@ -481,6 +484,7 @@ def main():
         sys.exit(2)
     import llmcp_amd as q8
     ctx = q8.Context(0)
+    ctx.set_platform(args.platform)
     if args.copy_calibration:
         copy_calibration(ctx)
     if args.gemm_only:

@@ -40,10 +40,11 @@ extern "C" {
 #endif
 
 /* Version of this C ABI (1: f32 entries; 2: bf16 twins and all four
- * activations; 3: linear + residual add).  The model ABI of the AOT library
- * (llmcp_model_abi_version() == 2, include/llmcp/Support/AotAbi.h:12) is not
- * changed by this library. */
-#define LLMCP_Q8_ABI_VERSION 3
+ * activations; 3: linear + residual add; 4: reference platform switch,
+ * weight budget, graph staleness check, grouped linears).  The model ABI of
+ * the AOT library (llmcp_model_abi_version() == 2,
+ * include/llmcp/Support/AotAbi.h:12) is not changed by this library. */
+#define LLMCP_Q8_ABI_VERSION 4
 
 enum llmcp_q8_status {
   LLMCP_Q8_OK = 0,
@@ -53,13 +54,19 @@ enum llmcp_q8_status {
   LLMCP_Q8_EHIP = 4,      /* HIP runtime error */
   LLMCP_Q8_EFORMAT = 5,   /* packed-weights header or manifest invalid */
   LLMCP_Q8_EIO = 6,       /* file open/map failure */
-  LLMCP_Q8_ENOMEM = 7     /* device allocation failed */
+  LLMCP_Q8_ENOMEM = 7,    /* device (or host) allocation failed, or the
+                             context's weight budget is exceeded */
+  LLMCP_Q8_EINTERNAL = 8, /* unexpected internal failure */
+  LLMCP_Q8_ESTALE = 9     /* graph captured before memory it uses was
+                             reallocated: capture it again */
 };
 
 /* The activations llmcp.linear accepts (LLMCPOps.cpp:74-77), applied to the
  * f32 accumulator before the store (applyMatmulActivation,
  * MatmulLoweringCommon.cpp:78-103): silu v/(1+exp(-v)) as v*(1/(1+exp(-v))),
- * sigmoid 1/(1+exp(-v)), softplus log1p(exp(v)). */
+ * sigmoid 1/(1+exp(-v)), softplus math.log1p(exp(v)), which the reference's
+ * --convert-math-to-llvm lowers to log(1 + exp(v)) with an f32 add
+ * (llmcp-compile.cpp:186). */
 enum llmcp_q8_activation {
   LLMCP_Q8_ACT_NONE = 0,
   LLMCP_Q8_ACT_SILU = 1,
@@ -67,12 +74,19 @@ enum llmcp_q8_activation {
   LLMCP_Q8_ACT_SOFTPLUS = 3
 };
 
-/* Per-block epilogue of the prefill GEMM.  Both are the reference's math:
- * FMA    acc = fma(f32(I), sa*dw, acc)  -- the SDOT GEMM, Q8Matmul.cpp:204-223
- * SCALAR acc = acc + f32(I)*(sa*dw)     -- the x86 scalar path, Q8Scalar.cpp:192-199
- * The decode path (GEMV, or the GEMM for several rows in DECODE mode)
- * always computes the SCALAR form. */
-enum llmcp_q8_epilogue { LLMCP_Q8_EPI_SCALAR = 0, LLMCP_Q8_EPI_FMA = 1 };
+/* The reference platform whose arithmetic every op reproduces bit for bit.
+ * The reference lowers q8_0_p4 per target (MatmulLoweringCommon.cpp:492-508):
+ * AARCH64 (default)  the SDOT emitters, decode and prefill alike:
+ *                    acc = fma(f32(I), sa*dw, acc) per block
+ *                    (Q8Decode.cpp:192-203, Q8Matmul.cpp:204-223);
+ * X86                the scalar fallback for every mode and M:
+ *                    acc = acc + f32(I)*(sa*dw)  (Q8Scalar.cpp:192-199).
+ * Blocks are summed in order b = 0..K/32-1 on both; each platform is within
+ * the other's 1e-5 relative / 1e-4 absolute tolerance. */
+enum llmcp_q8_platform {
+  LLMCP_Q8_PLATFORM_X86 = 0,
+  LLMCP_Q8_PLATFORM_AARCH64 = 1
+};
 
 /* llmcp.execution_mode (LowerToLinalg.cpp:40-52). */
 enum llmcp_q8_mode { LLMCP_Q8_PREFILL = 0, LLMCP_Q8_DECODE = 1 };
@@ -128,8 +142,14 @@ int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx);
 int llmcp_q8_ctx_set_stream(llmcp_q8_ctx *ctx, void *hip_stream);
 void *llmcp_q8_ctx_stream(llmcp_q8_ctx *ctx);
 int llmcp_q8_ctx_synchronize(llmcp_q8_ctx *ctx);
-/* Selects the prefill GEMM epilogue (default LLMCP_Q8_EPI_FMA). */
-int llmcp_q8_set_gemm_epilogue(llmcp_q8_ctx *ctx, int32_t variant);
+/* Selects the reference platform (llmcp_q8_platform) for every later call
+ * on the context; llmcp_q8_get_platform returns it (-1 for a null ctx). */
+int llmcp_q8_set_platform(llmcp_q8_ctx *ctx, int32_t platform);
+int32_t llmcp_q8_get_platform(llmcp_q8_ctx *ctx);
+/* Caps the device bytes of the context's registered weights (0: no cap, the
+ * default); a registration past the cap fails with LLMCP_Q8_ENOMEM.  Lets a
+ * serving process keep HBM for other state. */
+int llmcp_q8_set_weight_budget(llmcp_q8_ctx *ctx, uint64_t bytes);
 /* Context used by the _mlir_ciface_* entries (set by the AOT runtime). */
 int llmcp_q8_set_default_ctx(llmcp_q8_ctx *ctx);
 
@@ -156,7 +176,10 @@ int llmcp_q8_release(llmcp_q8_ctx *ctx, const void *key);
 /* Validates a mapped LLMCPWGT file (include/llmcp/Support/PackedWeights.h,
  * lib/Runtime/WeightArena.cpp:27-131 rules) and uploads every Q8_0 tensor.
  * `file` is the whole mapping, header first.  Returns the number of Q8_0
- * tensors uploaded through `num_q8` (nullable). */
+ * tensors uploaded through `num_q8` (nullable).  All or nothing: the
+ * tensors are staged on the device and registered together only when every
+ * one succeeded (Arena::load replaces the arena only on success,
+ * WeightArena.cpp:28-29, :124-130); on failure nothing changes. */
 int llmcp_q8_upload_arena(llmcp_q8_ctx *ctx, const void *file,
                           uint64_t file_bytes, int64_t *num_q8);
 
@@ -169,10 +192,9 @@ int llmcp_q8_arena_inspect(const void *file, uint64_t file_bytes,
 
 /* llmcp.linear with weight_format q8_0_p4 (LowerToLinalg.cpp:143-209):
  * y[M,N] = act(x[M,K] . W[N,K]^T), x quantized per call to Q8_1 blocks.
- * M == 1 runs the GEMV (scalar epilogue) in either mode.  M > 1 runs the
- * int8-MFMA GEMM: PREFILL with the epilogue llmcp_q8_set_gemm_epilogue
- * selects, DECODE (which the reference's decode emitter accepts for any M,
- * Q8Decode.cpp:236-256) always with the scalar one.  activation:
+ * M == 1 runs the GEMV, M > 1 the int8-MFMA GEMM, in either mode (the
+ * reference's decode emitter accepts any M, Q8Decode.cpp:236-256); both
+ * compute the selected platform's epilogue.  activation:
  * llmcp_q8_activation. */
 int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                     const llmcp_memref_i8_1d *weight,
@@ -407,7 +429,11 @@ int llmcp_q8_event_create(void **event);
 int llmcp_q8_event_destroy(void *event);
 int llmcp_q8_event_record(llmcp_q8_ctx *ctx, void *event);
 int llmcp_q8_event_elapsed_ms(void *start, void *stop, float *ms);
-/* Stream capture into a HIP graph and replay (launch-bound loops). */
+/* Stream capture into a HIP graph and replay (launch-bound loops).  A graph
+ * holds the device addresses of the context's workspace and weights at
+ * capture: graph_launch refuses it with LLMCP_Q8_ESTALE once any of them
+ * was freed or reallocated (a call that grew the workspace, a weight
+ * released or registered again). */
 int llmcp_q8_graph_begin(llmcp_q8_ctx *ctx);
 int llmcp_q8_graph_end(llmcp_q8_ctx *ctx, void **graph_exec);
 int llmcp_q8_graph_launch(llmcp_q8_ctx *ctx, void *graph_exec);

@@ -16,10 +16,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libllmcp_q8.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "llmcp_q8.h")
 
-OK, DECLINED, EINVAL, ENOTFOUND, EHIP, EFORMAT, EIO, ENOMEM = range(8)
+OK, DECLINED, EINVAL, ENOTFOUND, EHIP, EFORMAT, EIO, ENOMEM, EINTERNAL, ESTALE = range(10)
 ACT = {"none": 0, "silu": 1, "sigmoid": 2, "softplus": 3}
 DTYPES = ("f32", "bf16")
 MODE = {"prefill": 0, "decode": 1}
+# Reference platforms (llmcp_q8_platform) and the per-block epilogue each
+# computes: fma on aarch64 (SDOT emitters), mul+add on x86 (scalar path).
+PLATFORM = {"x86": 0, "aarch64": 1}
+EPILOGUE = {"x86": "scalar", "aarch64": "fma"}
 
 _lib = None
 
@@ -56,7 +60,7 @@ EXPORTS = [
     "llmcp_q8_abi_version", "llmcp_q8_last_error", "llmcp_q8_ctx_create",
     "llmcp_q8_ctx_destroy", "llmcp_q8_ctx_set_stream", "llmcp_q8_ctx_stream",
     "llmcp_q8_ctx_synchronize", "llmcp_q8_set_default_ctx",
-    "llmcp_q8_set_gemm_epilogue",
+    "llmcp_q8_set_platform", "llmcp_q8_get_platform", "llmcp_q8_set_weight_budget",
     "llmcp_q8_upload_p4", "llmcp_q8_register_device_p4", "llmcp_q8_release",
     "llmcp_q8_upload_arena", "llmcp_q8_arena_inspect", "llmcp_q8_linear", "llmcp_q8_swiglu",
     "llmcp_q8_lm_head", "llmcp_q8_mlp", "llmcp_q8_embedding", "llmcp_q8_quantize_activations",
@@ -100,7 +104,9 @@ def lib():
         "llmcp_q8_ctx_stream": (P, [P]),
         "llmcp_q8_ctx_synchronize": (I, [P]),
         "llmcp_q8_set_default_ctx": (I, [P]),
-        "llmcp_q8_set_gemm_epilogue": (I, [P, I32]),
+        "llmcp_q8_set_platform": (I, [P, I32]),
+        "llmcp_q8_get_platform": (I32, [P]),
+        "llmcp_q8_set_weight_budget": (I, [P, U64]),
         "llmcp_q8_upload_p4": (I, [P, P, I64, I64, F]),
         "llmcp_q8_register_device_p4": (I, [P, P, I64, I64, F]),
         "llmcp_q8_release": (I, [P, P]),
@@ -260,9 +266,33 @@ class Context:
     def __exit__(self, *exc):
         self.close()
 
-    def set_gemm_epilogue(self, variant):
-        """'fma' (SDOT GEMM, Q8Matmul.cpp) or 'scalar' (x86 path, Q8Scalar.cpp)."""
-        check(lib().llmcp_q8_set_gemm_epilogue(self.handle, {"scalar": 0, "fma": 1}[variant]))
+    def set_platform(self, platform):
+        """'aarch64' (SDOT emitters: fma epilogue, the default) or 'x86'
+        (scalar path: mul+add) for every later call."""
+        check(lib().llmcp_q8_set_platform(self.handle, PLATFORM[platform]))
+
+    def set_platform_code(self, code):
+        """llmcp_q8_set_platform with a raw code (tests of the error path)."""
+        check(lib().llmcp_q8_set_platform(self.handle, int(code)))
+
+    @property
+    def platform(self):
+        code = lib().llmcp_q8_get_platform(self.handle)
+        return {v: k for k, v in PLATFORM.items()}[code]
+
+    @property
+    def epilogue(self):
+        """The oracle epilogue this context reproduces bit for bit."""
+        return EPILOGUE[self.platform]
+
+    @property
+    def other_epilogue(self):
+        """The other platform's epilogue (agrees within tolerance)."""
+        return "scalar" if self.epilogue == "fma" else "fma"
+
+    def set_weight_budget(self, nbytes):
+        """Caps the device bytes of registered weights (0: no cap)."""
+        check(lib().llmcp_q8_set_weight_budget(self.handle, int(nbytes)))
 
     def sync(self):
         check(lib().llmcp_q8_ctx_synchronize(self.handle))

@@ -74,9 +74,9 @@ __device__ __forceinline__ double exp_f64_reduced(double x) {
 }
 
 // The activations of applyMatmulActivation (MatmulLoweringCommon.cpp:78-103),
-// each MLIR op rounded to f32 in turn.  math.exp / math.log1p are evaluated
-// in f64 and rounded once to f32 (the CPU oracle does the same with the host
-// libm).  exp saturates outside [-110, 100], where the f32 result is 0 or
+// each MLIR op rounded to f32 in turn.  math.exp and the log of softplus
+// are evaluated in f64 and rounded once to f32 (the CPU oracle does the same
+// with the host libm).  exp saturates outside [-110, 100], where the f32 result is 0 or
 // inf either way.  The device self-test (llmcp_q8_selftest_exp) lists every
 // float input whose exp lies near a rounding midpoint, the only inputs on
 // which two exp(double) evaluations accurate to 2^-46 can round differently.
@@ -95,9 +95,13 @@ __device__ __forceinline__ float sigmoid_f32(float v) {
 __device__ __forceinline__ float silu_f32(float v) {
   return v * sigmoid_f32(v);
 }
+// softplus = math.log1p(math.exp(v)); the reference's --convert-math-to-llvm
+// lowers log1p(y) to log(1 + y) with an f32 add (llmcp-compile.cpp:186), so
+// the sum is rounded to f32 before the logarithm.  log is evaluated in f64
+// and rounded once, like exp.
 __device__ __forceinline__ float softplus_f32(float v) {
-  const float e = exp_f32(v);
-  return (float)log1p((double)e);
+  const float s = 1.0f + exp_f32(v);
+  return (float)log((double)s);
 }
 // activate() over an array in straight-line code (no per-element branch, so
 // exp's constants stay in SGPRs across the elements), with one wave-uniform

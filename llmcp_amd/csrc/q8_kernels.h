@@ -46,6 +46,8 @@ struct GemvLaunch {
   int64_t cols = 0;              // K
   int nmat = 1;                  // 2 = fused SwiGLU (gate, up)
   int activation = 0;            // llmcp_q8_activation (nmat == 1 only)
+  bool fma = false;              // epilogue: fma (SDOT paths) or mul+add
+                                 // (x86 scalar path)
   const void *residual = nullptr;      // non-null (one matrix, no activation,
                                        // no argmax): y = r + acc, r [rows] of
                                        // y's element type (may alias y)

@@ -31,16 +31,31 @@ using namespace llmcp_q8;
 
 namespace {
 
-thread_local std::string g_last_error;
+// A fixed buffer: recording an error never allocates (so it cannot throw).
+thread_local char g_last_error[512];
 
 int fail(int code, const char *fmt, ...) {
-  char buf[512];
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
   va_end(ap);
-  g_last_error = buf;
   return code;
+}
+
+// Every entry of the C ABI runs its body through guarded(): a C++ exception
+// (std::bad_alloc from the registry, the arena parser or the writer) becomes
+// a status code instead of crossing into a C or MLIR caller.
+template <class F>
+int guarded(F &&body) noexcept {
+  try {
+    return body();
+  } catch (const std::bad_alloc &) {
+    return fail(LLMCP_Q8_ENOMEM, "host allocation failed");
+  } catch (const std::exception &e) {
+    return fail(LLMCP_Q8_EINTERNAL, "internal error: %s", e.what());
+  } catch (...) {
+    return fail(LLMCP_Q8_EINTERNAL, "internal error: unknown exception");
+  }
 }
 
 int hip_fail(hipError_t e, const char *what) {
@@ -85,13 +100,33 @@ struct llmcp_q8_ctx {
   float *up = nullptr;  // prefill SwiGLU: the up projection
   uint64_t up_bytes = 0;
   uint64_t hf_bytes = 0;
-  hipGraph_t capture = nullptr;
-  bool gemm_fma = true;  // prefill GEMM epilogue variant
+  // Reference platform whose arithmetic every path reproduces
+  // (llmcp_q8_platform): aarch64 = fma epilogue everywhere, x86 = mul+add.
+  int32_t platform = LLMCP_Q8_PLATFORM_AARCH64;
+  // Cap on device bytes of registered weights (0: none).
+  uint64_t weight_budget = 0;
+  uint64_t weight_bytes = 0;
+  // Bumped whenever device memory a captured graph may reference is freed
+  // (workspace regrowth, a weight released or replaced); graphs captured
+  // under an older generation are refused at launch.
+  uint64_t generation = 0;
+  // Orders work across llmcp_q8_ctx_set_stream.
+  hipEvent_t switch_event = nullptr;
+  bool fma() const { return platform == LLMCP_Q8_PLATFORM_AARCH64; }
 };
 
 namespace {
 
 llmcp_q8_ctx *g_default_ctx = nullptr;
+
+// Graphs captured through llmcp_q8_graph_end: their context and the
+// context's memory generation at capture.
+struct GraphInfo {
+  llmcp_q8_ctx *ctx;
+  uint64_t generation;
+};
+std::mutex g_graph_mutex;
+std::map<void *, GraphInfo> g_graphs;
 
 int set_device(llmcp_q8_ctx *ctx) {
   HIP_TRY(hipSetDevice(ctx->device));
@@ -134,6 +169,19 @@ struct Rows {
   bool bf16 = false;
 };
 
+// Device scratch a call uses: the quantized input rows with their scales
+// and the argmax slots.  Normally the context's own (grown on demand);
+// the no-allocation entry brings a fixed one.
+struct Workspace {
+  int8_t *qa = nullptr;
+  float *sa = nullptr;
+  uint64_t qa_bytes = 0;
+  uint64_t sa_bytes = 0;
+  unsigned long long *keys = nullptr;
+  bool *keys_dirty = nullptr;  // the slots may hold keys of a failed call
+  bool fixed = false;          // capacities are limits: never grow
+};
+
 template <class M>
 bool view_of(const M *d, bool bf16, Rows &r) {
   if (!dense_rows(d)) return false;
@@ -152,6 +200,7 @@ int grow(llmcp_q8_ctx *ctx, T *&ptr, uint64_t &have, uint64_t need,
   if (ptr) {
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     HIP_TRY(hipFree(ptr));
+    ++ctx->generation;  // graphs captured earlier may reference ptr
   }
   ptr = nullptr;
   have = 0;
@@ -165,6 +214,37 @@ int grow(llmcp_q8_ctx *ctx, T *&ptr, uint64_t &have, uint64_t need,
 int ensure_scratch(llmcp_q8_ctx *ctx, uint64_t qa_bytes, uint64_t sa_bytes) {
   int rc = grow(ctx, ctx->qa, ctx->qa_bytes, qa_bytes, "activation scratch");
   if (!rc) rc = grow(ctx, ctx->sa, ctx->sa_bytes, sa_bytes, "scale scratch");
+  return rc;
+}
+
+// The context's workspace as a Workspace (after any growth).
+Workspace ctx_workspace(llmcp_q8_ctx *ctx) {
+  Workspace ws;
+  ws.qa = ctx->qa;
+  ws.sa = ctx->sa;
+  ws.qa_bytes = ctx->qa_bytes;
+  ws.sa_bytes = ctx->sa_bytes;
+  ws.keys = ctx->keys;
+  ws.keys_dirty = &ctx->keys_dirty;
+  return ws;
+}
+
+// Room for qa_bytes / sa_bytes of quantized input: grows the context's
+// workspace, or checks a fixed one.
+int reserve(llmcp_q8_ctx *ctx, Workspace &ws, uint64_t qa_bytes,
+            uint64_t sa_bytes) {
+  if (ws.fixed) {
+    if (qa_bytes > ws.qa_bytes || sa_bytes > ws.sa_bytes)
+      return fail(LLMCP_Q8_DECLINED,
+                  "input needs %llu + %llu bytes of scratch; the fixed "
+                  "scratch holds %llu + %llu",
+                  (unsigned long long)qa_bytes, (unsigned long long)sa_bytes,
+                  (unsigned long long)ws.qa_bytes,
+                  (unsigned long long)ws.sa_bytes);
+    return LLMCP_Q8_OK;
+  }
+  int rc = ensure_scratch(ctx, qa_bytes, sa_bytes);
+  if (!rc) ws = ctx_workspace(ctx);
   return rc;
 }
 
@@ -192,50 +272,130 @@ int ensure_decode_scratch(llmcp_q8_ctx *ctx, int64_t rows, int64_t cols) {
   return grow(ctx, ctx->hf, ctx->hf_bytes, (uint64_t)rows * 4, "mlp hidden");
 }
 
-// Repacks device p4 bytes into a new registry entry under `key`.
-int register_from_device_p4(llmcp_q8_ctx *ctx, const void *key,
-                            const uint8_t *dev_p4, int64_t rows, int64_t cols,
-                            float *repack_ms) {
-  Tensor t;
+// Repacks device p4 bytes into a new device tensor for `key` (not yet
+// registered).  The weight budget counts `pending` bytes staged alongside.
+int stage_from_device_p4(llmcp_q8_ctx *ctx, const void *key,
+                         const uint8_t *dev_p4, int64_t rows, int64_t cols,
+                         float *repack_ms, uint64_t pending, Tensor &t) {
+  t = Tensor();
   t.key = (uintptr_t)key;
   t.rows = rows;
   t.cols = cols;
   t.key_bytes = (uint64_t)rows * (uint64_t)(cols / kBlock) * 34u;
   t.dev_bytes = (uint64_t)device_bytes_for(rows, cols);
-  if (hipMalloc(&t.dev, t.dev_bytes) != hipSuccess)
+  if (ctx->weight_budget &&
+      ctx->weight_bytes + pending + t.dev_bytes > ctx->weight_budget)
+    return fail(LLMCP_Q8_ENOMEM,
+                "device weight of %llu bytes exceeds the context's weight "
+                "budget (%llu of %llu bytes in use)",
+                (unsigned long long)t.dev_bytes,
+                (unsigned long long)(ctx->weight_bytes + pending),
+                (unsigned long long)ctx->weight_budget);
+  if (hipMalloc(&t.dev, t.dev_bytes) != hipSuccess) {
+    t.dev = nullptr;
     return fail(LLMCP_Q8_ENOMEM, "device weight of %llu bytes",
                 (unsigned long long)t.dev_bytes);
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (repack_ms) {
-    HIP_TRY(hipEventCreate(&e0));
-    HIP_TRY(hipEventCreate(&e1));
-    HIP_TRY(hipEventRecord(e0, ctx->stream));
   }
-  hipError_t err = launch_repack(dev_p4, t.dev, rows, cols, ctx->stream);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t err = hipSuccess;
+  if (repack_ms) {
+    err = hipEventCreate(&e0);
+    if (err == hipSuccess) err = hipEventCreate(&e1);
+    if (err == hipSuccess) err = hipEventRecord(e0, ctx->stream);
+  }
+  if (err == hipSuccess)
+    err = launch_repack(dev_p4, t.dev, rows, cols, ctx->stream);
+  if (err == hipSuccess && repack_ms) {
+    err = hipEventRecord(e1, ctx->stream);
+    if (err == hipSuccess) err = hipEventSynchronize(e1);
+    if (err == hipSuccess) err = hipEventElapsedTime(repack_ms, e0, e1);
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
   if (err != hipSuccess) {
     (void)hipFree(t.dev);
+    t.dev = nullptr;
     return hip_fail(err, "repack");
   }
-  if (repack_ms) {
-    HIP_TRY(hipEventRecord(e1, ctx->stream));
-    HIP_TRY(hipEventSynchronize(e1));
-    HIP_TRY(hipEventElapsedTime(repack_ms, e0, e1));
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-  }
-  int rc = ensure_decode_scratch(ctx, rows, cols);
-  if (rc) {
-    (void)hipFree(t.dev);
-    return rc;
-  }
-  auto old = ctx->registry.find(t.key);
-  if (old != ctx->registry.end()) {
-    HIP_TRY(hipStreamSynchronize(ctx->stream));
-    (void)hipFree(old->second.dev);
-    ctx->registry.erase(old);
-  }
-  ctx->registry[t.key] = t;
   return LLMCP_Q8_OK;
+}
+
+// Makes staged tensors visible all at once: the new registry is built on
+// the side (the only step that can throw) and swapped in; entries they
+// replace are freed afterwards.  On failure the staged tensors are freed
+// and the registry is unchanged.
+int commit_tensors(llmcp_q8_ctx *ctx, std::vector<Tensor> &staged) {
+  auto drop_staged = [&] {
+    for (Tensor &t : staged) (void)hipFree(t.dev);
+    staged.clear();
+  };
+  // workspace for each tensor's input row (and h for the MLP's down GEMV)
+  for (const Tensor &t : staged) {
+    int rc = ensure_decode_scratch(ctx, t.rows, t.cols);
+    if (rc) {
+      drop_staged();
+      return rc;
+    }
+  }
+  std::map<uintptr_t, Tensor> next;
+  std::vector<uint8_t *> replaced;
+  try {
+    next = ctx->registry;
+    for (const Tensor &t : staged) {
+      auto it = next.find(t.key);
+      if (it != next.end()) replaced.push_back(it->second.dev);
+      next[t.key] = t;
+    }
+  } catch (...) {
+    drop_staged();
+    throw;
+  }
+  if (!replaced.empty()) {
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+      drop_staged();
+      return hip_fail(e, "hipStreamSynchronize");
+    }
+  }
+  ctx->registry.swap(next);
+  staged.clear();
+  uint64_t bytes = 0;
+  for (const auto &kv : ctx->registry) bytes += kv.second.dev_bytes;
+  ctx->weight_bytes = bytes;
+  for (uint8_t *p : replaced) (void)hipFree(p);
+  if (!replaced.empty()) ++ctx->generation;
+  return LLMCP_Q8_OK;
+}
+
+// One tensor: stage and commit.
+int register_from_device_p4(llmcp_q8_ctx *ctx, const void *key,
+                            const uint8_t *dev_p4, int64_t rows, int64_t cols,
+                            float *repack_ms) {
+  std::vector<Tensor> staged(1);
+  int rc = stage_from_device_p4(ctx, key, dev_p4, rows, cols, repack_ms, 0,
+                                staged[0]);
+  if (rc) return rc;
+  return commit_tensors(ctx, staged);
+}
+
+// Host p4 bytes -> device staging copy -> staged tensor.
+int stage_from_host_p4(llmcp_q8_ctx *ctx, const void *host_p4, int64_t rows,
+                       int64_t cols, float *repack_ms, uint64_t pending,
+                       Tensor &t) {
+  const uint64_t bytes = (uint64_t)rows * (uint64_t)(cols / kBlock) * 34u;
+  uint8_t *staging = nullptr;
+  if (hipMalloc(&staging, bytes) != hipSuccess)
+    return fail(LLMCP_Q8_ENOMEM, "staging of %llu bytes",
+                (unsigned long long)bytes);
+  hipError_t e = hipMemcpyAsync(staging, host_p4, bytes, hipMemcpyHostToDevice,
+                                ctx->stream);
+  int rc = e == hipSuccess ? stage_from_device_p4(ctx, host_p4, staging, rows,
+                                                  cols, repack_ms, pending, t)
+                           : hip_fail(e, "upload");
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipFree(staging);
+  return rc;
 }
 
 bool packable(int64_t rows, int64_t cols) {
@@ -294,65 +454,90 @@ extern "C" {
 
 int32_t llmcp_q8_abi_version(void) { return LLMCP_Q8_ABI_VERSION; }
 
-const char *llmcp_q8_last_error(void) { return g_last_error.c_str(); }
+const char *llmcp_q8_last_error(void) { return g_last_error; }
 
 int llmcp_q8_ctx_create(int device, llmcp_q8_ctx **out) {
-  if (!out) return fail(LLMCP_Q8_EINVAL, "null output pointer");
-  *out = nullptr;
-  int count = 0;
-  HIP_TRY(hipGetDeviceCount(&count));
-  if (device < 0 || device >= count)
-    return fail(LLMCP_Q8_EINVAL, "device %d out of range (%d devices)", device,
-                count);
-  auto *ctx = new llmcp_q8_ctx();
-  ctx->device = device;
-  int rc = set_device(ctx);
-  if (rc) {
-    delete ctx;
-    return rc;
-  }
-  hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
-  if (e != hipSuccess) {
-    delete ctx;
-    return hip_fail(e, "hipStreamCreateWithFlags");
-  }
-  ctx->stream = ctx->own_stream;
-  if (hipMalloc(&ctx->err_flag, sizeof(int32_t)) != hipSuccess) {
-    llmcp_q8_ctx_destroy(ctx);
-    return fail(LLMCP_Q8_ENOMEM, "context workspace");
-  }
-  if (hipMemset(ctx->err_flag, 0, sizeof(int32_t)) != hipSuccess ||
-      hipDeviceSynchronize() != hipSuccess) {
-    llmcp_q8_ctx_destroy(ctx);
-    return fail(LLMCP_Q8_EHIP, "context workspace init");
-  }
-  *out = ctx;
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!out) return fail(LLMCP_Q8_EINVAL, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    HIP_TRY(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count)
+      return fail(LLMCP_Q8_EINVAL, "device %d out of range (%d devices)", device,
+                  count);
+    auto *ctx = new llmcp_q8_ctx();
+    ctx->device = device;
+    int rc = set_device(ctx);
+    if (rc) {
+      delete ctx;
+      return rc;
+    }
+    hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete ctx;
+      return hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    ctx->stream = ctx->own_stream;
+    e = hipEventCreateWithFlags(&ctx->switch_event, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      ctx->switch_event = nullptr;
+      llmcp_q8_ctx_destroy(ctx);
+      return hip_fail(e, "hipEventCreateWithFlags");
+    }
+    if (hipMalloc(&ctx->err_flag, sizeof(int32_t)) != hipSuccess) {
+      llmcp_q8_ctx_destroy(ctx);
+      return fail(LLMCP_Q8_ENOMEM, "context workspace");
+    }
+    if (hipMemset(ctx->err_flag, 0, sizeof(int32_t)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+      llmcp_q8_ctx_destroy(ctx);
+      return fail(LLMCP_Q8_EHIP, "context workspace init");
+    }
+    *out = ctx;
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx) {
-  if (!ctx) return LLMCP_Q8_OK;
-  (void)hipSetDevice(ctx->device);
-  if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
-  if (ctx->stream && ctx->stream != ctx->own_stream)
-    (void)hipStreamSynchronize(ctx->stream);
-  for (auto &kv : ctx->registry) (void)hipFree(kv.second.dev);
-  if (ctx->err_flag) (void)hipFree(ctx->err_flag);
-  if (ctx->qa) (void)hipFree(ctx->qa);
-  if (ctx->sa) (void)hipFree(ctx->sa);
-  if (ctx->keys) (void)hipFree(ctx->keys);
-  if (ctx->hf) (void)hipFree(ctx->hf);
-  if (ctx->up) (void)hipFree(ctx->up);
-  if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
-  if (g_default_ctx == ctx) g_default_ctx = nullptr;
-  delete ctx;
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return LLMCP_Q8_OK;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
+    if (ctx->stream && ctx->stream != ctx->own_stream)
+      (void)hipStreamSynchronize(ctx->stream);
+    for (auto &kv : ctx->registry) (void)hipFree(kv.second.dev);
+    if (ctx->err_flag) (void)hipFree(ctx->err_flag);
+    if (ctx->qa) (void)hipFree(ctx->qa);
+    if (ctx->sa) (void)hipFree(ctx->sa);
+    if (ctx->keys) (void)hipFree(ctx->keys);
+    if (ctx->hf) (void)hipFree(ctx->hf);
+    if (ctx->up) (void)hipFree(ctx->up);
+    {
+      std::lock_guard<std::mutex> lock(g_graph_mutex);
+      for (auto it = g_graphs.begin(); it != g_graphs.end();)
+        it = it->second.ctx == ctx ? g_graphs.erase(it) : std::next(it);
+    }
+    if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    if (g_default_ctx == ctx) g_default_ctx = nullptr;
+    delete ctx;
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_ctx_set_stream(llmcp_q8_ctx *ctx, void *hip_stream) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own_stream;
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    hipStream_t next = hip_stream ? (hipStream_t)hip_stream : ctx->own_stream;
+    if (next == ctx->stream) return LLMCP_Q8_OK;
+    // Work still queued on the old stream uses the shared workspace: the new
+    // stream waits for it before anything is launched there.
+    HIP_TRY(hipSetDevice(ctx->device));
+    HIP_TRY(hipEventRecord(ctx->switch_event, ctx->stream));
+    HIP_TRY(hipStreamWaitEvent(next, ctx->switch_event, 0));
+    ctx->stream = next;
+    return LLMCP_Q8_OK;
+  });
 }
 
 void *llmcp_q8_ctx_stream(llmcp_q8_ctx *ctx) {
@@ -360,146 +545,164 @@ void *llmcp_q8_ctx_stream(llmcp_q8_ctx *ctx) {
 }
 
 int llmcp_q8_ctx_synchronize(llmcp_q8_ctx *ctx) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_set_default_ctx(llmcp_q8_ctx *ctx) {
-  g_default_ctx = ctx;
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    g_default_ctx = ctx;
+    return LLMCP_Q8_OK;
+  });
 }
 
-int llmcp_q8_set_gemm_epilogue(llmcp_q8_ctx *ctx, int32_t variant) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  if (variant != LLMCP_Q8_EPI_FMA && variant != LLMCP_Q8_EPI_SCALAR)
-    return fail(LLMCP_Q8_EINVAL, "unknown epilogue variant %d", variant);
-  ctx->gemm_fma = variant == LLMCP_Q8_EPI_FMA;
-  return LLMCP_Q8_OK;
+int llmcp_q8_set_platform(llmcp_q8_ctx *ctx, int32_t platform) {
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    if (platform != LLMCP_Q8_PLATFORM_AARCH64 && platform != LLMCP_Q8_PLATFORM_X86)
+      return fail(LLMCP_Q8_EINVAL, "unknown platform %d", platform);
+    ctx->platform = platform;
+    return LLMCP_Q8_OK;
+  });
+}
+
+int32_t llmcp_q8_get_platform(llmcp_q8_ctx *ctx) {
+  return ctx ? ctx->platform : -1;
+}
+
+int llmcp_q8_set_weight_budget(llmcp_q8_ctx *ctx, uint64_t bytes) {
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    ctx->weight_budget = bytes;
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_ctx_check(llmcp_q8_ctx *ctx, int32_t *flag) {
-  if (!ctx || !flag) return fail(LLMCP_Q8_EINVAL, "null argument");
-  HIP_TRY(hipSetDevice(ctx->device));
-  HIP_TRY(hipMemcpyAsync(flag, ctx->err_flag, sizeof(int32_t),
-                         hipMemcpyDeviceToHost, ctx->stream));
-  HIP_TRY(hipMemsetAsync(ctx->err_flag, 0, sizeof(int32_t), ctx->stream));
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !flag) return fail(LLMCP_Q8_EINVAL, "null argument");
+    HIP_TRY(hipSetDevice(ctx->device));
+    HIP_TRY(hipMemcpyAsync(flag, ctx->err_flag, sizeof(int32_t),
+                           hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipMemsetAsync(ctx->err_flag, 0, sizeof(int32_t), ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_selftest_quantizer(llmcp_q8_ctx *ctx, uint64_t *mismatches) {
-  if (!ctx || !mismatches) return fail(LLMCP_Q8_EINVAL, "null argument");
-  int rc = set_device(ctx);
-  if (rc) return rc;
-  unsigned long long *bad = nullptr;
-  if (hipMalloc(&bad, sizeof(*bad)) != hipSuccess)
-    return fail(LLMCP_Q8_ENOMEM, "self-test counter");
-  unsigned long long host = 0;
-  hipError_t e = hipMemsetAsync(bad, 0, sizeof(*bad), ctx->stream);
-  if (e == hipSuccess) e = launch_selftest_quantizer(bad, ctx->stream);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(&host, bad, sizeof(host), hipMemcpyDeviceToHost,
-                       ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  (void)hipFree(bad);
-  if (e != hipSuccess) return hip_fail(e, "quantizer self-test");
-  *mismatches = host;
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !mismatches) return fail(LLMCP_Q8_EINVAL, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    unsigned long long *bad = nullptr;
+    if (hipMalloc(&bad, sizeof(*bad)) != hipSuccess)
+      return fail(LLMCP_Q8_ENOMEM, "self-test counter");
+    unsigned long long host = 0;
+    hipError_t e = hipMemsetAsync(bad, 0, sizeof(*bad), ctx->stream);
+    if (e == hipSuccess) e = launch_selftest_quantizer(bad, ctx->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(&host, bad, sizeof(host), hipMemcpyDeviceToHost,
+                         ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(bad);
+    if (e != hipSuccess) return hip_fail(e, "quantizer self-test");
+    *mismatches = host;
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_selftest_exp(llmcp_q8_ctx *ctx, uint64_t counts[4], float *inputs,
                           uint32_t *results, int64_t cap, int64_t *stored) {
-  if (!ctx || !counts || !stored || cap < 0 || (cap > 0 && (!inputs || !results)))
-    return fail(LLMCP_Q8_EINVAL, "null argument or negative capacity");
-  if (cap > (int64_t)1 << 24) return fail(LLMCP_Q8_EINVAL, "capacity above 2^24");
-  int rc = set_device(ctx);
-  if (rc) return rc;
-  unsigned long long *out = nullptr;
-  float *din = nullptr;
-  uint32_t *dres = nullptr;
-  const size_t n = cap > 0 ? (size_t)cap : 1;
-  if (hipMalloc(&out, 5 * sizeof(*out)) != hipSuccess ||
-      hipMalloc(&din, n * sizeof(float)) != hipSuccess ||
-      hipMalloc(&dres, n * sizeof(uint32_t)) != hipSuccess) {
+  return guarded([&]() -> int {
+    if (!ctx || !counts || !stored || cap < 0 || (cap > 0 && (!inputs || !results)))
+      return fail(LLMCP_Q8_EINVAL, "null argument or negative capacity");
+    if (cap > (int64_t)1 << 24) return fail(LLMCP_Q8_EINVAL, "capacity above 2^24");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    unsigned long long *out = nullptr;
+    float *din = nullptr;
+    uint32_t *dres = nullptr;
+    const size_t n = cap > 0 ? (size_t)cap : 1;
+    if (hipMalloc(&out, 5 * sizeof(*out)) != hipSuccess ||
+        hipMalloc(&din, n * sizeof(float)) != hipSuccess ||
+        hipMalloc(&dres, n * sizeof(uint32_t)) != hipSuccess) {
+      (void)hipFree(out);
+      (void)hipFree(din);
+      (void)hipFree(dres);
+      return fail(LLMCP_Q8_ENOMEM, "exp self-test buffers");
+    }
+    unsigned long long host[5] = {0, 0, 0, 0, 0};
+    hipError_t e = hipMemsetAsync(out, 0, sizeof(host), ctx->stream);
+    if (e == hipSuccess)
+      e = launch_selftest_exp(out, din, dres, (uint32_t)cap, ctx->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(host, out, sizeof(host), hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    const int64_t k = e == hipSuccess ? (int64_t)std::min<unsigned long long>(host[3], (unsigned long long)cap) : 0;
+    if (e == hipSuccess && k > 0)
+      e = hipMemcpy(inputs, din, (size_t)k * sizeof(float), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && k > 0)
+      e = hipMemcpy(results, dres, (size_t)k * sizeof(uint32_t), hipMemcpyDeviceToHost);
     (void)hipFree(out);
     (void)hipFree(din);
     (void)hipFree(dres);
-    return fail(LLMCP_Q8_ENOMEM, "exp self-test buffers");
-  }
-  unsigned long long host[5] = {0, 0, 0, 0, 0};
-  hipError_t e = hipMemsetAsync(out, 0, sizeof(host), ctx->stream);
-  if (e == hipSuccess)
-    e = launch_selftest_exp(out, din, dres, (uint32_t)cap, ctx->stream);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(host, out, sizeof(host), hipMemcpyDeviceToHost, ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  const int64_t k = e == hipSuccess ? (int64_t)std::min<unsigned long long>(host[3], (unsigned long long)cap) : 0;
-  if (e == hipSuccess && k > 0)
-    e = hipMemcpy(inputs, din, (size_t)k * sizeof(float), hipMemcpyDeviceToHost);
-  if (e == hipSuccess && k > 0)
-    e = hipMemcpy(results, dres, (size_t)k * sizeof(uint32_t), hipMemcpyDeviceToHost);
-  (void)hipFree(out);
-  (void)hipFree(din);
-  (void)hipFree(dres);
-  if (e != hipSuccess) return hip_fail(e, "exp self-test");
-  for (int i = 0; i < 3; ++i) counts[i] = host[i];
-  counts[3] = host[4];
-  *stored = k;
-  return LLMCP_Q8_OK;
+    if (e != hipSuccess) return hip_fail(e, "exp self-test");
+    for (int i = 0; i < 3; ++i) counts[i] = host[i];
+    counts[3] = host[4];
+    *stored = k;
+    return LLMCP_Q8_OK;
+  });
 }
 
 // ------------------------------------------------------------- weights --
 
 int llmcp_q8_upload_p4(llmcp_q8_ctx *ctx, const void *host_p4, int64_t rows,
                        int64_t cols, float *repack_ms) {
-  if (!ctx || !host_p4) return fail(LLMCP_Q8_EINVAL, "null argument");
-  if (!packable(rows, cols))
-    return fail(LLMCP_Q8_DECLINED,
-                "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
-  int rc = set_device(ctx);
-  if (rc) return rc;
-  const uint64_t bytes = (uint64_t)rows * (uint64_t)(cols / kBlock) * 34u;
-  uint8_t *staging = nullptr;
-  if (hipMalloc(&staging, bytes) != hipSuccess)
-    return fail(LLMCP_Q8_ENOMEM, "staging of %llu bytes",
-                (unsigned long long)bytes);
-  hipError_t e = hipMemcpyAsync(staging, host_p4, bytes, hipMemcpyHostToDevice,
-                                ctx->stream);
-  if (e != hipSuccess) {
-    (void)hipFree(staging);
-    return hip_fail(e, "upload");
-  }
-  rc = register_from_device_p4(ctx, host_p4, staging, rows, cols, repack_ms);
-  (void)hipStreamSynchronize(ctx->stream);
-  (void)hipFree(staging);
-  return rc;
+  return guarded([&]() -> int {
+    if (!ctx || !host_p4) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (!packable(rows, cols))
+      return fail(LLMCP_Q8_DECLINED,
+                  "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    std::vector<Tensor> staged(1);
+    rc = stage_from_host_p4(ctx, host_p4, rows, cols, repack_ms, 0, staged[0]);
+    if (rc) return rc;
+    return commit_tensors(ctx, staged);
+  });
 }
 
 int llmcp_q8_register_device_p4(llmcp_q8_ctx *ctx, const void *dev_p4,
                                 int64_t rows, int64_t cols, float *repack_ms) {
-  if (!ctx || !dev_p4) return fail(LLMCP_Q8_EINVAL, "null argument");
-  if (!packable(rows, cols))
-    return fail(LLMCP_Q8_DECLINED,
-                "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
-  int rc = set_device(ctx);
-  if (rc) return rc;
-  rc = register_from_device_p4(ctx, dev_p4, (const uint8_t *)dev_p4, rows,
-                               cols, repack_ms);
-  if (rc) return rc;
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !dev_p4) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (!packable(rows, cols))
+      return fail(LLMCP_Q8_DECLINED,
+                  "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    return register_from_device_p4(ctx, dev_p4, (const uint8_t *)dev_p4, rows,
+                                   cols, repack_ms);
+  });
 }
 
 int llmcp_q8_release(llmcp_q8_ctx *ctx, const void *key) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  auto it = ctx->registry.find((uintptr_t)key);
-  if (it == ctx->registry.end())
-    return fail(LLMCP_Q8_ENOTFOUND, "no tensor registered at %p", key);
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  HIP_TRY(hipFree(it->second.dev));
-  ctx->registry.erase(it);
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    auto it = ctx->registry.find((uintptr_t)key);
+    if (it == ctx->registry.end())
+      return fail(LLMCP_Q8_ENOTFOUND, "no tensor registered at %p", key);
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipFree(it->second.dev));
+    ctx->weight_bytes -= it->second.dev_bytes;
+    ctx->registry.erase(it);
+    ++ctx->generation;
+    return LLMCP_Q8_OK;
+  });
 }
 
 uint64_t llmcp_q8_device_bytes(llmcp_q8_ctx *ctx, const void *key) {
@@ -614,44 +817,75 @@ extern "C" {
 
 int llmcp_q8_arena_inspect(const void *file, uint64_t file_bytes,
                            int64_t *num_tensors, int64_t *num_q8) {
-  std::vector<ArenaTensor> tensors;
-  int rc = parse_arena(file, file_bytes, tensors);
-  if (rc) return rc;
-  int64_t q8 = 0;
-  for (const ArenaTensor &t : tensors) q8 += t.dtype == "Q8_0";
-  if (num_tensors) *num_tensors = (int64_t)tensors.size();
-  if (num_q8) *num_q8 = q8;
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    std::vector<ArenaTensor> tensors;
+    int rc = parse_arena(file, file_bytes, tensors);
+    if (rc) return rc;
+    int64_t q8 = 0;
+    for (const ArenaTensor &t : tensors) q8 += t.dtype == "Q8_0";
+    if (num_tensors) *num_tensors = (int64_t)tensors.size();
+    if (num_q8) *num_q8 = q8;
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_upload_arena(llmcp_q8_ctx *ctx, const void *file,
                           uint64_t file_bytes, int64_t *num_q8) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  std::vector<ArenaTensor> tensors;
-  int rc = parse_arena(file, file_bytes, tensors);
-  if (rc) return rc;
-  // Validation passed: upload.  A failure part-way leaves earlier tensors
-  // registered and reports the error.
-  int64_t n = 0;
-  for (const ArenaTensor &t : tensors) {
-    if (t.dtype != "Q8_0") continue;
-    rc = llmcp_q8_upload_p4(ctx, t.data, t.shape[0], t.shape[1], nullptr);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    std::vector<ArenaTensor> tensors;
+    int rc = parse_arena(file, file_bytes, tensors);
     if (rc) return rc;
-    ++n;
-  }
-  if (num_q8) *num_q8 = n;
-  return LLMCP_Q8_OK;
+    // Validation passed: stage every Q8_0 tensor on the device, then register
+    // them all at once.  A failure part-way frees what was staged and leaves
+    // the registry as it was (Arena::load builds the new arena aside and
+    // replaces the old one only on success, WeightArena.cpp:28-29, :124-130).
+    if ((rc = set_device(ctx))) return rc;
+    std::vector<Tensor> staged;
+    uint64_t pending = 0;
+    for (const ArenaTensor &t : tensors) {
+      if (t.dtype != "Q8_0") continue;
+      Tensor st;
+      rc = stage_from_host_p4(ctx, t.data, t.shape[0], t.shape[1], nullptr,
+                              pending, st);
+      if (!rc) {
+        try {
+          staged.push_back(st);
+        } catch (...) {
+          (void)hipFree(st.dev);
+          rc = fail(LLMCP_Q8_ENOMEM, "host allocation failed");
+        }
+      }
+      if (rc) {
+        for (Tensor &x : staged) (void)hipFree(x.dev);
+        return rc;
+      }
+      pending += st.dev_bytes;
+    }
+    const int64_t n = (int64_t)staged.size();
+    if ((rc = commit_tensors(ctx, staged))) return rc;
+    if (num_q8) *num_q8 = n;
+    return LLMCP_Q8_OK;
+  });
 }
 
 // ------------------------------------------------------------------ ops --
 
 // One-row GEMV (decode, or prefill with M == 1).  Narrow outputs quantize
 // the input inside the GEMV; wide ones (lm_head) quantize it once first.
+// `ws` (nullable): a fixed workspace in place of the context's.
 static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
                        const Tensor *w1, const Rows &y, int activation,
-                       int64_t *argmax_dev, const Rows *residual = nullptr) {
-  int rc = ensure_decode_scratch(ctx, w0->rows, w0->cols);
-  if (rc) return rc;
+                       int64_t *argmax_dev, const Rows *residual = nullptr,
+                       const Workspace *fixed = nullptr) {
+  Workspace ws;
+  if (fixed) {
+    ws = *fixed;
+  } else {
+    int rc = ensure_decode_scratch(ctx, w0->rows, w0->cols);
+    if (rc) return rc;
+    ws = ctx_workspace(ctx);
+  }
   GemvLaunch l;
   const bool in_loop = gemv_quantizes_input(w0->rows, w1 ? 2 : 1) &&
                        (uintptr_t)x.data % (x.bf16 ? 8 : 16) == 0;
@@ -660,12 +894,14 @@ static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
     l.x_bf16 = x.bf16;
   } else {
     const int64_t nblk = passes_for(w0->cols) * kPassBlocks;
+    int rc = reserve(ctx, ws, (uint64_t)(nblk * kBlock), (uint64_t)(nblk * 4));
+    if (rc) return rc;
     hipError_t e = launch_quantize(x.data, x.bf16, 1, w0->cols, w0->cols,
-                                   ctx->qa, nblk * kBlock, ctx->sa, nblk, nblk,
+                                   ws.qa, nblk * kBlock, ws.sa, nblk, nblk,
                                    ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
-    l.qa = ctx->qa;
-    l.sa = ctx->sa;
+    l.qa = ws.qa;
+    l.sa = ws.sa;
   }
   l.w[0] = w0->dev;
   l.w[1] = w1 ? w1->dev : nullptr;
@@ -675,54 +911,56 @@ static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
   l.cols = w0->cols;
   l.nmat = w1 ? 2 : 1;
   l.activation = activation;
+  l.fma = ctx->fma();
   if (residual) l.residual = residual->data;
   if (argmax_dev) {
-    l.keys = ctx->keys;
+    l.keys = ws.keys;
     l.argmax_out = argmax_dev;
     // a failed call may have folded keys without the reduce that clears them
-    if (ctx->keys_dirty) {
-      hipError_t e = launch_argmax_reduce(ctx->keys, nullptr, ctx->stream);
+    if (*ws.keys_dirty) {
+      hipError_t e = launch_argmax_reduce(ws.keys, nullptr, ctx->stream);
       if (e != hipSuccess) return hip_fail(e, "argmax clear launch");
-      ctx->keys_dirty = false;
+      *ws.keys_dirty = false;
     }
   }
   hipError_t e = launch_gemv(l, ctx->stream);
   if (e != hipSuccess) {
-    if (argmax_dev) ctx->keys_dirty = true;
+    if (argmax_dev) *ws.keys_dirty = true;
     return hip_fail(e, "gemv launch");
   }
   return LLMCP_Q8_OK;
 }
 
-// Prefill: quantize all M rows once (zero-padded to whole units), then the
-// int8-MFMA GEMM.  The activation scratch grows on first use for a larger M.
-// Q8_1 of the input rows into the context's scratch (the GEMM's tiled
-// layout).  The scratch grows on first use for a larger M.
-static int gemm_quantize(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w) {
+// Q8_1 of the input rows into the workspace (the GEMM's tiled layout; the
+// context's scratch grows on first use for a larger M).
+static int gemm_quantize(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
+                         Workspace &ws) {
   const int64_t m = in.rows;
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   const int64_t row_tiles = (m + 31) / 32;  // the tiled layout pads M to 32
-  int rc = ensure_scratch(ctx, (uint64_t)(row_tiles * 32 * nblk * kBlock),
-                          (uint64_t)(row_tiles * 32 * nblk * 4));
+  int rc = reserve(ctx, ws, (uint64_t)(row_tiles * 32 * nblk * kBlock),
+                   (uint64_t)(row_tiles * 32 * nblk * 4));
   if (rc) return rc;
   hipError_t e = launch_quantize_tiled(in.data, in.bf16, m, in.ld, w->cols,
-                                       ctx->qa, ctx->sa, nblk, ctx->stream);
+                                       ws.qa, ws.sa, nblk, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "quantize launch");
   return LLMCP_Q8_OK;
 }
 
 // int8-MFMA GEMM of the quantized rows (gemm_quantize) against w.  `mul`
 // (nullable, f32 [m, ldg]) turns the epilogue into the SwiGLU multiply.
-// Decode-mode calls take the scalar epilogue whatever the prefill variant
-// (the decode path computes the x86 scalar form for every M, like the GEMV).
-static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
-                       const Rows &out, int activation, const float *mul,
-                       int64_t ldg, bool decode,
+// Both execution modes take the platform's epilogue: the reference's
+// decode and prefill emitters of one platform share it (fma on aarch64,
+// Q8Decode.cpp:200-203 and Q8Matmul.cpp:204-223; mul+add in the x86 scalar
+// path, Q8Scalar.cpp:192-199, which serves both modes).
+static int gemm_launch(llmcp_q8_ctx *ctx, const Workspace &ws, int64_t m,
+                       const Tensor *w, const Rows &out, int activation,
+                       const float *mul, int64_t ldg,
                        const Rows *residual = nullptr) {
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   GemmLaunch g;
-  g.qa = ctx->qa;
-  g.sa = ctx->sa;
+  g.qa = ws.qa;
+  g.sa = ws.sa;
   g.row_tiles = (int32_t)((m + 31) / 32);
   g.nblk = (int32_t)nblk;
   g.w = w->dev;
@@ -733,7 +971,7 @@ static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
   g.y_bf16 = out.bf16;
   g.ldy = out.ld;
   g.activation = activation;
-  g.fma = ctx->gemm_fma && !decode;
+  g.fma = ctx->fma();
   g.mul = mul;
   g.ldg = ldg;
   if (residual) {
@@ -746,10 +984,12 @@ static int gemm_launch(llmcp_q8_ctx *ctx, int64_t m, const Tensor *w,
 }
 
 static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
-                       const Rows &out, int activation, bool decode) {
-  int rc = gemm_quantize(ctx, in, w);
+                       const Rows &out, int activation,
+                       const Workspace *fixed = nullptr) {
+  Workspace ws = fixed ? *fixed : ctx_workspace(ctx);
+  int rc = gemm_quantize(ctx, in, w, ws);
   if (rc) return rc;
-  return gemm_launch(ctx, in.rows, w, out, activation, nullptr, 0, decode);
+  return gemm_launch(ctx, ws, in.rows, w, out, activation, nullptr, 0);
 }
 
 static int check_linear_shapes(const Rows &in, const Tensor *w,
@@ -787,12 +1027,11 @@ static int linear_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
   // One row (decode, or a one-row prefill such as the last-row lm_head):
-  // the GEMV (scalar epilogue) beats a 1/128-full GEMM tile.  Several rows:
-  // the GEMM (decode ones with the scalar epilogue, as Q8Decode.cpp:236-256
-  // accepts any M).
+  // the GEMV beats a 1/128-full GEMM tile.  Several rows: the GEMM (in
+  // either mode, as Q8Decode.cpp:236-256 accepts any M).  Both compute the
+  // platform's epilogue in block order.
   if (m == 1) return gemv_common(ctx, in, w, nullptr, out, activation, nullptr);
-  return gemm_common(ctx, in, w, out, activation,
-                     execution_mode == LLMCP_Q8_DECODE);
+  return gemm_common(ctx, in, w, out, activation);
 }
 
 // llmcp.linear + llmcp.add (ModelBuilder.cpp:271, :275): the residual add
@@ -812,9 +1051,9 @@ static int linear_add_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if ((rc = set_device(ctx))) return rc;
   if (m == 1)
     return gemv_common(ctx, in, w, nullptr, out, LLMCP_Q8_ACT_NONE, nullptr, &res);
-  if ((rc = gemm_quantize(ctx, in, w))) return rc;
-  return gemm_launch(ctx, m, w, out, LLMCP_Q8_ACT_NONE, nullptr, 0,
-                     execution_mode == LLMCP_Q8_DECODE, &res);
+  Workspace ws = ctx_workspace(ctx);
+  if ((rc = gemm_quantize(ctx, in, w, ws))) return rc;
+  return gemm_launch(ctx, ws, m, w, out, LLMCP_Q8_ACT_NONE, nullptr, 0, &res);
 }
 
 static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
@@ -833,7 +1072,6 @@ static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if (m == 0) return LLMCP_Q8_OK;
   if ((rc = set_device(ctx))) return rc;
   if (m == 1) return gemv_common(ctx, in, wg, wu, out, LLMCP_Q8_ACT_NONE, nullptr);
-  const bool decode = execution_mode == LLMCP_Q8_DECODE;
   // Several rows: the input quantized once; the gate GEMM with SiLU, then the up
   // GEMM whose epilogue does the multiply (MulOpLowering,
   // LowerToLinalg.cpp:377-393) with the gate's output.  f32: the gate goes
@@ -849,16 +1087,18 @@ static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
     g.bf16 = false;
     g.ld = wg->rows;
   }
-  if ((rc = gemm_quantize(ctx, in, wg))) return rc;
-  if ((rc = gemm_launch(ctx, m, wg, g, LLMCP_Q8_ACT_SILU, nullptr, 0, decode)))
+  Workspace ws = ctx_workspace(ctx);
+  if ((rc = gemm_quantize(ctx, in, wg, ws))) return rc;
+  if ((rc = gemm_launch(ctx, ws, m, wg, g, LLMCP_Q8_ACT_SILU, nullptr, 0)))
     return rc;
-  return gemm_launch(ctx, m, wu, out, LLMCP_Q8_ACT_NONE, (const float *)g.data,
-                     g.ld, decode);
+  return gemm_launch(ctx, ws, m, wu, out, LLMCP_Q8_ACT_NONE,
+                     (const float *)g.data, g.ld);
 }
 
 static int lm_head_impl(llmcp_q8_ctx *ctx, const Rows &in,
                         const llmcp_memref_i8_1d *table, const Rows &logits,
-                        int64_t *argmax_dev, int32_t execution_mode) {
+                        int64_t *argmax_dev, int32_t execution_mode,
+                        const Workspace *fixed = nullptr) {
   const Tensor *w = nullptr;
   int rc = resolve_weight(ctx, table, &w);
   if (rc) return rc;
@@ -869,23 +1109,28 @@ static int lm_head_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if ((rc = set_device(ctx))) return rc;
   if (m == 1)
     return gemv_common(ctx, in, w, nullptr, logits, LLMCP_Q8_ACT_NONE,
-                       argmax_dev);
+                       argmax_dev, nullptr, fixed);
   // Several rows: the GEMM writes every row's logits, then the first
   // maximum of the last row is reduced from HBM.
-  if ((rc = gemm_common(ctx, in, w, logits, LLMCP_Q8_ACT_NONE,
-                        execution_mode == LLMCP_Q8_DECODE)))
+  if ((rc = gemm_common(ctx, in, w, logits, LLMCP_Q8_ACT_NONE, fixed)))
     return rc;
   if (!argmax_dev) return LLMCP_Q8_OK;
-  if ((rc = ensure_argmax_slots(ctx))) return rc;
-  if (ctx->keys_dirty) {
-    hipError_t e = launch_argmax_reduce(ctx->keys, nullptr, ctx->stream);
+  Workspace ws;
+  if (fixed) {
+    ws = *fixed;
+  } else {
+    if ((rc = ensure_argmax_slots(ctx))) return rc;
+    ws = ctx_workspace(ctx);
+  }
+  if (*ws.keys_dirty) {
+    hipError_t e = launch_argmax_reduce(ws.keys, nullptr, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "argmax clear launch");
-    ctx->keys_dirty = false;
+    *ws.keys_dirty = false;
   }
   hipError_t e = launch_argmax_row((const float *)logits.data + (m - 1) * logits.ld,
-                                   logits.cols, argmax_dev, ctx->keys, ctx->stream);
+                                   logits.cols, argmax_dev, ws.keys, ctx->stream);
   if (e != hipSuccess) {
-    ctx->keys_dirty = true;
+    *ws.keys_dirty = true;
     return hip_fail(e, "argmax launch");
   }
   return LLMCP_Q8_OK;
@@ -917,8 +1162,7 @@ static int mlp_impl(llmcp_q8_ctx *ctx, const Rows &in,
   if (m > 1) {
     // Several rows: the SwiGLU GEMMs of llmcp_q8_swiglu (gate with SiLU,
     // then up with the multiply in its epilogue) into h, then the GEMM of h,
-    // with llmcp_q8_linear's epilogue choice (scalar in decode mode).
-    const bool decode = execution_mode == LLMCP_Q8_DECODE;
+    // with the platform's epilogue as for llmcp_q8_linear.
     const int64_t f = wg->rows;
     Rows h;
     if (hidden) {
@@ -940,13 +1184,14 @@ static int mlp_impl(llmcp_q8_ctx *ctx, const Rows &in,
       g.bf16 = false;
       g.ld = f;
     }
-    if ((rc = gemm_quantize(ctx, in, wg))) return rc;
-    if ((rc = gemm_launch(ctx, m, wg, g, LLMCP_Q8_ACT_SILU, nullptr, 0, decode)))
+    Workspace ws = ctx_workspace(ctx);
+    if ((rc = gemm_quantize(ctx, in, wg, ws))) return rc;
+    if ((rc = gemm_launch(ctx, ws, m, wg, g, LLMCP_Q8_ACT_SILU, nullptr, 0)))
       return rc;
-    if ((rc = gemm_launch(ctx, m, wu, h, LLMCP_Q8_ACT_NONE, (const float *)g.data,
-                          g.ld, decode)))
+    if ((rc = gemm_launch(ctx, ws, m, wu, h, LLMCP_Q8_ACT_NONE,
+                          (const float *)g.data, g.ld)))
       return rc;
-    return gemm_common(ctx, h, wd, out, LLMCP_Q8_ACT_NONE, decode);
+    return gemm_common(ctx, h, wd, out, LLMCP_Q8_ACT_NONE);
   }
   if ((rc = ensure_decode_scratch(ctx, wg->rows, wg->cols))) return rc;
   // Gate/up with the SwiGLU epilogue into h, then the down GEMV, which
@@ -976,9 +1221,10 @@ static int embedding_impl(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
   if (out.cols != w->cols || out.rows != tokens->sizes[0])
     return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
   // one thread per (token, 16 columns) on a one-dimensional grid of
-  // 256-thread workgroups, which allows 2^32 - 1 of them
+  // 256-thread workgroups; HIP bounds the grid's work-items (workgroups x
+  // 256) by 2^32 - 1
   if (tokens->sizes[0] > (1ll << 40) ||
-      (tokens->sizes[0] * (w->cols / 16) + 255) / 256 > 0xFFFFFFFFll)
+      (tokens->sizes[0] * (w->cols / 16) + 255) / 256 * 256 > 0xFFFFFFFFll)
     return fail(LLMCP_Q8_DECLINED, "too many tokens for one launch (%lld)",
                 (long long)tokens->sizes[0]);
   if ((rc = set_device(ctx))) return rc;
@@ -996,34 +1242,40 @@ int llmcp_q8_linear(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                     const llmcp_memref_i8_1d *weight,
                     llmcp_memref_f32_2d *output, int32_t activation,
                     int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  Rows in, out;
-  if (!view_of(input, false, in) || !view_of(output, false, out))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return linear_impl(ctx, in, weight, out, activation, execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    if (!view_of(input, false, in) || !view_of(output, false, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return linear_impl(ctx, in, weight, out, activation, execution_mode);
+  });
 }
 
 int llmcp_q8_linear_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
                          const llmcp_memref_i8_1d *weight,
                          llmcp_memref_bf16_2d *output, int32_t activation,
                          int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  Rows in, out;
-  if (!view_of(input, true, in) || !view_of(output, true, out))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return linear_impl(ctx, in, weight, out, activation, execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    if (!view_of(input, true, in) || !view_of(output, true, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return linear_impl(ctx, in, weight, out, activation, execution_mode);
+  });
 }
 
 int llmcp_q8_linear_add(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                         const llmcp_memref_i8_1d *weight,
                         const llmcp_memref_f32_2d *residual,
                         llmcp_memref_f32_2d *output, int32_t execution_mode) {
-  if (!ctx || !residual) return fail(LLMCP_Q8_EINVAL, "null argument");
-  Rows in, res, out;
-  if (!view_of(input, false, in) || !view_of(residual, false, res) ||
-      !view_of(output, false, out))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return linear_add_impl(ctx, in, weight, res, out, execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx || !residual) return fail(LLMCP_Q8_EINVAL, "null argument");
+    Rows in, res, out;
+    if (!view_of(input, false, in) || !view_of(residual, false, res) ||
+        !view_of(output, false, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return linear_add_impl(ctx, in, weight, res, out, execution_mode);
+  });
 }
 
 int llmcp_q8_linear_add_bf16(llmcp_q8_ctx *ctx,
@@ -1032,56 +1284,66 @@ int llmcp_q8_linear_add_bf16(llmcp_q8_ctx *ctx,
                              const llmcp_memref_bf16_2d *residual,
                              llmcp_memref_bf16_2d *output,
                              int32_t execution_mode) {
-  if (!ctx || !residual) return fail(LLMCP_Q8_EINVAL, "null argument");
-  Rows in, res, out;
-  if (!view_of(input, true, in) || !view_of(residual, true, res) ||
-      !view_of(output, true, out))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return linear_add_impl(ctx, in, weight, res, out, execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx || !residual) return fail(LLMCP_Q8_EINVAL, "null argument");
+    Rows in, res, out;
+    if (!view_of(input, true, in) || !view_of(residual, true, res) ||
+        !view_of(output, true, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return linear_add_impl(ctx, in, weight, res, out, execution_mode);
+  });
 }
 
 int llmcp_q8_swiglu(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                     const llmcp_memref_i8_1d *w_gate,
                     const llmcp_memref_i8_1d *w_up,
                     llmcp_memref_f32_2d *output, int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  Rows in, out;
-  if (!view_of(input, false, in) || !view_of(output, false, out))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return swiglu_impl(ctx, in, w_gate, w_up, out, execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    if (!view_of(input, false, in) || !view_of(output, false, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return swiglu_impl(ctx, in, w_gate, w_up, out, execution_mode);
+  });
 }
 
 int llmcp_q8_swiglu_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
                          const llmcp_memref_i8_1d *w_gate,
                          const llmcp_memref_i8_1d *w_up,
                          llmcp_memref_bf16_2d *output, int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  Rows in, out;
-  if (!view_of(input, true, in) || !view_of(output, true, out))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return swiglu_impl(ctx, in, w_gate, w_up, out, execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    if (!view_of(input, true, in) || !view_of(output, true, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return swiglu_impl(ctx, in, w_gate, w_up, out, execution_mode);
+  });
 }
 
 int llmcp_q8_lm_head(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *hidden,
                      const llmcp_memref_i8_1d *table,
                      llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
                      int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  Rows in, out;
-  if (!view_of(hidden, false, in) || !view_of(logits, false, out))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    if (!view_of(hidden, false, in) || !view_of(logits, false, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode);
+  });
 }
 
 int llmcp_q8_lm_head_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *hidden,
                           const llmcp_memref_i8_1d *table,
                           llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
                           int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  Rows in, out;
-  if (!view_of(hidden, true, in) || !view_of(logits, false, out))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    if (!view_of(hidden, true, in) || !view_of(logits, false, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode);
+  });
 }
 
 int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
@@ -1089,13 +1351,15 @@ int llmcp_q8_mlp(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                  const llmcp_memref_i8_1d *w_up,
                  const llmcp_memref_i8_1d *w_down, llmcp_memref_f32_2d *hidden,
                  llmcp_memref_f32_2d *output, int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  Rows in, out, h;
-  if (!view_of(input, false, in) || !view_of(output, false, out) ||
-      (hidden && !view_of(hidden, false, h)))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return mlp_impl(ctx, in, w_gate, w_up, w_down, hidden ? &h : nullptr, out,
-                  execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out, h;
+    if (!view_of(input, false, in) || !view_of(output, false, out) ||
+        (hidden && !view_of(hidden, false, h)))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return mlp_impl(ctx, in, w_gate, w_up, w_down, hidden ? &h : nullptr, out,
+                    execution_mode);
+  });
 }
 
 int llmcp_q8_mlp_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
@@ -1104,205 +1368,221 @@ int llmcp_q8_mlp_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
                       const llmcp_memref_i8_1d *w_down,
                       llmcp_memref_bf16_2d *hidden,
                       llmcp_memref_bf16_2d *output, int32_t execution_mode) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  Rows in, out, h;
-  if (!view_of(input, true, in) || !view_of(output, true, out) ||
-      (hidden && !view_of(hidden, true, h)))
-    return fail(LLMCP_Q8_DECLINED, kDenseMsg);
-  return mlp_impl(ctx, in, w_gate, w_up, w_down, hidden ? &h : nullptr, out,
-                  execution_mode);
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out, h;
+    if (!view_of(input, true, in) || !view_of(output, true, out) ||
+        (hidden && !view_of(hidden, true, h)))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return mlp_impl(ctx, in, w_gate, w_up, w_down, hidden ? &h : nullptr, out,
+                    execution_mode);
+  });
 }
 
 int llmcp_q8_embedding(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
                        const llmcp_memref_i8_1d *table,
                        llmcp_memref_f32_2d *output) {
-  if (!ctx || !tokens || !output) return fail(LLMCP_Q8_EINVAL, "null argument");
-  Rows out;
-  if (!view_of(output, false, out))
-    return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
-  return embedding_impl(ctx, tokens, table, out);
+  return guarded([&]() -> int {
+    if (!ctx || !tokens || !output) return fail(LLMCP_Q8_EINVAL, "null argument");
+    Rows out;
+    if (!view_of(output, false, out))
+      return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
+    return embedding_impl(ctx, tokens, table, out);
+  });
 }
 
 int llmcp_q8_embedding_bf16(llmcp_q8_ctx *ctx,
                             const llmcp_memref_i64_1d *tokens,
                             const llmcp_memref_i8_1d *table,
                             llmcp_memref_bf16_2d *output) {
-  if (!ctx || !tokens || !output) return fail(LLMCP_Q8_EINVAL, "null argument");
-  Rows out;
-  if (!view_of(output, true, out))
-    return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
-  return embedding_impl(ctx, tokens, table, out);
+  return guarded([&]() -> int {
+    if (!ctx || !tokens || !output) return fail(LLMCP_Q8_EINVAL, "null argument");
+    Rows out;
+    if (!view_of(output, true, out))
+      return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
+    return embedding_impl(ctx, tokens, table, out);
+  });
 }
 
 int llmcp_q8_quantize_activations(llmcp_q8_ctx *ctx,
                                   const llmcp_memref_f32_2d *input,
                                   int8_t *qa_dev, float *sa_dev) {
-  if (!ctx || !qa_dev || !sa_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
-  if (!dense_rows(input) || input->sizes[1] % kBlock)
-    return fail(LLMCP_Q8_DECLINED, "input must be row-major with K %% 32 == 0");
-  int rc = set_device(ctx);
-  if (rc) return rc;
-  const int64_t m = input->sizes[0], k = input->sizes[1];
-  if (m == 0) return LLMCP_Q8_OK;
-  hipError_t e = launch_quantize(input->data + input->offset, false, m,
-                                 input->strides[0], k, qa_dev, k, sa_dev,
-                                 k / kBlock, k / kBlock, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "quantize launch");
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !qa_dev || !sa_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (!dense_rows(input) || input->sizes[1] % kBlock)
+      return fail(LLMCP_Q8_DECLINED, "input must be row-major with K %% 32 == 0");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const int64_t m = input->sizes[0], k = input->sizes[1];
+    if (m == 0) return LLMCP_Q8_OK;
+    hipError_t e = launch_quantize(input->data + input->offset, false, m,
+                                   input->strides[0], k, qa_dev, k, sa_dev,
+                                   k / kBlock, k / kBlock, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_block_dots(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
                         const llmcp_memref_i8_1d *weight, int32_t *out_dev) {
-  if (!ctx || !out_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
-  const Tensor *w = nullptr;
-  int rc = resolve_weight(ctx, weight, &w);
-  if (rc) return rc;
-  if (!dense_rows(input) || input->sizes[1] != w->cols)
-    return fail(LLMCP_Q8_DECLINED, "input must be row-major [M, K]");
-  if ((rc = set_device(ctx))) return rc;
-  const int64_t m = input->sizes[0], k = input->sizes[1], b = k / kBlock;
-  if (m == 0) return LLMCP_Q8_OK;
-  if ((rc = ensure_scratch(ctx, (uint64_t)(m * k), (uint64_t)(m * b * 4))))
-    return rc;
-  hipError_t e = launch_quantize(input->data + input->offset, false, m,
-                                 input->strides[0], k, ctx->qa, k, ctx->sa, b,
-                                 b, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "quantize launch");
-  e = launch_block_dots(ctx->qa, k, m, w->dev, w->rows, w->cols, out_dev,
-                        ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "block dots launch");
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !out_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
+    const Tensor *w = nullptr;
+    int rc = resolve_weight(ctx, weight, &w);
+    if (rc) return rc;
+    if (!dense_rows(input) || input->sizes[1] != w->cols)
+      return fail(LLMCP_Q8_DECLINED, "input must be row-major [M, K]");
+    if ((rc = set_device(ctx))) return rc;
+    const int64_t m = input->sizes[0], k = input->sizes[1], b = k / kBlock;
+    if (m == 0) return LLMCP_Q8_OK;
+    if ((rc = ensure_scratch(ctx, (uint64_t)(m * k), (uint64_t)(m * b * 4))))
+      return rc;
+    hipError_t e = launch_quantize(input->data + input->offset, false, m,
+                                   input->strides[0], k, ctx->qa, k, ctx->sa, b,
+                                   b, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+    e = launch_block_dots(ctx->qa, k, m, w->dev, w->rows, w->cols, out_dev,
+                          ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "block dots launch");
+    return LLMCP_Q8_OK;
+  });
 }
 
 // ------------------------------------------------------ offline packing --
 
 int llmcp_q8_pack_p4_host(const float *w, int64_t rows, int64_t cols,
                           uint8_t *out) {
-  if (!w || !out) return fail(LLMCP_Q8_EINVAL, "null argument");
-  if (!packable(rows, cols))
-    return fail(LLMCP_Q8_DECLINED,
-                "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
-  const int64_t blocks = cols / kBlock, groups = rows / kLanes;
-#pragma omp parallel for schedule(static)
-  for (int64_t g = 0; g < groups; ++g) {
-    for (int64_t b = 0; b < blocks; ++b) {
-      uint8_t *rec = out + (g * blocks + b) * kRecord;
-      for (int r = 0; r < kLanes; ++r) {
-        const float *v = w + (g * kLanes + r) * cols + b * kBlock;
-        float amax = 0.0f;
-        for (int i = 0; i < kBlock; ++i) amax = std::max(amax, std::fabs(v[i]));
-        uint16_t d = 0;
-        int8_t q[kBlock] = {0};
-        if (amax != 0.0f) {
-          const float scale = amax / 127.0f;
-          d = host_f32_to_f16(scale);
-          for (int i = 0; i < kBlock; ++i) {
-            long x = std::lround(v[i] / scale);
-            q[i] = (int8_t)std::min(127L, std::max(-127L, x));
+  return guarded([&]() -> int {
+    if (!w || !out) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (!packable(rows, cols))
+      return fail(LLMCP_Q8_DECLINED,
+                  "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
+    const int64_t blocks = cols / kBlock, groups = rows / kLanes;
+  #pragma omp parallel for schedule(static)
+    for (int64_t g = 0; g < groups; ++g) {
+      for (int64_t b = 0; b < blocks; ++b) {
+        uint8_t *rec = out + (g * blocks + b) * kRecord;
+        for (int r = 0; r < kLanes; ++r) {
+          const float *v = w + (g * kLanes + r) * cols + b * kBlock;
+          float amax = 0.0f;
+          for (int i = 0; i < kBlock; ++i) amax = std::max(amax, std::fabs(v[i]));
+          uint16_t d = 0;
+          int8_t q[kBlock] = {0};
+          if (amax != 0.0f) {
+            const float scale = amax / 127.0f;
+            d = host_f32_to_f16(scale);
+            for (int i = 0; i < kBlock; ++i) {
+              long x = std::lround(v[i] / scale);
+              q[i] = (int8_t)std::min(127L, std::max(-127L, x));
+            }
           }
+          rec[2 * r] = (uint8_t)(d & 0xff);
+          rec[2 * r + 1] = (uint8_t)(d >> 8);
+          for (int c = 0; c < 8; ++c)
+            std::memcpy(rec + 8 + 16 * c + 4 * r, q + 4 * c, 4);
         }
-        rec[2 * r] = (uint8_t)(d & 0xff);
-        rec[2 * r + 1] = (uint8_t)(d >> 8);
-        for (int c = 0; c < 8; ++c)
-          std::memcpy(rec + 8 + 16 * c + 4 * r, q + 4 * c, 4);
       }
     }
-  }
-  return LLMCP_Q8_OK;
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_synthesize_p4(llmcp_q8_ctx *ctx, uint64_t seed, int64_t rows,
                            int64_t cols, float stddev, float *w_dev,
                            void *p4_dev) {
-  if (!ctx || !p4_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
-  if (!packable(rows, cols))
-    return fail(LLMCP_Q8_DECLINED,
-                "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
-  int rc = set_device(ctx);
-  if (rc) return rc;
-  float *w = w_dev;
-  if (!w && hipMalloc(&w, (size_t)rows * (size_t)cols * 4) != hipSuccess)
-    return fail(LLMCP_Q8_ENOMEM, "synthetic weight staging");
-  hipError_t e = launch_synth(seed, rows, cols, stddev, w, ctx->stream);
-  if (e == hipSuccess)
-    e = launch_pack_p4(w, rows, cols, (uint8_t *)p4_dev, ctx->stream);
-  if (!w_dev) {
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(w);
-  }
-  if (e != hipSuccess) return hip_fail(e, "synthesize");
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !p4_dev) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (!packable(rows, cols))
+      return fail(LLMCP_Q8_DECLINED,
+                  "packed Q8_0 requires rows %% 8 == 0 and cols %% 32 == 0");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    float *w = w_dev;
+    if (!w && hipMalloc(&w, (size_t)rows * (size_t)cols * 4) != hipSuccess)
+      return fail(LLMCP_Q8_ENOMEM, "synthetic weight staging");
+    hipError_t e = launch_synth(seed, rows, cols, stddev, w, ctx->stream);
+    if (e == hipSuccess)
+      e = launch_pack_p4(w, rows, cols, (uint8_t *)p4_dev, ctx->stream);
+    if (!w_dev) {
+      (void)hipStreamSynchronize(ctx->stream);
+      (void)hipFree(w);
+    }
+    if (e != hipSuccess) return hip_fail(e, "synthesize");
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_write_arena(const char *path, int32_t count,
                          const char *const *names, const int64_t *rows,
                          const int64_t *cols, const void *const *p4) {
-  if (!path || count <= 0 || !names || !rows || !cols || !p4)
-    return fail(LLMCP_Q8_EINVAL, "bad arena writer arguments");
-  std::vector<uint64_t> offsets(count), sizes(count);
-  uint64_t cursor = 64;
-  for (int32_t i = 0; i < count; ++i) {
-    if (!names[i] || !names[i][0] || !packable(rows[i], cols[i]))
-      return fail(LLMCP_Q8_EINVAL, "tensor %d: bad name or shape", i);
-    cursor = (cursor + 63) / 64 * 64;
-    offsets[i] = cursor;
-    sizes[i] = (uint64_t)rows[i] * (uint64_t)(cols[i] / 32) * 34u;
-    cursor += sizes[i];
-  }
-  const uint64_t arena = (cursor + 63) / 64 * 64;
-  std::string m = "{\"model\":\"synthetic\",\"total_bytes\":" +
-                  std::to_string(arena) +
-                  ",\"header_bytes\":64,\"group_stride\":0,\"num_groups\":0,"
-                  "\"alignment\":64,\"quantization\":\"q8_0\",\"block_size\":32,"
-                  "\"quant_layout\":\"q8_0_p4\",\"tensors\":[";
-  for (int32_t i = 0; i < count; ++i) {
-    std::string name;
-    for (const char *c = names[i]; *c; ++c) {
-      if (*c == '"' || *c == '\\') name += '\\';
-      name += *c;
+  return guarded([&]() -> int {
+    if (!path || count <= 0 || !names || !rows || !cols || !p4)
+      return fail(LLMCP_Q8_EINVAL, "bad arena writer arguments");
+    std::vector<uint64_t> offsets(count), sizes(count);
+    uint64_t cursor = 64;
+    for (int32_t i = 0; i < count; ++i) {
+      if (!names[i] || !names[i][0] || !packable(rows[i], cols[i]))
+        return fail(LLMCP_Q8_EINVAL, "tensor %d: bad name or shape", i);
+      cursor = (cursor + 63) / 64 * 64;
+      offsets[i] = cursor;
+      sizes[i] = (uint64_t)rows[i] * (uint64_t)(cols[i] / 32) * 34u;
+      cursor += sizes[i];
     }
-    m += (i ? "," : "");
-    m += "{\"name\":\"" + name + "\",\"offset\":" + std::to_string(offsets[i]) +
-         ",\"size\":" + std::to_string(sizes[i]) +
-         ",\"dtype\":\"Q8_0\",\"source_size\":" +
-         std::to_string((uint64_t)rows[i] * (uint64_t)cols[i] * 4u) +
-         ",\"shape\":[" + std::to_string(rows[i]) + "," +
-         std::to_string(cols[i]) + "]}";
-  }
-  m += "]}\n";
-  FILE *fp = std::fopen(path, "wb");
-  if (!fp) return fail(LLMCP_Q8_EIO, "cannot open %s", path);
-  std::vector<uint8_t> header(64, 0);
-  bool ok = std::fwrite(header.data(), 1, 64, fp) == 64;
-  uint64_t pos = 64;
-  std::vector<uint8_t> zeros(64, 0);
-  for (int32_t i = 0; i < count && ok; ++i) {
-    while (ok && pos < offsets[i]) {
-      const uint64_t n = std::min<uint64_t>(64, offsets[i] - pos);
+    const uint64_t arena = (cursor + 63) / 64 * 64;
+    std::string m = "{\"model\":\"synthetic\",\"total_bytes\":" +
+                    std::to_string(arena) +
+                    ",\"header_bytes\":64,\"group_stride\":0,\"num_groups\":0,"
+                    "\"alignment\":64,\"quantization\":\"q8_0\",\"block_size\":32,"
+                    "\"quant_layout\":\"q8_0_p4\",\"tensors\":[";
+    for (int32_t i = 0; i < count; ++i) {
+      std::string name;
+      for (const char *c = names[i]; *c; ++c) {
+        if (*c == '"' || *c == '\\') name += '\\';
+        name += *c;
+      }
+      m += (i ? "," : "");
+      m += "{\"name\":\"" + name + "\",\"offset\":" + std::to_string(offsets[i]) +
+           ",\"size\":" + std::to_string(sizes[i]) +
+           ",\"dtype\":\"Q8_0\",\"source_size\":" +
+           std::to_string((uint64_t)rows[i] * (uint64_t)cols[i] * 4u) +
+           ",\"shape\":[" + std::to_string(rows[i]) + "," +
+           std::to_string(cols[i]) + "]}";
+    }
+    m += "]}\n";
+    FILE *fp = std::fopen(path, "wb");
+    if (!fp) return fail(LLMCP_Q8_EIO, "cannot open %s", path);
+    std::vector<uint8_t> header(64, 0);
+    bool ok = std::fwrite(header.data(), 1, 64, fp) == 64;
+    uint64_t pos = 64;
+    std::vector<uint8_t> zeros(64, 0);
+    for (int32_t i = 0; i < count && ok; ++i) {
+      while (ok && pos < offsets[i]) {
+        const uint64_t n = std::min<uint64_t>(64, offsets[i] - pos);
+        ok = std::fwrite(zeros.data(), 1, n, fp) == n;
+        pos += n;
+      }
+      ok = ok && std::fwrite(p4[i], 1, sizes[i], fp) == sizes[i];
+      pos += sizes[i];
+    }
+    while (ok && pos < arena) {
+      const uint64_t n = std::min<uint64_t>(64, arena - pos);
       ok = std::fwrite(zeros.data(), 1, n, fp) == n;
       pos += n;
     }
-    ok = ok && std::fwrite(p4[i], 1, sizes[i], fp) == sizes[i];
-    pos += sizes[i];
-  }
-  while (ok && pos < arena) {
-    const uint64_t n = std::min<uint64_t>(64, arena - pos);
-    ok = std::fwrite(zeros.data(), 1, n, fp) == n;
-    pos += n;
-  }
-  ok = ok && std::fwrite(m.data(), 1, m.size(), fp) == m.size();
-  // Publish the header last (WeightPacker.cpp:269-272).
-  std::memcpy(header.data(), "LLMCPWGT", 8);
-  wr32(header.data() + 8, 1);
-  wr32(header.data() + 12, 64);
-  wr64(header.data() + 16, arena);
-  wr64(header.data() + 24, arena);
-  wr64(header.data() + 32, m.size());
-  ok = ok && std::fflush(fp) == 0 && std::fseek(fp, 0, SEEK_SET) == 0 &&
-       std::fwrite(header.data(), 1, 64, fp) == 64;
-  ok = (std::fclose(fp) == 0) && ok;
-  if (!ok) return fail(LLMCP_Q8_EIO, "short write to %s", path);
-  return LLMCP_Q8_OK;
+    ok = ok && std::fwrite(m.data(), 1, m.size(), fp) == m.size();
+    // Publish the header last (WeightPacker.cpp:269-272).
+    std::memcpy(header.data(), "LLMCPWGT", 8);
+    wr32(header.data() + 8, 1);
+    wr32(header.data() + 12, 64);
+    wr64(header.data() + 16, arena);
+    wr64(header.data() + 24, arena);
+    wr64(header.data() + 32, m.size());
+    ok = ok && std::fflush(fp) == 0 && std::fseek(fp, 0, SEEK_SET) == 0 &&
+         std::fwrite(header.data(), 1, 64, fp) == 64;
+    ok = (std::fclose(fp) == 0) && ok;
+    if (!ok) return fail(LLMCP_Q8_EIO, "short write to %s", path);
+    return LLMCP_Q8_OK;
+  });
 }
 
 // ---------------------------------------------------- MLIR C interface --
@@ -1312,9 +1592,11 @@ int32_t _mlir_ciface_llmcp_q8_linear(llmcp_memref_f32_2d *input,
                                      llmcp_memref_f32_2d *output,
                                      int32_t activation,
                                      int32_t execution_mode) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  return llmcp_q8_linear(g_default_ctx, input, weight, output, activation,
-                         execution_mode);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_linear(g_default_ctx, input, weight, output, activation,
+                           execution_mode);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_linear_add(llmcp_memref_f32_2d *input,
@@ -1322,9 +1604,11 @@ int32_t _mlir_ciface_llmcp_q8_linear_add(llmcp_memref_f32_2d *input,
                                          llmcp_memref_f32_2d *residual,
                                          llmcp_memref_f32_2d *output,
                                          int32_t execution_mode) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  return llmcp_q8_linear_add(g_default_ctx, input, weight, residual, output,
-                             execution_mode);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_linear_add(g_default_ctx, input, weight, residual, output,
+                               execution_mode);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_linear_add_bf16(llmcp_memref_bf16_2d *input,
@@ -1332,9 +1616,11 @@ int32_t _mlir_ciface_llmcp_q8_linear_add_bf16(llmcp_memref_bf16_2d *input,
                                               llmcp_memref_bf16_2d *residual,
                                               llmcp_memref_bf16_2d *output,
                                               int32_t execution_mode) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  return llmcp_q8_linear_add_bf16(g_default_ctx, input, weight, residual,
-                                  output, execution_mode);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_linear_add_bf16(g_default_ctx, input, weight, residual,
+                                    output, execution_mode);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
@@ -1342,9 +1628,11 @@ int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
                                      llmcp_memref_i8_1d *w_up,
                                      llmcp_memref_f32_2d *output,
                                      int32_t execution_mode) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  return llmcp_q8_swiglu(g_default_ctx, input, w_gate, w_up, output,
-                         execution_mode);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_swiglu(g_default_ctx, input, w_gate, w_up, output,
+                           execution_mode);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_lm_head(llmcp_memref_f32_2d *hidden,
@@ -1352,17 +1640,21 @@ int32_t _mlir_ciface_llmcp_q8_lm_head(llmcp_memref_f32_2d *hidden,
                                       llmcp_memref_f32_2d *logits,
                                       llmcp_memref_i64_1d *argmax,
                                       int32_t execution_mode) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  int64_t *am = argmax ? argmax->data + argmax->offset : nullptr;
-  return llmcp_q8_lm_head(g_default_ctx, hidden, table, logits, am,
-                          execution_mode);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    int64_t *am = argmax ? argmax->data + argmax->offset : nullptr;
+    return llmcp_q8_lm_head(g_default_ctx, hidden, table, logits, am,
+                            execution_mode);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_embedding(llmcp_memref_i64_1d *tokens,
                                         llmcp_memref_i8_1d *table,
                                         llmcp_memref_f32_2d *output) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  return llmcp_q8_embedding(g_default_ctx, tokens, table, output);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_embedding(g_default_ctx, tokens, table, output);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_linear_bf16(llmcp_memref_bf16_2d *input,
@@ -1370,9 +1662,11 @@ int32_t _mlir_ciface_llmcp_q8_linear_bf16(llmcp_memref_bf16_2d *input,
                                           llmcp_memref_bf16_2d *output,
                                           int32_t activation,
                                           int32_t execution_mode) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  return llmcp_q8_linear_bf16(g_default_ctx, input, weight, output, activation,
-                              execution_mode);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_linear_bf16(g_default_ctx, input, weight, output, activation,
+                                execution_mode);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_swiglu_bf16(llmcp_memref_bf16_2d *input,
@@ -1380,9 +1674,11 @@ int32_t _mlir_ciface_llmcp_q8_swiglu_bf16(llmcp_memref_bf16_2d *input,
                                           llmcp_memref_i8_1d *w_up,
                                           llmcp_memref_bf16_2d *output,
                                           int32_t execution_mode) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  return llmcp_q8_swiglu_bf16(g_default_ctx, input, w_gate, w_up, output,
-                              execution_mode);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_swiglu_bf16(g_default_ctx, input, w_gate, w_up, output,
+                                execution_mode);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_lm_head_bf16(llmcp_memref_bf16_2d *hidden,
@@ -1390,115 +1686,171 @@ int32_t _mlir_ciface_llmcp_q8_lm_head_bf16(llmcp_memref_bf16_2d *hidden,
                                            llmcp_memref_f32_2d *logits,
                                            llmcp_memref_i64_1d *argmax,
                                            int32_t execution_mode) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  int64_t *am = argmax ? argmax->data + argmax->offset : nullptr;
-  return llmcp_q8_lm_head_bf16(g_default_ctx, hidden, table, logits, am,
-                               execution_mode);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    int64_t *am = argmax ? argmax->data + argmax->offset : nullptr;
+    return llmcp_q8_lm_head_bf16(g_default_ctx, hidden, table, logits, am,
+                                 execution_mode);
+  });
 }
 
 int32_t _mlir_ciface_llmcp_q8_embedding_bf16(llmcp_memref_i64_1d *tokens,
                                              llmcp_memref_i8_1d *table,
                                              llmcp_memref_bf16_2d *output) {
-  if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
-  return llmcp_q8_embedding_bf16(g_default_ctx, tokens, table, output);
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_embedding_bf16(g_default_ctx, tokens, table, output);
+  });
 }
 
 // --------------------------------------------------- device plumbing --
 
 int llmcp_q8_dev_alloc(llmcp_q8_ctx *ctx, uint64_t bytes, void **out) {
-  if (!ctx || !out) return fail(LLMCP_Q8_EINVAL, "null argument");
-  int rc = set_device(ctx);
-  if (rc) return rc;
-  if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess)
-    return fail(LLMCP_Q8_ENOMEM, "hipMalloc of %llu bytes",
-                (unsigned long long)bytes);
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !out) return fail(LLMCP_Q8_EINVAL, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess)
+      return fail(LLMCP_Q8_ENOMEM, "hipMalloc of %llu bytes",
+                  (unsigned long long)bytes);
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_dev_free(llmcp_q8_ctx *ctx, void *ptr) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  if (!ptr) return LLMCP_Q8_OK;
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  HIP_TRY(hipFree(ptr));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    if (!ptr) return LLMCP_Q8_OK;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipFree(ptr));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_memcpy_h2d(llmcp_q8_ctx *ctx, void *dst, const void *src,
                         uint64_t bytes) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_memcpy_d2h(llmcp_q8_ctx *ctx, void *dst, const void *src,
                         uint64_t bytes) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_memcpy_d2d(llmcp_q8_ctx *ctx, void *dst, const void *src,
                         uint64_t bytes) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_event_create(void **event) {
-  if (!event) return fail(LLMCP_Q8_EINVAL, "null argument");
-  hipEvent_t e;
-  HIP_TRY(hipEventCreate(&e));
-  *event = (void *)e;
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!event) return fail(LLMCP_Q8_EINVAL, "null argument");
+    hipEvent_t e;
+    HIP_TRY(hipEventCreate(&e));
+    *event = (void *)e;
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_event_destroy(void *event) {
-  if (event) HIP_TRY(hipEventDestroy((hipEvent_t)event));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (event) HIP_TRY(hipEventDestroy((hipEvent_t)event));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_event_record(llmcp_q8_ctx *ctx, void *event) {
-  if (!ctx || !event) return fail(LLMCP_Q8_EINVAL, "null argument");
-  HIP_TRY(hipEventRecord((hipEvent_t)event, ctx->stream));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !event) return fail(LLMCP_Q8_EINVAL, "null argument");
+    HIP_TRY(hipEventRecord((hipEvent_t)event, ctx->stream));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_event_elapsed_ms(void *start, void *stop, float *ms) {
-  if (!start || !stop || !ms) return fail(LLMCP_Q8_EINVAL, "null argument");
-  HIP_TRY(hipEventSynchronize((hipEvent_t)stop));
-  HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!start || !stop || !ms) return fail(LLMCP_Q8_EINVAL, "null argument");
+    HIP_TRY(hipEventSynchronize((hipEvent_t)stop));
+    HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_graph_begin(llmcp_q8_ctx *ctx) {
-  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
-  HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_graph_end(llmcp_q8_ctx *ctx, void **graph_exec) {
-  if (!ctx || !graph_exec) return fail(LLMCP_Q8_EINVAL, "null argument");
-  hipGraph_t g = nullptr;
-  HIP_TRY(hipStreamEndCapture(ctx->stream, &g));
-  hipGraphExec_t ex = nullptr;
-  hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-  (void)hipGraphDestroy(g);
-  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
-  *graph_exec = (void *)ex;
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !graph_exec) return fail(LLMCP_Q8_EINVAL, "null argument");
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture(ctx->stream, &g));
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    try {
+      std::lock_guard<std::mutex> lock(g_graph_mutex);
+      g_graphs[(void *)ex] = {ctx, ctx->generation};
+    } catch (...) {
+      (void)hipGraphExecDestroy(ex);
+      throw;
+    }
+    *graph_exec = (void *)ex;
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_graph_launch(llmcp_q8_ctx *ctx, void *graph_exec) {
-  if (!ctx || !graph_exec) return fail(LLMCP_Q8_EINVAL, "null argument");
-  HIP_TRY(hipGraphLaunch((hipGraphExec_t)graph_exec, ctx->stream));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!ctx || !graph_exec) return fail(LLMCP_Q8_EINVAL, "null argument");
+    {
+      std::lock_guard<std::mutex> lock(g_graph_mutex);
+      auto it = g_graphs.find(graph_exec);
+      if (it == g_graphs.end() || it->second.ctx != ctx)
+        return fail(LLMCP_Q8_EINVAL, "graph %p was not captured on this context",
+                    graph_exec);
+      // Its kernels hold the addresses of the workspace and weights as they
+      // were at capture; replaying after one of them was freed would touch
+      // freed memory.
+      if (it->second.generation != ctx->generation)
+        return fail(LLMCP_Q8_ESTALE,
+                    "the workspace or a weight was reallocated after this "
+                    "graph was captured; capture it again");
+    }
+    HIP_TRY(hipGraphLaunch((hipGraphExec_t)graph_exec, ctx->stream));
+    return LLMCP_Q8_OK;
+  });
 }
 
 int llmcp_q8_graph_destroy(void *graph_exec) {
-  if (graph_exec) HIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
-  return LLMCP_Q8_OK;
+  return guarded([&]() -> int {
+    if (!graph_exec) return LLMCP_Q8_OK;
+    {
+      std::lock_guard<std::mutex> lock(g_graph_mutex);
+      g_graphs.erase(graph_exec);
+    }
+    HIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    return LLMCP_Q8_OK;
+  });
 }
 
 }  // extern "C"

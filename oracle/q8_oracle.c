@@ -26,8 +26,10 @@
  *   block_dots          brute-force int64 einsum.
  *   linear_*            exact-operand construction of run_numeric.py:690-732
  *                       against an float64 matmul at rel 1e-5 / abs 1e-6.
- *   silu/sigmoid/       float64 closed forms within ulp-level tolerance
- *   softplus            (softplus also against log1p(exp) at the overflow end).
+ *   silu/sigmoid/       float64 closed forms within ulp-level tolerance;
+ *   softplus            softplus against log(f32(1 + f32(exp v))), the
+ *                       lowered log1p, which is 0 where exp(v) < 2^-24 (a
+ *                       true log1p there is not), and at the overflow end.
  *   f32_to_bf16         torch's float32 -> bfloat16 conversion (round to
  *                       nearest even) on ties, subnormals, inf and NaN.
  *   argmax              numpy argmax (first maximum), std::max_element rule.
@@ -275,13 +277,18 @@ void oracle_block_dots(const int8_t *qa, const uint8_t *p4, int64_t rows,
  * round once to f32, so the two agree bit for bit. */
 float oracle_expf(float x) { return (float)exp((double)x); }
 
-/* log1p for the softplus activation (math.log1p -> libm log1pf), evaluated
- * in double and rounded once, like oracle_expf. */
-float oracle_log1pf(float x) { return (float)log1p((double)x); }
+/* math.log1p as the reference compiles it: --convert-math-to-llvm
+ * (tools/llmcp-compile/llmcp-compile.cpp:186) lowers log1p(y) to
+ * log(1 + y), the sum an f32 add; the log is evaluated in double and
+ * rounded once, like oracle_expf. */
+float oracle_log1pf(float x) {
+  float s = 1.0f + x;
+  return (float)log((double)s);
+}
 
 /* applyMatmulActivation (MatmulLoweringCommon.cpp:78-103), one MLIR op at a
  * time in f32: sigmoid = 1/(1+exp(-v)); silu(v) = v * sigmoid(v);
- * softplus(v) = log1p(exp(v)). */
+ * softplus(v) = log1p(exp(v)) with log1p lowered as above. */
 float oracle_sigmoid(float v) {
   float e = oracle_expf(-v);
   return 1.0f / (1.0f + e);

@@ -27,8 +27,12 @@ def q8():
     return llmcp_amd
 
 
-@pytest.fixture(scope="session")
-def ctx(q8):
+# Every GPU test that takes `ctx` runs once per reference platform: the
+# aarch64 SDOT arithmetic (fma epilogue, the library default) and the x86
+# scalar path (mul+add); `ctx.epilogue` names the oracle variant to match.
+@pytest.fixture(scope="session", params=["aarch64", "x86"])
+def ctx(q8, request):
     c = q8.Context(0)
+    c.set_platform(request.param)
     yield c
     c.close()

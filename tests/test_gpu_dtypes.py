@@ -38,7 +38,7 @@ def test_linear_activations(ctx, oracle, act, m):
     mode = "decode" if m == 1 else "prefill"
     ctx.linear(xd, t, yd, m, activation=act, mode=mode)
     y = ctx.to_host(yd, (m, n), np.float32)
-    epi = "scalar" if m == 1 else "fma"  # GEMV: scalar path; GEMM: default fma
+    epi = ctx.epilogue  # GEMV and GEMM: the platform's epilogue
     assert bits_equal(y, oracle.linear(x, p4, n, activation=act, epilogue=epi))
     ctx.release(t)
 
@@ -57,7 +57,7 @@ def test_linear_bf16(ctx, oracle, m, k, act):
     mode = "decode" if m == 1 else "prefill"
     ctx.linear(xd, t, yd, m, activation=act, mode=mode, dtype="bf16")
     y = ctx.to_host(yd, (m, n), np.uint16)
-    epi = "scalar" if m == 1 else "fma"
+    epi = ctx.epilogue
     ref = oracle.linear(oracle.bf16_bits_to_f32(xb), p4, n, activation=act,
                         epilogue=epi)
     assert bits_equal(y, to_bf16(oracle, ref))
@@ -78,16 +78,16 @@ def test_linear_bf16_misaligned_row(ctx, oracle):
     yd = ctx.alloc(n * 2)
     ctx.linear(buf.ptr + 2, t, yd, 1, dtype="bf16")
     y = ctx.to_host(yd, (1, n), np.uint16)
-    ref = oracle.linear(oracle.bf16_bits_to_f32(xb), p4, n)
+    ref = oracle.linear(oracle.bf16_bits_to_f32(xb), p4, n, epilogue=ctx.epilogue)
     assert bits_equal(y, to_bf16(oracle, ref))
     ctx.release(t)
 
 
-def swiglu_ref_bf16(oracle, xf, p4g, p4u, n):
+def swiglu_ref_bf16(oracle, xf, p4g, p4u, n, epi):
     g = to_bf16(oracle, oracle.linear(xf, p4g, n, activation="silu",
-                                      epilogue="scalar" if xf.shape[0] == 1 else "fma"))
+                                      epilogue=epi))
     u = to_bf16(oracle, oracle.linear(xf, p4u, n,
-                                      epilogue="scalar" if xf.shape[0] == 1 else "fma"))
+                                      epilogue=epi))
     prod = oracle.bf16_bits_to_f32(g) * oracle.bf16_bits_to_f32(u)  # exact in f32
     return to_bf16(oracle, prod)
 
@@ -103,7 +103,7 @@ def test_swiglu_bf16(ctx, oracle, m):
     xd, hd = ctx.to_device(xb), ctx.alloc(m * n * 2)
     ctx.swiglu(xd, tg, tu, hd, m, mode="decode" if m == 1 else "prefill", dtype="bf16")
     h = ctx.to_host(hd, (m, n), np.uint16)
-    assert bits_equal(h, swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb), p4g, p4u, n))
+    assert bits_equal(h, swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb), p4g, p4u, n, ctx.epilogue))
     ctx.release(tg)
     ctx.release(tu)
 
@@ -119,9 +119,9 @@ def test_mlp_bf16(ctx, oracle):
     ctx.mlp(xd, tg, tu, td, yd, h=hd, dtype="bf16")
     h = ctx.to_host(hd, (1, f), np.uint16)
     y = ctx.to_host(yd, (1, hdim), np.uint16)
-    href = swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb), p4g, p4u, f)
+    href = swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb), p4g, p4u, f, ctx.epilogue)
     assert bits_equal(h, href)
-    yref = to_bf16(oracle, oracle.linear(oracle.bf16_bits_to_f32(href), p4d, hdim))
+    yref = to_bf16(oracle, oracle.linear(oracle.bf16_bits_to_f32(href), p4d, hdim, epilogue=ctx.epilogue))
     assert bits_equal(y, yref)
     # without a caller buffer for h the result is the same
     y2d = ctx.alloc(hdim * 2)
@@ -141,7 +141,7 @@ def test_lm_head_bf16_hidden(ctx, oracle):
     xd, ld, am = ctx.to_device(xb), ctx.alloc(v * 4), ctx.alloc(8)
     ctx.lm_head(xd, t, ld, 1, argmax=am, dtype="bf16")
     logits = ctx.to_host(ld, (1, v), np.float32)
-    ref = oracle.linear(oracle.bf16_bits_to_f32(xb), p4, v)
+    ref = oracle.linear(oracle.bf16_bits_to_f32(xb), p4, v, epilogue=ctx.epilogue)
     assert bits_equal(logits, ref)
     assert int(ctx.to_host(am, (1,), np.int64)[0]) == oracle.argmax(ref[0])
     ctx.release(t)
@@ -181,7 +181,7 @@ def test_linear_bf16_persistent_tiles(ctx, oracle):
     y = ctx.to_host(yd, (m, n), np.uint16)
     rows = _rows(rng, m)
     ref = oracle.linear(oracle.bf16_bits_to_f32(xb[rows]), p4, n, activation="silu",
-                        epilogue="fma")
+                        epilogue=ctx.epilogue)
     assert bits_equal(y[rows], to_bf16(oracle, ref))
     ctx.release(t)
 
@@ -197,7 +197,7 @@ def test_swiglu_bf16_persistent_tiles(ctx, oracle):
     ctx.swiglu(xd, tg, tu, hd, m, mode="prefill", dtype="bf16")
     h = ctx.to_host(hd, (m, n), np.uint16)
     rows = _rows(rng, m)
-    ref = swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb[rows]), p4g, p4u, n)
+    ref = swiglu_ref_bf16(oracle, oracle.bf16_bits_to_f32(xb[rows]), p4g, p4u, n, ctx.epilogue)
     assert bits_equal(h[rows], ref)
     ctx.release(tg)
     ctx.release(tu)
@@ -220,6 +220,6 @@ def test_matmul_benchmark_all_ones_fixture(ctx, oracle, m, k):
     y = ctx.to_host(yd, (m, n), np.uint16)
     assert np.all(oracle.bf16_bits_to_f32(y) == np.float32(k))  # first == K
     ref = oracle.linear(np.ones((m, k), np.float32), p4, n,
-                        epilogue="scalar" if m == 1 else "fma")
+                        epilogue=ctx.epilogue)
     assert bits_equal(y, to_bf16(oracle, ref))
     ctx.release(t)

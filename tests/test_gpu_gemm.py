@@ -34,21 +34,15 @@ def gemm(ctx, p4, n, k, x, activation="none"):
 @pytest.mark.parametrize("m,n,k", [(2, 136, 288), (19, 136, 288), (64, 264, 512),
                                    (130, 520, 1056), (256, 1024, 2560),
                                    (33, 136, 4096), (17, 264, 8864)])
-@pytest.mark.parametrize("epi", ["fma", "scalar"])
-def test_gemm_bitwise(ctx, oracle, m, n, k, epi):
+def test_gemm_bitwise(ctx, oracle, m, n, k):
     rng = np.random.default_rng(m * 7 + n + k)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[m // 2, 32:64] = 0.0
     p4 = oracle.pack_q8_0_p4(w)
-    ctx.set_gemm_epilogue(epi)
-    try:
-        y = gemm(ctx, p4, n, k, x)
-    finally:
-        ctx.set_gemm_epilogue("fma")
-    assert bits_equal(y, oracle.linear(x, p4, n, epilogue=epi))
-    other = "scalar" if epi == "fma" else "fma"
-    assert close(y, oracle.linear(x, p4, n, epilogue=other))
+    y = gemm(ctx, p4, n, k, x)
+    assert bits_equal(y, oracle.linear(x, p4, n, epilogue=ctx.epilogue))
+    assert close(y, oracle.linear(x, p4, n, epilogue=ctx.other_epilogue))
 
 
 def test_gemm_extreme_input_scales(ctx, oracle):
@@ -64,7 +58,7 @@ def test_gemm_extreme_input_scales(ctx, oracle):
     x[69, 2528:2560] *= np.float32(3e-39)
     x[33, :] = 0.0
     p4 = oracle.pack_q8_0_p4(w)
-    assert bits_equal(gemm(ctx, p4, n, k, x), oracle.linear(x, p4, n, epilogue="fma"))
+    assert bits_equal(gemm(ctx, p4, n, k, x), oracle.linear(x, p4, n, epilogue=ctx.epilogue))
 
 
 def test_gemm_exact_operand_boundaries(ctx, oracle):
@@ -93,7 +87,7 @@ def test_gemm_silu(ctx, oracle):
     x = rng.standard_normal((m, k)).astype(np.float32)
     p4 = oracle.pack_q8_0_p4(w)
     y = gemm(ctx, p4, n, k, x, activation="silu")
-    assert bits_equal(y, oracle.linear(x, p4, n, activation="silu", epilogue="fma"))
+    assert bits_equal(y, oracle.linear(x, p4, n, activation="silu", epilogue=ctx.epilogue))
 
 
 @pytest.mark.parametrize("m", [64, 256, 1024])
@@ -110,7 +104,7 @@ def test_gemm_config4_rows(ctx, oracle, m):
     ctx.linear(xd, t, yd, m, mode="prefill")
     y = ctx.to_host(yd, (m, n), np.float32)
     rows = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, 22)]))
-    ref = oracle.linear(x[rows], p4, n, epilogue="fma")
+    ref = oracle.linear(x[rows], p4, n, epilogue=ctx.epilogue)
     assert bits_equal(y[rows], ref)
     ctx.release(t)
 
@@ -127,7 +121,7 @@ def test_prefill_swiglu(ctx, oracle):
     xd, hd = ctx.to_device(x), ctx.alloc(m * n * 4)
     ctx.swiglu(xd, tg, tu, hd, m, mode="prefill")
     h = ctx.to_host(hd, (m, n), np.float32)
-    assert bits_equal(h, oracle.swiglu(x, pg, pu, n, epilogue="fma"))
+    assert bits_equal(h, oracle.swiglu(x, pg, pu, n, epilogue=ctx.epilogue))
     ctx.release(tg)
     ctx.release(tu)
 
@@ -152,7 +146,7 @@ def test_gemm_persistent_tiles(ctx, oracle, k):
     p4 = oracle.pack_q8_0_p4(w)
     y = gemm(ctx, p4, n, k, x)
     rows = _sampled_rows(rng, m)
-    assert bits_equal(y[rows], oracle.linear(x[rows], p4, n, epilogue="fma"))
+    assert bits_equal(y[rows], oracle.linear(x[rows], p4, n, epilogue=ctx.epilogue))
 
 
 def test_prefill_swiglu_persistent_tiles(ctx, oracle):
@@ -167,6 +161,6 @@ def test_prefill_swiglu_persistent_tiles(ctx, oracle):
     ctx.swiglu(xd, tg, tu, hd, m, mode="prefill")
     h = ctx.to_host(hd, (m, n), np.float32)
     rows = _sampled_rows(rng, m)
-    assert bits_equal(h[rows], oracle.swiglu(x[rows], pg, pu, n, epilogue="fma"))
+    assert bits_equal(h[rows], oracle.swiglu(x[rows], pg, pu, n, epilogue=ctx.epilogue))
     ctx.release(tg)
     ctx.release(tu)

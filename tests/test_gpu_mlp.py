@@ -32,20 +32,20 @@ def mlp_weights(ctx, oracle):
         ctx.release(x)
 
 
-def reference(oracle, p4, x, dtype):
+def reference(oracle, p4, x, dtype, epi):
     if dtype == "f32":
-        h = oracle.swiglu(x, p4[0], p4[1], FFN, colpar=True)
-        return h, oracle.linear(h, p4[2], HIDDEN, colpar=True)
+        h = oracle.swiglu(x, p4[0], p4[1], FFN, colpar=True, epilogue=epi)
+        return h, oracle.linear(h, p4[2], HIDDEN, colpar=True, epilogue=epi)
     # bf16 tensors: each linear rounded to bf16 before the bf16 multiply,
     # then the down linear of the bf16 h, rounded to bf16
     xf = oracle.bf16_bits_to_f32(x)
-    g = oracle.linear(xf, p4[0], FFN, activation="silu", colpar=True)
-    u = oracle.linear(xf, p4[1], FFN, colpar=True)
+    g = oracle.linear(xf, p4[0], FFN, activation="silu", colpar=True, epilogue=epi)
+    u = oracle.linear(xf, p4[1], FFN, colpar=True, epilogue=epi)
     gs = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(g))
     ub = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(u))
     h = oracle.f32_to_bf16_bits((gs * ub).astype(np.float32))
     y = oracle.f32_to_bf16_bits(
-        oracle.linear(oracle.bf16_bits_to_f32(h), p4[2], HIDDEN, colpar=True))
+        oracle.linear(oracle.bf16_bits_to_f32(h), p4[2], HIDDEN, colpar=True, epilogue=epi))
     return h, y
 
 
@@ -63,7 +63,7 @@ def test_mlp_consecutive_calls(ctx, oracle, mlp_weights, dtype):
         y1, y2 = ctx.alloc(HIDDEN * esz), ctx.alloc(HIDDEN * esz)
         ctx.mlp(xd, tg, tu, td, y1, h=hd, dtype=dtype)
         ctx.mlp(xd, tg, tu, td, y2, dtype=dtype)  # the context's h
-        h_ref, y_ref = reference(oracle, p4, x, dtype)
+        h_ref, y_ref = reference(oracle, p4, x, dtype, ctx.epilogue)
         assert bits_equal(ctx.to_host(hd, (1, FFN), et), h_ref), trial
         assert bits_equal(ctx.to_host(y1, (1, HIDDEN), et), y_ref), trial
         assert bits_equal(ctx.to_host(y2, (1, HIDDEN), et), y_ref), trial
@@ -77,7 +77,7 @@ def test_mlp_back_to_back(ctx, oracle, mlp_weights):
     yds = [ctx.alloc(HIDDEN * 4) for _ in range(24)]
     for i, yd in enumerate(yds):
         ctx.mlp(xds[i % 3], tg, tu, td, yd)
-    refs = [reference(oracle, p4, x, "f32")[1] for x in xs]
+    refs = [reference(oracle, p4, x, "f32", ctx.epilogue)[1] for x in xs]
     for i, yd in enumerate(yds):
         assert bits_equal(ctx.to_host(yd, (1, HIDDEN), np.float32), refs[i % 3]), i
     assert ctx.check_flag() == 0
@@ -97,7 +97,7 @@ def test_mlp_in_a_captured_graph(ctx, oracle, mlp_weights, q8):
                                                 x.nbytes) == 0
             ctx.graph_launch(g)
             y = ctx.to_host(yd, (1, HIDDEN), np.float32)
-            assert bits_equal(y, reference(oracle, p4, x, "f32")[1]), rep
+            assert bits_equal(y, reference(oracle, p4, x, "f32", ctx.epilogue)[1]), rep
             ye = ctx.alloc(HIDDEN * 4)  # eager work between replays
             ctx.mlp(xd, tg, tu, td, ye)
             assert bits_equal(ctx.to_host(ye, (1, HIDDEN), np.float32), y), rep
@@ -109,14 +109,14 @@ def test_mlp_in_a_captured_graph(ctx, oracle, mlp_weights, q8):
 @pytest.mark.parametrize("mode,dtype", [("prefill", "f32"), ("decode", "f32"),
                                         ("prefill", "bf16"), ("decode", "bf16")])
 def test_mlp_several_rows(ctx, oracle, mlp_weights, mode, dtype):
-    # M = 24: the SwiGLU GEMMs and the down GEMM, prefill with the FMA
-    # epilogue, decode with the scalar one; equal to llmcp_q8_swiglu then
-    # llmcp_q8_linear and to the oracle, with and without a caller h
+    # M = 24: the SwiGLU GEMMs and the down GEMM with the platform's
+    # epilogue in either mode; equal to llmcp_q8_swiglu then llmcp_q8_linear
+    # and to the oracle, with and without a caller h
     p4, (tg, tu, td) = mlp_weights
     m = 24
     rng = np.random.default_rng(12 if dtype == "f32" else 13)
     x = rng.standard_normal((m, HIDDEN)).astype(np.float32)
-    epi = "fma" if mode == "prefill" else "scalar"
+    epi = ctx.epilogue
     esz, et = (4, np.float32) if dtype == "f32" else (2, np.uint16)
     if dtype == "f32":
         xh = x

@@ -1,11 +1,13 @@
 """GPU parity of the HIP path against the CPU oracle, through the C ABI.
 
 Bars: integer/byte/index work bit-exact (packed bytes, Q8_1 activations,
-per-block int32 dots, argmax id, embedding values).  f32 outputs: the GEMV
-keeps the reference scalar path's block order (Q8Scalar.cpp:192-199), so it
-is compared bit for bit with the oracle's scalar epilogue and, within the
-north-star tolerance (max relative error 1e-5 or absolute 1e-4), with the
-SDOT-path fma epilogue (Q8Decode.cpp:192-203).
+per-block int32 dots, argmax id, embedding values).  f32 outputs: every
+path keeps the reference's block order with the selected platform's
+epilogue -- fma on aarch64 (Q8Decode.cpp:192-203), mul+add on x86
+(Q8Scalar.cpp:192-199) -- so it is compared bit for bit with the oracle's
+matching epilogue and, within the north-star tolerance (max relative error
+1e-5 or absolute 1e-4), with the other one.  The session context runs every
+test on both platforms (tests/conftest.py).
 """
 import os
 
@@ -56,8 +58,9 @@ def test_golden_fixture_rows(ctx, oracle):
         yd = ctx.alloc(n * 4)
         ctx.linear(xd, wt, yd, 1)
         y = ctx.to_host(yd, (1, n), np.float32)
-        assert bits_equal(y, z["y_scalar"][r:r + 1])
-        assert close(y, z["y_fma"][r:r + 1])
+        same, other = ("y_fma", "y_scalar") if ctx.epilogue == "fma" else ("y_scalar", "y_fma")
+        assert bits_equal(y, z[same][r:r + 1])
+        assert close(y, z[other][r:r + 1])
     ctx.release(wt)
 
 
@@ -72,9 +75,9 @@ def test_gemv_matches_scalar_reference_bitwise(ctx, oracle, k):
     w = weights(rng, n, k)
     x = rng.standard_normal((1, k)).astype(np.float32)
     y, p4 = run_linear(ctx, oracle, w, x)
-    ref = oracle.linear(x, p4, n, epilogue="scalar")
+    ref = oracle.linear(x, p4, n, epilogue=ctx.epilogue)
     assert bits_equal(y, ref), np.max(np.abs(y - ref))
-    assert close(y, oracle.linear(x, p4, n, epilogue="fma"))
+    assert close(y, oracle.linear(x, p4, n, epilogue=ctx.other_epilogue))
 
 
 # Input rows whose blocks have extreme scales: subnormal (the reciprocal's
@@ -95,7 +98,7 @@ def test_gemv_extreme_input_scales(ctx, oracle, k):
     x[0, 192:224] = 0.0
     x[0, k - 32:] *= np.float32(3e-39)
     y, p4 = run_linear(ctx, oracle, w, x)
-    assert bits_equal(y, oracle.linear(x, p4, n, epilogue="scalar"))
+    assert bits_equal(y, oracle.linear(x, p4, n, epilogue=ctx.epilogue))
 
 
 def test_gemv_exact_operands(ctx, oracle):
@@ -124,7 +127,7 @@ def test_gemv_silu_activation(ctx, oracle):
     w = weights(rng, 512, 2560)
     x = rng.standard_normal((1, 2560)).astype(np.float32)
     y, p4 = run_linear(ctx, oracle, w, x, activation="silu")
-    assert bits_equal(y, oracle.linear(x, p4, 512, activation="silu"))
+    assert bits_equal(y, oracle.linear(x, p4, 512, activation="silu", epilogue=ctx.epilogue))
 
 
 def test_prefill_single_row_uses_same_math(ctx, oracle):
@@ -132,13 +135,15 @@ def test_prefill_single_row_uses_same_math(ctx, oracle):
     w = weights(rng, 128, 1024)
     x = rng.standard_normal((1, 1024)).astype(np.float32)
     y, p4 = run_linear(ctx, oracle, w, x, mode="prefill")
-    assert bits_equal(y, oracle.linear(x, p4, 128))
+    assert bits_equal(y, oracle.linear(x, p4, 128, epilogue=ctx.epilogue))
 
 
-def test_decode_several_rows_use_the_scalar_epilogue(ctx, oracle, q8):
-    # The reference's decode emitter takes any M (Q8Decode.cpp:236-256); on
-    # x86 it lowers to the scalar path, so decode rows use the scalar
-    # epilogue even while the prefill GEMM is set to FMA (the default).
+def test_decode_and_prefill_rows_share_the_platform_epilogue(ctx, oracle, q8):
+    # The reference's decode emitter takes any M (Q8Decode.cpp:236-256) and
+    # computes the same per-block epilogue as its prefill GEMM on one
+    # platform (fma on aarch64, the scalar path's mul+add for every mode on
+    # x86), so decode and prefill rows agree bit for bit with the platform's
+    # oracle epilogue.
     rng = np.random.default_rng(9)
     for m, n, k in ((2, 64, 256), (37, 264, 2560), (70, 1032, 9216)):
         w = weights(rng, n, k)
@@ -146,12 +151,12 @@ def test_decode_several_rows_use_the_scalar_epilogue(ctx, oracle, q8):
         p4 = oracle.pack_q8_0_p4(w)
         t = ctx.upload_p4(p4, n, k)
         xd, yd = ctx.to_device(x), ctx.alloc(m * n * 4)
-        ctx.linear(xd, t, yd, m, mode="decode")
-        y = ctx.to_host(yd, (m, n), np.float32)
-        assert bits_equal(y, oracle.linear(x, p4, n, epilogue="scalar")), (m, n, k)
-        ctx.linear(xd, t, yd, m, mode="prefill")
-        assert bits_equal(ctx.to_host(yd, (m, n), np.float32),
-                          oracle.linear(x, p4, n, epilogue="fma")), (m, n, k)
+        ref = oracle.linear(x, p4, n, epilogue=ctx.epilogue)
+        for mode in ("decode", "prefill"):
+            ctx.linear(xd, t, yd, m, mode=mode)
+            y = ctx.to_host(yd, (m, n), np.float32)
+            assert bits_equal(y, ref), (m, n, k, mode)
+            assert close(y, oracle.linear(x, p4, n, epilogue=ctx.other_epilogue))
         ctx.release(t)
 
 
@@ -175,7 +180,7 @@ def test_swiglu_bitwise(ctx, oracle):
     xd, hd = ctx.to_device(x), ctx.alloc(n * 4)
     ctx.swiglu(xd, tg, tu, hd, 1)
     h = ctx.to_host(hd, (1, n), np.float32)
-    ref = oracle.swiglu(x, pg, pu, n, colpar=True)
+    ref = oracle.swiglu(x, pg, pu, n, colpar=True, epilogue=ctx.epilogue)
     assert bits_equal(h, ref)
     ctx.release(tg)
     ctx.release(tu)
@@ -194,8 +199,8 @@ def test_decode_mlp_end_to_end(ctx, oracle):
     ctx.swiglu(xd, tg, tu, hd, 1)
     ctx.linear(hd, td, yd, 1)
     y = ctx.to_host(yd, (1, hidden), np.float32)
-    h_ref = oracle.swiglu(x, pg, pu, ffn, colpar=True)
-    y_ref = oracle.linear(h_ref, pd, hidden, colpar=True)
+    h_ref = oracle.swiglu(x, pg, pu, ffn, colpar=True, epilogue=ctx.epilogue)
+    y_ref = oracle.linear(h_ref, pd, hidden, colpar=True, epilogue=ctx.epilogue)
     assert bits_equal(y, y_ref)
     for t in (tg, tu, td):
         ctx.release(t)
@@ -217,8 +222,8 @@ def test_fused_mlp_matches_separate_ops(ctx, oracle):
             ctx.mlp(xd, tg, tu, td, yd, h=hd)
             h = ctx.to_host(hd, (1, ffn), np.float32)
             y = ctx.to_host(yd, (1, hidden), np.float32)
-            h_ref = oracle.swiglu(x, pg, pu, ffn, colpar=True)
-            y_ref = oracle.linear(h_ref, pd, hidden, colpar=True)
+            h_ref = oracle.swiglu(x, pg, pu, ffn, colpar=True, epilogue=ctx.epilogue)
+            y_ref = oracle.linear(h_ref, pd, hidden, colpar=True, epilogue=ctx.epilogue)
             assert bits_equal(h, h_ref)
             assert bits_equal(y, y_ref), (hidden, ffn, trial)
             y2d = ctx.alloc(hidden * 4)
@@ -236,7 +241,7 @@ def test_wide_output_uses_prequantized_input(ctx, oracle, q8):
     w = weights(rng, n, k)
     x = rng.standard_normal((1, k)).astype(np.float32)
     y, p4 = run_linear(ctx, oracle, w, x)
-    assert bits_equal(y, oracle.linear(x, p4, n))
+    assert bits_equal(y, oracle.linear(x, p4, n, epilogue=ctx.epilogue))
     n2 = 264
     w2 = weights(rng, n2, k)
     p42 = oracle.pack_q8_0_p4(w2)
@@ -244,7 +249,7 @@ def test_wide_output_uses_prequantized_input(ctx, oracle, q8):
     xd = ctx.to_device(np.concatenate([[0.0], x.ravel()]).astype(np.float32))
     yd = ctx.alloc(n2 * 4)
     ctx.linear(xd.ptr + 4, t, yd, 1)
-    assert bits_equal(ctx.to_host(yd, (1, n2), np.float32), oracle.linear(x, p42, n2))
+    assert bits_equal(ctx.to_host(yd, (1, n2), np.float32), oracle.linear(x, p42, n2, epilogue=ctx.epilogue))
     ctx.release(t)
 
 
@@ -254,7 +259,7 @@ def test_lm_head_argmax_and_ties(ctx, oracle):
     w = weights(rng, v, k)
     x = rng.standard_normal((1, k)).astype(np.float32)
     p4 = oracle.pack_q8_0_p4(w)
-    ref = oracle.linear(x, p4, v)
+    ref = oracle.linear(x, p4, v, epilogue=ctx.epilogue)
     best = int(np.argmax(ref))
     # Duplicate the winning row at a lower and a higher index: equal logits,
     # the first maximum must win (std::max_element).
@@ -270,7 +275,7 @@ def test_lm_head_argmax_and_ties(ctx, oracle):
             ctx.lm_head(xd, t, ld, 1, argmax=am)
             logits = ctx.to_host(ld, (1, v), np.float32)
             idx = int(ctx.to_host(am, (1,), np.int64)[0])
-            assert bits_equal(logits, oracle.linear(x, p4, v))
+            assert bits_equal(logits, oracle.linear(x, p4, v, epilogue=ctx.epilogue))
             assert idx == oracle.argmax(logits) == expect
         ctx.release(t)
 
@@ -287,7 +292,7 @@ def test_lm_head_argmax_back_to_back(ctx, oracle):
     x1 = rng.standard_normal((1, k)).astype(np.float32)
     x2 = (-0.01 * x1).astype(np.float32)
     xs = [ctx.to_device(x1), ctx.to_device(x2)]
-    expect = [oracle.argmax(oracle.linear(x, p4, v)) for x in (x1, x2)]
+    expect = [oracle.argmax(oracle.linear(x, p4, v, epilogue=ctx.epilogue)) for x in (x1, x2)]
     assert expect[0] != expect[1]
     ld = ctx.alloc(v * 4)
     ams = [ctx.alloc(8) for _ in range(6)]
@@ -312,7 +317,7 @@ def test_device_resident_token_loop(ctx, oracle):
     chain = [7]
     for _ in range(6):
         x = oracle.embedding(np.array(chain[-1:], np.int64), pe, k)
-        chain.append(int(oracle.argmax(oracle.linear(x, pw, v))))
+        chain.append(int(oracle.argmax(oracle.linear(x, pw, v, epilogue=ctx.epilogue))))
     assert len(set(chain)) == len(chain)
     xd, ld = ctx.alloc(k * 4), ctx.alloc(v * 4)
     ids = [ctx.to_device(np.array([chain[0]], np.int64))]
@@ -348,7 +353,7 @@ def test_lm_head_full_vocab(ctx, oracle):
     ctx.lm_head(xd, t, ld, 1, argmax=am)
     logits = ctx.to_host(ld, (1, v), np.float32)
     idx = int(ctx.to_host(am, (1,), np.int64)[0])
-    ref = oracle.linear(x, p4, v, colpar=True)
+    ref = oracle.linear(x, p4, v, colpar=True, epilogue=ctx.epilogue)
     assert bits_equal(logits, ref)
     top2 = np.sort(ref.ravel())[-2:]
     assert top2[1] - top2[0] > 1e-4  # the id is meaningful at tolerance level
@@ -467,7 +472,7 @@ def test_arena_upload_and_descriptor_translation(ctx, oracle, q8, tmp_path):
         x = rng.standard_normal((1, k)).astype(np.float32)
         xd, yd = ctx.to_device(x), ctx.alloc(n * 4)
         ctx.linear(xd, wt, yd, 1)
-        assert bits_equal(ctx.to_host(yd, (1, n), np.float32), oracle.linear(x, p4, n))
+        assert bits_equal(ctx.to_host(yd, (1, n), np.float32), oracle.linear(x, p4, n, epilogue=ctx.epilogue))
         ctx.release(wt)
 
 
@@ -488,6 +493,6 @@ def test_mlir_ciface_entry_uses_default_context(ctx, oracle, q8):
     assert rc == 0
     ctx.sync()
     assert bits_equal(ctx.to_host(yd, (1, 64), np.float32),
-                      oracle.linear(x, p4, 64, activation="silu"))
+                      oracle.linear(x, p4, 64, activation="silu", epilogue=ctx.epilogue))
     L.llmcp_q8_set_default_ctx(None)
     ctx.release(t)

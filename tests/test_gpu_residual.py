@@ -19,8 +19,7 @@ def to_bf16(oracle, x):
     return oracle.f32_to_bf16_bits(np.asarray(x, np.float32))
 
 
-def reference(oracle, x, p4, n, r, dtype):
-    epi = "scalar" if x.shape[0] == 1 else "fma"
+def reference(oracle, x, p4, n, r, dtype, epi):
     lin = oracle.linear(x, p4, n, epilogue=epi)
     if dtype == "f32":
         return (lin + r).astype(np.float32)
@@ -50,7 +49,7 @@ def test_linear_add(ctx, oracle, m, n, k, dtype):
     rows = np.arange(m) if m <= 64 else np.unique(
         np.concatenate([[0, m - 1], rng.integers(0, m, 30)]))
     xf = oracle.bf16_bits_to_f32(x[rows]) if dtype == "bf16" else x[rows]
-    assert bits_equal(y[rows], reference(oracle, xf, p4, n, r[rows], dtype))
+    assert bits_equal(y[rows], reference(oracle, xf, p4, n, r[rows], dtype, ctx.epilogue))
     ctx.release(t)
 
 
@@ -68,7 +67,7 @@ def test_linear_add_in_place(ctx, oracle, m):
     xd, rd = ctx.to_device(x), ctx.to_device(r)
     ctx.linear_add(xd, t, rd, rd, m, mode="decode" if m == 1 else "prefill")
     assert bits_equal(ctx.to_host(rd, (m, n), np.float32),
-                      reference(oracle, x, p4, n, r, "f32"))
+                      reference(oracle, x, p4, n, r, "f32", ctx.epilogue))
     ctx.release(t)
 
 

@@ -29,7 +29,8 @@ def test_two_contexts_on_two_threads(q8, oracle):
         w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
         p4 = oracle.pack_q8_0_p4(w)
         xs = [rng.standard_normal((1, k)).astype(np.float32) for _ in range(3)]
-        refs = [oracle.linear(x, p4, n, colpar=True) for x in xs]
+        # fresh contexts compute the default platform's (aarch64) fma epilogue
+        refs = [oracle.linear(x, p4, n, colpar=True, epilogue="fma") for x in xs]
         jobs.append((n, k, p4, xs, refs))
     errors, done = [], []
 
@@ -68,7 +69,7 @@ def test_caller_stream_is_adopted_and_ordered(ctx, oracle, q8):
     p4 = oracle.pack_q8_0_p4((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
     t = ctx.upload_p4(p4, n, k)
     x = rng.standard_normal((1, k)).astype(np.float32)
-    ref = oracle.linear(x, p4, n, colpar=True)
+    ref = oracle.linear(x, p4, n, colpar=True, epilogue=ctx.epilogue)
     xd = ctx.to_device(x)
     yd = ctx.to_device(np.full((1, n), np.nan, np.float32))
     stream = ctypes.c_void_p()

@@ -53,7 +53,7 @@ def test_random_linear_case(ctx, oracle, case):
     x = (rng.standard_normal((m, k)) * scale).astype(np.float32)
     if m > 2:
         x[m // 2] = 0.0  # an all-zero row: zero scales, zero dots
-    epi = "scalar" if m == 1 or mode == "decode" else "fma"
+    epi = ctx.epilogue
     t = ctx.upload_p4(p4, n, k)
     try:
         if dtype == "f32":

@@ -379,9 +379,21 @@ def test_activations_closed_form(oracle):
     assert np.allclose(sig, 1.0 / (1.0 + np.exp(-d)), rtol=4e-7, atol=1e-30)
     silu = oracle.silu(v)
     assert np.array_equal(silu, (v * sig).astype(np.float32))  # v * sigmoid(v)
+    # softplus = math.log1p(math.exp(v)) as the reference compiles it:
+    # --convert-math-to-llvm (llmcp-compile.cpp:186) lowers log1p(y) to
+    # log(1 + y) with an f32 add.  Closed form: f64 log of the f32 sum.
     sp = oracle.softplus(v)
-    assert np.allclose(sp, np.log1p(np.exp(d)), rtol=4e-7, atol=1e-30)
-    # softplus overflows where f32 exp does (exp(89) = inf), like the
-    # reference's log1p(exp(v)) on f32
+    e32 = np.exp(d).astype(np.float32)
+    s32 = (np.float32(1.0) + e32).astype(np.float32)
+    assert np.allclose(sp, np.log(s32.astype(np.float64)), rtol=4e-7, atol=1e-30)
+    # where exp(v) < 2^-24 the f32 sum rounds to 1 and the result is 0 (a
+    # true log1p would return exp(v)); between, the sum keeps only the
+    # leading bits of exp(v)
+    tail = oracle.softplus(np.array([-20.0, -17.5, -16.0], np.float32))
+    assert tail[0] == 0.0 and tail[1] == 0.0
+    assert tail[2] == np.float32(np.log(np.float64(np.float32(1.0) + np.float32(np.exp(-16.0)))))
+    assert tail[2] != np.float32(np.log1p(np.exp(-16.0)))
+    # softplus overflows where f32 exp does (exp(89) = inf)
     assert np.isinf(oracle.softplus(np.array([89.0], np.float32))[0])
-    assert oracle.softplus(np.array([88.0], np.float32))[0] == np.float32(np.log1p(np.float32(np.exp(88.0))))
+    assert oracle.softplus(np.array([88.0], np.float32))[0] == np.float32(
+        np.log(np.float64(np.float32(1.0) + np.float32(np.exp(88.0)))))
