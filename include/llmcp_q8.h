@@ -286,6 +286,26 @@ int llmcp_q8_lm_head_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *hidden,
                           llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
                           int32_t execution_mode);
 
+/* Size of the per-GPU scratch array of llmcp_q8_lm_head_noalloc: 16 KiB of
+ * argmax slots, the rest for the quantized hidden rows (at K = 2560 about
+ * 2800 rows; M = 1 needs 2880 bytes). */
+#define LLMCP_Q8_STATIC_SCRATCH_BYTES (8u << 20)
+
+/* llmcp_q8_lm_head that allocates nothing.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Results equal llmcp_q8_lm_head's.  Its scratch (the quantized
+ * hidden rows and the argmax slots) is one file-scope device array of
+ * LLMCP_Q8_STATIC_SCRATCH_BYTES that each GPU holds until the process ends,
+ * set up when the first context on that GPU is created; a hidden state that
+ * needs more returns LLMCP_Q8_DECLINED.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (two contexts, two streams) race. */
+int llmcp_q8_lm_head_noalloc(llmcp_q8_ctx *ctx,
+                             const llmcp_memref_f32_2d *hidden,
+                             const llmcp_memref_i8_1d *table,
+                             llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
+                             int32_t execution_mode);
+
 /* llmcp.embedding with weight_format q8_0_p4 (emitQ8PackedEmbedding,
  * LowerToLinalg.cpp:435-531): out[t, c] = f32(q(token_t, c)) * f32(d).
  * Tokens outside [0, rows) produce a zero row and set the context's

@@ -75,7 +75,7 @@ EXPORTS = [
     "llmcp_q8_graph_launch", "llmcp_q8_graph_destroy",
     "llmcp_q8_device_bytes", "llmcp_q8_selftest_quantizer", "llmcp_q8_selftest_exp",
     "llmcp_q8_linear_bf16", "llmcp_q8_swiglu_bf16", "llmcp_q8_mlp_bf16",
-    "llmcp_q8_lm_head_bf16", "llmcp_q8_embedding_bf16",
+    "llmcp_q8_lm_head_bf16", "llmcp_q8_embedding_bf16", "llmcp_q8_lm_head_noalloc",
     "_mlir_ciface_llmcp_q8_linear_bf16", "_mlir_ciface_llmcp_q8_swiglu_bf16",
     "_mlir_ciface_llmcp_q8_lm_head_bf16", "_mlir_ciface_llmcp_q8_embedding_bf16",
     "llmcp_q8_linear_add", "llmcp_q8_linear_add_bf16",
@@ -149,6 +149,7 @@ def lib():
         "llmcp_q8_swiglu_bf16": (I, [P, P, P, P, P, I32]),
         "llmcp_q8_mlp_bf16": (I, [P, P, P, P, P, P, P, I32]),
         "llmcp_q8_lm_head_bf16": (I, [P, P, P, P, P, I32]),
+        "llmcp_q8_lm_head_noalloc": (I, [P, P, P, P, P, I32]),
         "llmcp_q8_embedding_bf16": (I, [P, P, P, P]),
         "_mlir_ciface_llmcp_q8_linear_bf16": (I32, [P, P, P, I32, I32]),
         "_mlir_ciface_llmcp_q8_swiglu_bf16": (I32, [P, P, P, P, I32]),

@@ -248,6 +248,59 @@ int reserve(llmcp_q8_ctx *ctx, Workspace &ws, uint64_t qa_bytes,
   return rc;
 }
 
+// ------------------------------------------------ fixed scratch (no alloc) --
+// The device scratch of llmcp_q8_lm_head_noalloc: the argmax slots, then the
+// quantized input rows' f32 scales and int8 values.  Each GPU the library
+// runs on holds its own copy for the life of the process; host code reaches
+// it only through the address hipGetSymbolAddress returns for that device
+// (g_scratch_ptr), never through the array's name.
+constexpr uint64_t kSlotsBytes = (uint64_t)kArgmaxSlots * 8u;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices];
+bool g_scratch_dirty[kMaxDevices];  // the slots may hold a failed call's keys
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[LLMCP_Q8_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+// Resolves this device's copy of `scratch` (the device must be current) and
+// zeroes its argmax slots with the reduce kernel in clearing mode (a kernel,
+// not a memset).  Once per device; called when a context is created.
+int setup_static_scratch(int device, hipStream_t stream) {
+  if (device >= kMaxDevices)
+    return fail(LLMCP_Q8_EINVAL, "device %d beyond the library's %d", device,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device]) return LLMCP_Q8_OK;
+  void *p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  e = launch_argmax_reduce((unsigned long long *)p, nullptr, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "clearing the fixed scratch");
+  g_scratch_ptr[device] = p;
+  return LLMCP_Q8_OK;
+}
+
+// The fixed scratch as a Workspace: slots first, then scales and values in
+// the ratio the quantized rows use them (4 B of scale per 32 values).
+Workspace static_workspace(int device) {
+  Workspace ws;
+  unsigned char *base = (unsigned char *)g_scratch_ptr[device];
+  const uint64_t rest = (uint64_t)LLMCP_Q8_STATIC_SCRATCH_BYTES - kSlotsBytes;
+  ws.keys = (unsigned long long *)base;
+  ws.sa_bytes = rest / 9 / 256 * 256;
+  ws.sa = (float *)(base + kSlotsBytes);
+  ws.qa = (int8_t *)(base + kSlotsBytes + ws.sa_bytes);
+  ws.qa_bytes = rest - ws.sa_bytes;
+  ws.keys_dirty = &g_scratch_dirty[device];
+  ws.fixed = true;
+  return ws;
+}
+
 // The argmax slots, allocated and zeroed once (before any graph capture).
 int ensure_argmax_slots(llmcp_q8_ctx *ctx) {
   if (ctx->keys) return LLMCP_Q8_OK;
@@ -492,6 +545,11 @@ int llmcp_q8_ctx_create(int device, llmcp_q8_ctx **out) {
         hipDeviceSynchronize() != hipSuccess) {
       llmcp_q8_ctx_destroy(ctx);
       return fail(LLMCP_Q8_EHIP, "context workspace init");
+    }
+    // the device's fixed scratch, for llmcp_q8_lm_head_noalloc
+    if ((rc = setup_static_scratch(device, ctx->stream))) {
+      llmcp_q8_ctx_destroy(ctx);
+      return rc;
     }
     *out = ctx;
     return LLMCP_Q8_OK;
@@ -1343,6 +1401,27 @@ int llmcp_q8_lm_head_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *hidden,
     if (!view_of(hidden, true, in) || !view_of(logits, false, out))
       return fail(LLMCP_Q8_DECLINED, kDenseMsg);
     return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode);
+  });
+}
+
+// llmcp_q8_lm_head with the device's fixed scratch in place of the
+// context's workspace: no allocation on any path (sizes beyond the scratch
+// are declined), so it may run under graph capture or where hipMalloc is
+// forbidden.
+int llmcp_q8_lm_head_noalloc(llmcp_q8_ctx *ctx,
+                             const llmcp_memref_f32_2d *hidden,
+                             const llmcp_memref_i8_1d *table,
+                             llmcp_memref_f32_2d *logits, int64_t *argmax_dev,
+                             int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    if (!view_of(hidden, false, in) || !view_of(logits, false, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    if (ctx->device >= kMaxDevices || !g_scratch_ptr[ctx->device])
+      return fail(LLMCP_Q8_EINVAL, "no fixed scratch on device %d", ctx->device);
+    const Workspace ws = static_workspace(ctx->device);
+    return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode, &ws);
   });
 }
 
