@@ -240,3 +240,30 @@ def test_arena_fuzz_numeric_extremes(q8, fuzz_arena, field, value):
         else:
             t[field] = value
     _inspect_outcome(q8, _rewrite_manifest(f, edit))
+
+
+def test_model_arena_layout_matches_the_reference_pack():
+    # WeightLayout::build restated for the 4B-class config: the reference's
+    # own packing of the real model reports 426 tensors and 4,469,519,936
+    # arena bytes (docs/int8-quantization.md:718-724).
+    from llmcp_amd import model_arena
+    entries, stride, groups, total = model_arena.layout()
+    assert len(entries) == 426
+    assert total == 4469519936
+    assert groups == 8 and stride % 64 == 0
+    assert sum(e["dtype"] == "Q8_0" for e in entries) == 249
+    offsets = [e["offset"] for e in entries]
+    assert offsets == sorted(offsets) and all(o % 64 == 0 for o in offsets)
+    assert entries[0]["name"] == "model.language_model.embed_tokens.weight"
+    assert entries[0]["dtype"] == "Q8_0" and entries[0]["size"] == 248320 * 2560 // 32 * 34
+
+
+def test_model_arena_image_validates(q8):
+    # a reduced model (4 layers, small vocab) built by the same code passes
+    # the host validator with every tensor and dtype counted
+    from llmcp_amd import model_arena
+    cfg = dict(model_arena.CONFIG_4B, layers=4, vocab=1024, intermediate=512)
+    image, entries = model_arena.build_image(cfg, seed=1)
+    q8n = sum(e["dtype"] == "Q8_0" for e in entries)
+    assert q8.arena_inspect(image) == (len(entries), q8n)
+    assert {e["dtype"] for e in entries} == {"Q8_0", "BF16", "F32"}
