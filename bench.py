@@ -4,16 +4,22 @@ Headline workload: the decode MLP at M=1 --
 gate and up Q8_0 projections 2560 -> 9216 with the fused silu(gate)*up
 epilogue, then the Q8_0 down projection 9216 -> 2560.  A step is one pass of
 that MLP over one synthetic input row, activation quantization included.
-Weights are N(0, 0.02) synthesized on the device and packed to q8_0_p4; a
-rotating pool of distinct weight copies larger than the 256 MB Infinity Cache
-keeps the timing on HBM.  Steps are replayed from a HIP graph so host launch
-cost stays out of the timed region.
+Weights are N(0, 0.02) synthesized on the device and packed to q8_0_p4; the
+steps cycle through distinct weight copies larger together than the 256 MB
+Infinity Cache, which keeps the timing on HBM.  The timed steps (exactly
+--steps of them, after exactly --warmup untimed ones) are replayed from one
+HIP graph, so host launch cost stays out of the timed region.  The
+arithmetic is the selected reference platform's (--platform, default the
+aarch64 SDOT paths' fma epilogue).
 
 `value` = whole-step algorithmic bytes / time (GB/s).  `roofline` = the fused
-gate/up GEMV (the dominant kernel) timed alone with HIP events on the
-library's stream.  `cpu_baseline` = the oracle's C restatement of the
-reference's x86 scalar Q8 path (row-parallel OpenMP, so 1 thread at M=1) on a
-bounded sample of the same workload.
+gate/up GEMV (the dominant kernel) timed alone the same way with HIP events
+on the library's stream.  `extra` = the other configs (config 1 GEMV, config
+3 lm_head + argmax and gather, config 4 GEMMs at M = 64/256/1024, config 5
+sequence at M = 1 and 1024, the real model's arena upload and decode step)
+and the one-time device repack of each tensor shape.  `cpu_baseline` = the
+oracle's C restatement of the reference's x86 scalar Q8 path on bounded
+samples of every config, with the host described.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -78,64 +84,61 @@ def bench_decode_mlp(ctx, q8, steps, warmup, hidden=2560, ffn=9216):
     copies = max(2, -(-int(1.6 * MALL_BYTES) // per_copy))
     log("decode_mlp: %d weight copies x %.1f MB" % (copies, per_copy / 1e6))
     pool = []
+    repack_ms = {}
     for c in range(copies):
         mats = []
         for i, (n, k) in enumerate([(ffn, hidden), (ffn, hidden), (hidden, ffn)]):
             p4d, _ = ctx.synthesize_p4(seed=1000 + 10 * c + i, rows=n, cols=k)
-            mats.append((ctx.register_device_p4(p4d, n, k), p4d))
+            w = ctx.register_device_p4(p4d, n, k, time_repack=(c == 0))
+            if c == 0:
+                repack_ms["%dx%d" % (n, k)] = round(w.repack_ms, 3)
+            mats.append((w, p4d))
         pool.append(mats)
     rng = np.random.default_rng(2560)
     x = rng.standard_normal((1, hidden)).astype(np.float32)
     xd, hd, yd = ctx.to_device(x), ctx.alloc(ffn * 4), ctx.alloc(hidden * 4)
 
-    def one_rotation():
-        for mats in pool:
-            ctx.mlp(xd, mats[0][0], mats[1][0], mats[2][0], yd, h=hd)
+    # Graphs of exactly n steps, cycling through the weight copies, so the
+    # timed region holds exactly `steps` steps (and the warmup `warmup`).
+    def mlp_steps(n):
+        return lambda: [ctx.mlp(xd, pool[i % copies][0][0], pool[i % copies][1][0],
+                                pool[i % copies][2][0], yd, h=hd) for i in range(n)]
 
-    def gateup_rotation():
-        for mats in pool:
-            ctx.swiglu(xd, mats[0][0], mats[1][0], hd, 1)
+    def gateup_steps(n):
+        return lambda: [ctx.swiglu(xd, pool[i % copies][0][0], pool[i % copies][1][0],
+                                   hd, 1) for i in range(n)]
 
-    def down_rotation():
-        for mats in pool:
-            ctx.linear(hd, mats[2][0], yd, 1)
-
-    # fixed cost of one kernel node in graph replay: a 32-element quantize
-    tq, ts = ctx.alloc(64), ctx.alloc(64)
-
-    def tiny_rotation():
-        for _ in pool:
-            ctx.quantize(xd, 1, 32, tq, ts)
+    def down_steps(n):
+        return lambda: [ctx.linear(hd, pool[i % copies][2][0], yd, 1) for i in range(n)]
 
     timer = Timer(ctx)
-    g_step = graph_of(ctx, one_rotation)
-    g_gu = graph_of(ctx, gateup_rotation)
-    rounds_w = max(1, -(-warmup // copies))
-    rounds = max(1, -(-steps // copies))
-    run_graph(ctx, timer, g_step, rounds_w)
-    ms = run_graph(ctx, timer, g_step, rounds)
-    n_steps = rounds * copies
-    step_bytes = (per_copy + hidden * 4 + 2 * ffn * 4 + hidden * 4)
-    gb_s = step_bytes * n_steps / (ms * 1e-3) / 1e9
 
-    run_graph(ctx, timer, g_gu, rounds_w)
-    ms_gu = run_graph(ctx, timer, g_gu, rounds)
-    gu_launch_us = ms_gu * 1e3 / (rounds * copies)
-    g_down, g_tiny = graph_of(ctx, down_rotation), graph_of(ctx, tiny_rotation)
-    run_graph(ctx, timer, g_down, rounds_w)
-    down_launch_us = run_graph(ctx, timer, g_down, rounds) * 1e3 / (rounds * copies)
-    run_graph(ctx, timer, g_tiny, rounds_w)
-    tiny_launch_us = run_graph(ctx, timer, g_tiny, rounds) * 1e3 / (rounds * copies)
+    def timed(make):
+        if warmup:
+            gw = graph_of(ctx, make(warmup))
+            run_graph(ctx, timer, gw, 1)
+            ctx.graph_destroy(gw)
+        g = graph_of(ctx, make(steps))
+        ms = run_graph(ctx, timer, g, 1)
+        ctx.graph_destroy(g)
+        return ms
+
+    ms = timed(mlp_steps)
+    step_bytes = (per_copy + hidden * 4 + 2 * ffn * 4 + hidden * 4)
+    gb_s = step_bytes * steps / (ms * 1e-3) / 1e9
+    gu_launch_us = timed(gateup_steps) * 1e3 / steps
+    down_launch_us = timed(down_steps) * 1e3 / steps
     gu_bytes = 2 * p4_bytes(ffn, hidden) + hidden * 4 + ffn * 4
     gu_gbs = gu_bytes / (gu_launch_us * 1e-6) / 1e9
+    down_bytes = p4_bytes(hidden, ffn) + ffn * 4 + hidden * 4
 
     # keep one copy's packed bytes for the CPU baseline
     host = [ctx.to_host(m[1], (m[1].nbytes,), np.uint8) for m in pool[0]]
-    res = dict(ms=ms, steps=n_steps, gb_s=gb_s, step_bytes=step_bytes,
+    res = dict(ms=ms, steps=steps, gb_s=gb_s, step_bytes=step_bytes,
                copies=copies, pool_bytes=copies * per_copy,
                gu_launch_us=gu_launch_us, gu_bytes=gu_bytes, gu_gbs=gu_gbs,
-               down_launch_us=down_launch_us, tiny_launch_us=tiny_launch_us,
-               x=x, host_p4=host, hidden=hidden, ffn=ffn)
+               down_launch_us=down_launch_us, down_bytes=down_bytes,
+               repack_ms=repack_ms, x=x, host_p4=host, hidden=hidden, ffn=ffn)
     for mats in pool:
         for w, p4d in mats:
             ctx.release(w)
@@ -152,7 +155,8 @@ def bench_gemv(ctx, n, k, iters=200, residual=False):
     ws = []
     for c in range(copies):
         p4d, _ = ctx.synthesize_p4(seed=5000 + c, rows=n, cols=k)
-        ws.append((ctx.register_device_p4(p4d, n, k), p4d))
+        ws.append((ctx.register_device_p4(p4d, n, k, time_repack=(c == 0)), p4d))
+    repack_ms = ws[0][0].repack_ms
     x = np.random.default_rng(k).standard_normal((1, k)).astype(np.float32)
     xd, yd = ctx.to_device(x), ctx.alloc(n * 4)
 
@@ -170,17 +174,19 @@ def bench_gemv(ctx, n, k, iters=200, residual=False):
     ms = run_graph(ctx, timer, g, rounds)
     us = ms * 1e3 / (rounds * copies)
     nbytes = per + k * 4 + n * 4
+    host_p4 = ctx.to_host(ws[0][1], (per,), np.uint8)
     for w, p4d in ws:
         ctx.release(w)
         p4d.free()
-    return dict(us=us, gb_s=nbytes / (us * 1e-6) / 1e9, bytes=nbytes, copies=copies)
+    return dict(us=us, gb_s=nbytes / (us * 1e-6) / 1e9, bytes=nbytes, copies=copies,
+                repack_ms=repack_ms, p4=host_p4)
 
 
 def bench_lm_head(ctx, v=248320, k=2560, iters=20):
     """Config 3: tied lm_head with fused argmax, plus the embedding gather."""
     per = p4_bytes(v, k)
     p4d, _ = ctx.synthesize_p4(seed=77, rows=v, cols=k)
-    w = ctx.register_device_p4(p4d, v, k)
+    w = ctx.register_device_p4(p4d, v, k, time_repack=True)
     x = np.random.default_rng(v).standard_normal((1, k)).astype(np.float32)
     xd, ld, am = ctx.to_device(x), ctx.alloc(v * 4), ctx.alloc(8)
     timer = Timer(ctx)
@@ -200,10 +206,12 @@ def bench_lm_head(ctx, v=248320, k=2560, iters=20):
     ms2 = run_graph(ctx, timer, g2, iters)
     us2 = ms2 * 1e3 / (iters * reps)
     gather_bytes = 1024 * k * 34 // 32 + 1024 * k * 4
+    host_p4 = ctx.to_host(p4d, (per,), np.uint8)
     ctx.release(w)
     p4d.free()
     return dict(us=us, gb_s=nbytes / (us * 1e-6) / 1e9, bytes=nbytes,
-                gather_us=us2, gather_gb_s=gather_bytes / (us2 * 1e-6) / 1e9)
+                gather_us=us2, gather_gb_s=gather_bytes / (us2 * 1e-6) / 1e9,
+                repack_ms=w.repack_ms, p4=host_p4, x=x)
 
 
 def bench_gemm(ctx, m, n=9216, k=2560, iters=30):
@@ -262,14 +270,17 @@ def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320
         ws = {}
         for j, (name, n, k) in enumerate(shapes):
             p4d, _ = ctx.synthesize_p4(seed=100000 + 16 * li + j, rows=n, cols=k)
-            ws[name] = (ctx.register_device_p4(p4d, n, k), p4d)
+            ws[name] = (ctx.register_device_p4(p4d, n, k, time_repack=(li == 0)), p4d)
             total += p4_bytes(n, k)
         layer.append(ws)
+    qkv_repack_ms = layer[0]["qkv"][0].repack_ms
+    qkv_p4 = ctx.to_host(layer[0]["qkv"][1], (p4_bytes(qkv, hidden),), np.uint8)
     p4d, _ = ctx.synthesize_p4(seed=99, rows=vocab, cols=hidden)
     head = (ctx.register_device_p4(p4d, vocab, hidden), p4d)
     total += p4_bytes(vocab, hidden)
     rng = np.random.default_rng(5)
-    out = {"weight_bytes": total, "linears": layers * len(shapes) + 1}
+    out = {"weight_bytes": total, "linears": layers * len(shapes) + 1,
+           "_qkv_repack_ms": qkv_repack_ms, "_qkv_p4": qkv_p4}
     timer = Timer(ctx)
     for m, mode in ((1, "decode"), (1024, "prefill")):
         x = ctx.to_device(rng.standard_normal((m, hidden)).astype(np.float32))
@@ -309,59 +320,55 @@ def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320
     return out
 
 
-def bench_arena(ctx, q8, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320):
-    """The whole config-5 model from one LLMCPWGT arena file, as the AOT
-    runtime loads it: written once (synthetic weights of the sequence's
-    shapes), mapped, uploaded by llmcp_q8_upload_arena (validation, host ->
-    HBM copies, device repack), then one decode step run through weight
-    descriptors that point into the mapping."""
-    import struct
+def bench_arena(ctx, q8):
+    """The real 4B-class model's arena (426 tensors: Q8_0 matmul weights and
+    tied table, BF16/F32 norms and conv/gate parameters; 4.47 GB laid out as
+    WeightLayout::build does), written to a file, mapped and uploaded whole
+    by llmcp_q8_upload_arena (validation, host -> HBM copies, device repack)
+    as the AOT runtime would; then one decode step of all 249 Q8_0 linears
+    (every layer's projections and MLP, the last-row lm_head with argmax)
+    through weight descriptors that point into the mapping."""
     import tempfile
-    shapes = [("gate", ffn, hidden), ("up", ffn, hidden), ("down", hidden, ffn),
-              ("qkv", qkv, hidden), ("o", hidden, hidden), ("a", hidden, hidden),
-              ("b", hidden, hidden)]
-    tensors = []
-    for li in range(layers):
-        for j, (name, n, k) in enumerate(shapes):
-            p4d, _ = ctx.synthesize_p4(seed=200000 + 16 * li + j, rows=n, cols=k)
-            tensors.append(("model.layers.%d.%s.weight" % (li, name), n, k,
-                            ctx.to_host(p4d, (p4d.nbytes,), np.uint8)))
-            p4d.free()
-    p4d, _ = ctx.synthesize_p4(seed=199, rows=vocab, cols=hidden)
-    tensors.append(("model.embed_tokens.weight", vocab, hidden,
-                    ctx.to_host(p4d, (p4d.nbytes,), np.uint8)))
-    p4d.free()
+    from llmcp_amd import model_arena
+    t0 = time.perf_counter()
+    image, entries = model_arena.build_image(seed=11)
+    build_s = time.perf_counter() - t0
     d = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
     path = os.path.join(d, "llmcp_q8_bench_arena_%d.bin" % os.getpid())
     try:
-        t0 = time.perf_counter()
-        q8.write_arena(path, tensors)
-        write_s = time.perf_counter() - t0
-        del tensors
+        image.tofile(path)
+        del image
         f = np.memmap(path, dtype=np.uint8, mode="r")
         ctx.sync()
         t0 = time.perf_counter()
         count = ctx.upload_arena(f)
         ctx.sync()
         upload_s = time.perf_counter() - t0
-        arena = struct.unpack_from("<Q", f, 16)[0]
-        entries = json.loads(bytes(f[arena:]).decode())["tensors"]
         w = {e["name"]: q8.Weight(ctx, f.ctypes.data + e["offset"], e["shape"][0],
-                                  e["shape"][1], owner=f) for e in entries}
+                                  e["shape"][1], owner=f)
+             for e in entries if e["dtype"] == "Q8_0"}
+        cfg = model_arena.CONFIG_4B
+        hidden, vocab = cfg["hidden"], cfg["vocab"]
         rng = np.random.default_rng(6)
         x = ctx.to_device(rng.standard_normal((1, hidden)).astype(np.float32))
-        yq, yh = ctx.alloc(qkv * 4), ctx.alloc(ffn * 4)
-        y, logits, am = ctx.alloc(hidden * 4), ctx.alloc(vocab * 4), ctx.alloc(8)
+        xv = ctx.to_device(rng.standard_normal((1, 4096)).astype(np.float32))
+        out = ctx.alloc(16384 * 4)
+        h = ctx.alloc(cfg["intermediate"] * 4)
+        logits, am = ctx.alloc(vocab * 4), ctx.alloc(8)
+        names = sorted(w)
 
         def step():
-            for li in range(layers):
-                pre = "model.layers.%d." % li
-                ctx.linear(x, w[pre + "qkv.weight"], yq, 1)
-                for nm in ("o", "a", "b"):
-                    ctx.linear(x, w[pre + nm + ".weight"], y, 1)
-                ctx.mlp(x, w[pre + "gate.weight"], w[pre + "up.weight"],
-                        w[pre + "down.weight"], y, h=yh)
-            ctx.lm_head(x, w["model.embed_tokens.weight"], logits, 1, argmax=am)
+            for layer in range(cfg["layers"]):
+                pre = "model.language_model.layers.%d." % layer
+                for nm in names:
+                    if not nm.startswith(pre) or ".mlp." in nm:
+                        continue
+                    t = w[nm]
+                    ctx.linear(xv if t.cols == 4096 else x, t, out, 1)
+                ctx.mlp(x, w[pre + "mlp.gate_proj.weight"], w[pre + "mlp.up_proj.weight"],
+                        w[pre + "mlp.down_proj.weight"], out, h=h)
+            ctx.lm_head(x, w["model.language_model.embed_tokens.weight"], logits, 1,
+                        argmax=am)
 
         step()
         ctx.sync()
@@ -369,6 +376,8 @@ def bench_arena(ctx, q8, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=24832
         g = graph_of(ctx, step)
         run_graph(ctx, timer, g, 1)
         step_us = run_graph(ctx, timer, g, 5) * 1e3 / 5
+        ctx.graph_destroy(g)
+        q8_bytes = sum(e["size"] for e in entries if e["dtype"] == "Q8_0")
         for wt in w.values():
             ctx.release(wt)
         nbytes = int(f.nbytes)
@@ -376,62 +385,126 @@ def bench_arena(ctx, q8, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=24832
     finally:
         if os.path.exists(path):
             os.unlink(path)
-    return {"file_bytes": nbytes, "q8_tensors": count, "write_s": round(write_s, 2),
+    return {"file_bytes": nbytes, "tensors": len(entries), "q8_tensors": count,
+            "build_s": round(build_s, 2),
             "upload_s": round(upload_s, 3), "upload_GB/s": round(nbytes / upload_s / 1e9, 2),
-            "decode_step_us": round(step_us, 1)}
+            "decode_step_us": round(step_us, 1),
+            "decode_step_GB/s": round(q8_bytes / (step_us * 1e-6) / 1e9, 1)}
 
 
-def cpu_baseline(res, budget_s=12.0):
-    """Reference x86 scalar Q8 path (oracle restatement) on the host cores."""
-    from oracle import q8_oracle as o
-    o.set_threads(int(os.environ.get("OMP_NUM_THREADS", "16")))
-    x = res["x"]
-    pg, pu, pd = res["host_p4"]
-    hidden, ffn = res["hidden"], res["ffn"]
+def host_description():
+    """The GPU box's host as the CPU baseline sees it."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {"nproc": os.cpu_count(), "affinity_cpus": affinity, "model": model}
+
+
+def _timed(fn, budget_s, max_calls):
     t0 = time.perf_counter()
     n = 0
     while True:
-        h = o.swiglu(x, pg, pu, ffn)              # row-parallel: 1 thread at M=1
-        o.linear(h, pd, hidden)
+        fn()
         n += 1
-        if time.perf_counter() - t0 > budget_s or n >= 250:
-            break
-    dt = (time.perf_counter() - t0) / n
-    t0 = time.perf_counter()
-    m = 0
-    while True:
-        h = o.swiglu(x, pg, pu, ffn, colpar=True)
-        o.linear(h, pd, hidden, colpar=True)
-        m += 1
-        if time.perf_counter() - t0 > budget_s / 2 or m >= 200:
-            break
-    dt_col = (time.perf_counter() - t0) / m
-    # Config 4's GEMM on the same path: the scalar GEMM is row-parallel over
-    # M (Q8Scalar.cpp:84,127), so a 64-row sample on all threads gives its
-    # per-row rate, which holds for M = 1024.
-    rows = 64
+        if time.perf_counter() - t0 > budget_s or n >= max_calls:
+            return (time.perf_counter() - t0) / n, n
+
+
+def cpu_baseline(res, c1, c3, seq, budget_s=18.0):
+    """The reference's x86 Q8 CPU path (the oracle's C restatement of
+    ScalarQ8::emit, Q8Scalar.cpp:65-212, scalar epilogue) on the host cores,
+    on bounded samples of each config.  The reference parallelises that path
+    over rows only (Q8Scalar.cpp:84,127), so every M = 1 figure runs on one
+    thread; the multi-row GEMM runs row-parallel on all threads the box
+    allots (OMP_NUM_THREADS, else the process's CPU affinity).  A
+    column-parallel variant of the decode MLP on those threads is labelled
+    as such."""
+    from oracle import q8_oracle as o
+    host = host_description()
+    threads = int(os.environ.get("OMP_NUM_THREADS") or host["affinity_cpus"] or 1)
+    o.set_threads(threads)
+    host["omp_max_threads"] = o.max_threads()
+    x = res["x"]
+    pg, pu, pd = res["host_p4"]
+    hidden, ffn = res["hidden"], res["ffn"]
+
+    def mlp():
+        o.linear(o.swiglu(x, pg, pu, ffn), pd, hidden)
+
+    dt, n = _timed(mlp, budget_s * 0.3, 250)
+    dt_col, m_col = _timed(lambda: o.linear(o.swiglu(x, pg, pu, ffn, colpar=True),
+                                            pd, hidden, colpar=True),
+                           budget_s * 0.1, 200)
+    # config 1: one 2560 x 2560 GEMV (one thread at M = 1)
+    x1 = np.random.default_rng(1).standard_normal((1, 2560)).astype(np.float32)
+    dt1, n1 = _timed(lambda: o.linear(x1, c1["p4"], 2560), budget_s * 0.08, 500)
+    # config 3: the 248320 x 2560 lm_head row and its first-max argmax, and
+    # the 1024-id gather
+    x3 = c3["x"]
+    dt3, n3 = _timed(lambda: o.argmax(o.linear(x3, c3["p4"], 248320)),
+                     budget_s * 0.15, 20)
+    ids = np.random.default_rng(3).integers(0, 248320, 1024).astype(np.int64)
+    dtg, ng = _timed(lambda: o.embedding(ids, c3["p4"], 2560), budget_s * 0.03, 200)
+    # config 4: M = 1024 GEMM, row-parallel; a 256-row sample on all threads
+    # gives the per-row rate, which a 1024-row call keeps (rows are
+    # independent and equal in cost)
+    rows = 256
     xg = np.random.default_rng(4).standard_normal((rows, hidden)).astype(np.float32)
-    t0 = time.perf_counter()
-    k = 0
-    while True:
-        o.linear(xg, pg, ffn)
-        k += 1
-        if time.perf_counter() - t0 > budget_s / 4 or k >= 50:
-            break
-    dt_g = (time.perf_counter() - t0) / k
+    dtg4, ng4 = _timed(lambda: o.linear(xg, pg, ffn), budget_s * 0.12, 20)
     gemm_ops = 2.0 * rows * ffn * hidden
-    return dict(value=res["step_bytes"] / dt / 1e9, unit="GB/s", cores=1,
-                kind="port",
-                sample="%d decode-MLP steps (2560->9216 x2 SwiGLU, 9216->2560) on one "
-                       "weight copy, scalar epilogue, row-parallel OpenMP as "
-                       "Q8Scalar.cpp:84,127 (M=1 -> 1 thread); %.1f ms/step" % (n, dt * 1e3),
-                colpar_value=res["step_bytes"] / dt_col / 1e9,
-                colpar_threads=o.max_threads(),
-                colpar_ms_per_step=dt_col * 1e3,
-                gemm={"TOPS": round(gemm_ops / dt_g / 1e12, 4), "threads": o.max_threads(),
-                      "sample": "%d-row samples of config 4 (K=2560 -> N=9216), scalar "
-                                "epilogue, row-parallel OpenMP; %d calls" % (rows, k),
-                      "ms_per_m1024_call": round(dt_g * 1024 / rows * 1e3, 1)})
+    # config 5: the 32-layer sequence at M = 1 from one-thread times of each
+    # shape (the QKV block timed here, the rest above), at M = 1024 from the
+    # row-parallel per-row rate
+    xq = np.random.default_rng(5).standard_normal((1, 2560)).astype(np.float32)
+    dtq, nq = _timed(lambda: o.linear(xq, seq["_qkv_p4"], 7680), budget_s * 0.05, 200)
+    t_layer = dtq + 3 * dt1 + dt
+    t_seq1 = 32 * t_layer + dt3
+    seq_bytes = seq["weight_bytes"]
+    seq_ops_layers = 2.0 * (seq_bytes - 248320 * 2560 // 32 * 34) * 32 / 34
+    # the GEMM's row-parallel rate on `threads` threads, applied to the
+    # sequence's ops
+    gemm_rate = gemm_ops / dtg4  # ops/s on all threads
+    t_seq1024 = 1024 * seq_ops_layers / gemm_rate + dt3
+    c2_bytes = res["step_bytes"]
+    return dict(
+        value=c2_bytes / dt / 1e9, unit="GB/s", cores=1, kind="port",
+        sample="%d decode-MLP steps (2560->9216 x2 SwiGLU, 9216->2560) on one weight "
+               "copy, x86 scalar path, row-parallel OpenMP as Q8Scalar.cpp:84,127 "
+               "(M=1 -> 1 thread); %.1f ms/step" % (n, dt * 1e3),
+        host=host, threads=threads,
+        colpar={"GB/s": round(c2_bytes / dt_col / 1e9, 3), "threads": o.max_threads(),
+                "ms_per_step": round(dt_col * 1e3, 3), "calls": m_col,
+                "note": "column-parallel variant of the same scalar math (not the "
+                        "reference's parallelisation)"},
+        configs={
+            "gemv_2560x2560": {"us": round(dt1 * 1e6, 1), "threads": 1, "calls": n1,
+                               "GB/s": round(c1["bytes"] / dt1 / 1e9, 3)},
+            "lm_head_248320x2560_argmax": {"us": round(dt3 * 1e6, 1), "threads": 1,
+                                           "calls": n3,
+                                           "GB/s": round(c3["bytes"] / dt3 / 1e9, 3)},
+            "embedding_gather_1024": {"us": round(dtg * 1e6, 1), "threads": 1, "calls": ng},
+            "gemm_m1024_n9216_k2560": {"TOPS": round(gemm_ops / dtg4 / 1e12, 4),
+                                       "threads": threads,
+                                       "ms_per_call": round(dtg4 * 1024 / rows * 1e3, 1),
+                                       "sample": "%d-row calls x %d, row-parallel" % (rows, ng4)},
+            "sequence_32_layers": {
+                "m1_us": round(t_seq1 * 1e6, 1), "m1_threads": 1,
+                "m1_GB/s": round(seq_bytes / t_seq1 / 1e9, 3),
+                "m1024_ms": round(t_seq1024 * 1e3, 1), "m1024_threads": threads,
+                "sample": "sum over the layer's shapes of the one-thread times above "
+                          "(QKV 7680x2560 timed %d calls); M=1024 at the GEMM's "
+                          "row-parallel rate" % nq},
+        })
 
 
 def copy_calibration(ctx, nbytes=256 << 20, reps=10):
@@ -467,9 +540,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration)")
-    ap.add_argument("--arena", action="store_true",
-                    help="also load the 32-layer model from a 4.4 GB arena "
-                         "file (written to /dev/shm) and time the upload")
+    ap.add_argument("--no-arena", action="store_true",
+                    help="skip the real-model arena (4.47 GB file in /dev/shm: "
+                         "upload and one decode step through it)")
     ap.add_argument("--gemm-only", type=int, default=0, metavar="M",
                     help="time only config 4's prefill GEMM at M rows and print "
                          "its figures (a short run for counter collection)")
@@ -492,25 +565,35 @@ def main():
         print(json.dumps({"gemm_m%d_n9216_k2560" % args.gemm_only: r}), flush=True)
         return
     res = bench_decode_mlp(ctx, q8, args.steps, args.warmup)
-    extra = {}
+    extra = {"platform": args.platform}
+    repack = dict(res["repack_ms"])
+    c1 = c3 = seq = None
     if not args.no_extra:
         c1 = bench_gemv(ctx, 2560, 2560)
         extra["gemv_2560x2560"] = {"us": round(c1["us"], 3), "GB/s": round(c1["gb_s"], 1),
                                    "frac_hbm": round(c1["gb_s"] / HBM_PEAK_GBS, 4)}
+        repack["2560x2560"] = round(c1["repack_ms"], 3)
         c1a = bench_gemv(ctx, 2560, 2560, residual=True)
         extra["gemv_2560x2560_residual_add"] = {"us": round(c1a["us"], 3)}
         c3 = bench_lm_head(ctx)
         extra["lm_head_248320x2560_argmax"] = {
             "us": round(c3["us"], 2), "GB/s": round(c3["gb_s"], 1),
             "frac_hbm": round(c3["gb_s"] / HBM_PEAK_GBS, 4)}
+        repack["248320x2560"] = round(c3["repack_ms"], 3)
         extra["embedding_gather_1024"] = {"us": round(c3["gather_us"], 2),
                                           "GB/s": round(c3["gather_gb_s"], 1)}
         for m in (64, 256, 1024):
             extra["gemm_m%d_n9216_k2560" % m] = bench_gemm(ctx, m)
-        extra["sequence_32_layers"] = bench_sequence(ctx)
-    if args.arena:
-        extra["arena_32_layers"] = bench_arena(ctx, q8)
-    cpu = None if args.no_cpu else cpu_baseline(res)
+        seq = bench_sequence(ctx)
+        repack["7680x2560"] = round(seq["_qkv_repack_ms"], 3)
+        extra["sequence_32_layers"] = {k: v for k, v in seq.items() if not k.startswith("_")}
+        if not args.no_arena:
+            extra["arena_real_model_32_layers"] = bench_arena(ctx, q8)
+    # the one-time device repack (unit layout) of one tensor of each shape,
+    # timed with HIP events on its own, outside every timed step
+    extra["repack_ms"] = repack
+    cpu = None if args.no_cpu or c1 is None else cpu_baseline(res, c1, c3, seq)
+    fv = 16 if args.platform == "aarch64" else 0
     line = {
         "metric": "Q8_0 linear: M=1 GEMV HBM GB/s (% peak); M=1024 GEMM int8 TOPS (% peak)",
         "value": round(res["gb_s"], 1),
@@ -535,13 +618,14 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": (load_traffic() or {}).get("hbm_bytes_per_launch"),
-                     "kernel": "gemv_kernel<2,false,IN_WG,4,4,5,0> (fused gate/up "
-                               "SwiGLU, 4-wave workgroups, input row quantized "
-                               "per workgroup; timed alone via llmcp_q8_swiglu)",
+                     "kernel": "gemv_kernel<2,false,1,4,4,5,%d> (fused gate/up SwiGLU, "
+                               "4-wave workgroups, input row quantized per workgroup; "
+                               "timed alone via llmcp_q8_swiglu, %d launches)"
+                               % (fv, res["steps"]),
                      "launch_us": round(res["gu_launch_us"], 3),
                      "algorithmic_bytes": res["gu_bytes"],
                      "down_launch_us": round(res["down_launch_us"], 3),
-                     "graph_kernel_floor_us": round(res["tiny_launch_us"], 3)},
+                     "down_GB/s": round(res["down_bytes"] / res["down_launch_us"] / 1e3, 1)},
         "cpu_baseline": None if cpu is None else {
             k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()},
         "extra": extra,
