@@ -289,11 +289,18 @@ def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320
         y = ctx.alloc(m * hidden * 4)
         logits, am = ctx.alloc(vocab * 4), ctx.alloc(8)
 
-        def step():
+        ya, yb = ctx.alloc(m * hidden * 4), ctx.alloc(m * hidden * 4)
+
+        def step(grouped=False):
             for ws in layer:
-                ctx.linear(x, ws["qkv"][0], yq, m, mode=mode)
-                for nm in ("o", "a", "b"):
-                    ctx.linear(x, ws[nm][0], y, m, mode=mode)
+                if grouped:
+                    # the four linears of one input as one group
+                    ctx.linear_group(x, [ws[nm][0] for nm in ("qkv", "o", "a", "b")],
+                                     [yq, y, ya, yb], m, mode=mode)
+                else:
+                    ctx.linear(x, ws["qkv"][0], yq, m, mode=mode)
+                    for nm in ("o", "a", "b"):
+                        ctx.linear(x, ws[nm][0], y, m, mode=mode)
                 if m == 1:
                     ctx.mlp(x, ws["gate"][0], ws["up"][0], ws["down"][0], y, h=yh)
                 else:
@@ -301,16 +308,22 @@ def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320
                     ctx.linear(h, ws["down"][0], y, m, mode=mode)
             ctx.lm_head(x, head[0], logits, 1, argmax=am, mode=mode)
 
-        step()  # sizes scratch outside capture
-        ctx.sync()
-        g = graph_of(ctx, step)
-        run_graph(ctx, timer, g, 1)
-        reps = 10 if m == 1 else 3
-        us = run_graph(ctx, timer, g, reps) * 1e3 / reps
         ops = 2.0 * m * (total - p4_bytes(vocab, hidden)) * 32 / 34 + 2.0 * vocab * hidden
         key = "m%d" % m
-        out[key] = {"us": round(us, 1), "GB/s": round(total / (us * 1e-6) / 1e9, 1),
-                    "TOPS": round(ops / (us * 1e-6) / 1e12, 2)}
+        for grouped in (False, True):
+            step(grouped)  # sizes scratch outside capture
+            ctx.sync()
+            g = graph_of(ctx, lambda: step(grouped))
+            run_graph(ctx, timer, g, 1)
+            reps = 10 if m == 1 else 3
+            us = run_graph(ctx, timer, g, reps) * 1e3 / reps
+            ctx.graph_destroy(g)
+            fig = {"us": round(us, 1), "GB/s": round(total / (us * 1e-6) / 1e9, 1),
+                   "TOPS": round(ops / (us * 1e-6) / 1e12, 2)}
+            if grouped:
+                out[key]["grouped"] = fig
+            else:
+                out[key] = fig
     for ws in layer:
         for w, p4d in ws.values():
             ctx.release(w)
@@ -357,26 +370,33 @@ def bench_arena(ctx, q8):
         logits, am = ctx.alloc(vocab * 4), ctx.alloc(8)
         names = sorted(w)
 
-        def step():
+        outs = [ctx.alloc(8192 * 4) for _ in range(4)]
+
+        def step(grouped=False):
             for layer in range(cfg["layers"]):
                 pre = "model.language_model.layers.%d." % layer
-                for nm in names:
-                    if not nm.startswith(pre) or ".mlp." in nm:
-                        continue
-                    t = w[nm]
-                    ctx.linear(xv if t.cols == 4096 else x, t, out, 1)
+                mix = [nm for nm in names if nm.startswith(pre) and ".mlp." not in nm]
+                shared = [nm for nm in mix if w[nm].cols == hidden]  # the normed input's
+                for nm in mix:
+                    if not grouped or nm not in shared:
+                        ctx.linear(xv if w[nm].cols == 4096 else x, w[nm], out, 1)
+                if grouped:
+                    # qkv/z/a/b (linear attention) or q/k/v (full attention)
+                    ctx.linear_group(x, [w[nm] for nm in shared], outs[:len(shared)], 1)
                 ctx.mlp(x, w[pre + "mlp.gate_proj.weight"], w[pre + "mlp.up_proj.weight"],
                         w[pre + "mlp.down_proj.weight"], out, h=h)
             ctx.lm_head(x, w["model.language_model.embed_tokens.weight"], logits, 1,
                         argmax=am)
 
-        step()
-        ctx.sync()
         timer = Timer(ctx)
-        g = graph_of(ctx, step)
-        run_graph(ctx, timer, g, 1)
-        step_us = run_graph(ctx, timer, g, 5) * 1e3 / 5
-        ctx.graph_destroy(g)
+        step_us = {}
+        for grouped in (False, True):
+            step(grouped)
+            ctx.sync()
+            g = graph_of(ctx, lambda: step(grouped))
+            run_graph(ctx, timer, g, 1)
+            step_us[grouped] = run_graph(ctx, timer, g, 5) * 1e3 / 5
+            ctx.graph_destroy(g)
         q8_bytes = sum(e["size"] for e in entries if e["dtype"] == "Q8_0")
         for wt in w.values():
             ctx.release(wt)
@@ -388,8 +408,10 @@ def bench_arena(ctx, q8):
     return {"file_bytes": nbytes, "tensors": len(entries), "q8_tensors": count,
             "build_s": round(build_s, 2),
             "upload_s": round(upload_s, 3), "upload_GB/s": round(nbytes / upload_s / 1e9, 2),
-            "decode_step_us": round(step_us, 1),
-            "decode_step_GB/s": round(q8_bytes / (step_us * 1e-6) / 1e9, 1)}
+            "decode_step_us": round(step_us[False], 1),
+            "decode_step_GB/s": round(q8_bytes / (step_us[False] * 1e-6) / 1e9, 1),
+            "decode_step_grouped_us": round(step_us[True], 1),
+            "decode_step_grouped_GB/s": round(q8_bytes / (step_us[True] * 1e-6) / 1e9, 1)}
 
 
 def host_description():

@@ -232,6 +232,32 @@ int llmcp_q8_linear_add_bf16(llmcp_q8_ctx *ctx,
                              llmcp_memref_bf16_2d *output,
                              int32_t execution_mode);
 
+/* Most linears one llmcp_q8_linear_group call takes. */
+#define LLMCP_Q8_MAX_GROUP 8
+
+/* Linears that share one input: y_i[M,N_i] = act_i(x[M,K] . W_i[N_i,K]^T)
+ * for i < count (1 to LLMCP_Q8_MAX_GROUP), the pattern of the model
+ * builder's in_proj_qkv/z/a/b (ModelBuilder.cpp:229-236) and q/k/v
+ * (:288-294), which the reference lowers as separate llmcp.linear ops.  The
+ * input is quantized once; for one row, one GEMV launch covers every
+ * weight (when the row is 16 B aligned, f32 outputs or all bf16, and the
+ * weights' rows total at most 16384), else each weight's GEMV follows.
+ * Results equal count separate llmcp_q8_linear calls bit for bit.
+ * activations (nullable: none) holds llmcp_q8_activation per linear. */
+int llmcp_q8_linear_group(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                          int32_t count,
+                          const llmcp_memref_i8_1d *const *weights,
+                          llmcp_memref_f32_2d *const *outputs,
+                          const int32_t *activations, int32_t execution_mode);
+
+/* bf16 input and outputs (as llmcp_q8_linear_bf16 per linear). */
+int llmcp_q8_linear_group_bf16(llmcp_q8_ctx *ctx,
+                               const llmcp_memref_bf16_2d *input, int32_t count,
+                               const llmcp_memref_i8_1d *const *weights,
+                               llmcp_memref_bf16_2d *const *outputs,
+                               const int32_t *activations,
+                               int32_t execution_mode);
+
 /* Fused SwiGLU hidden: h = silu(x . Wg^T) * (x . Wu^T), the pair
  * `linear{activation=silu}` + `mul` that FuseSiluMul produces
  * (FuseLinearActivations.cpp:27-43, LowerToLinalg.cpp:377-393). */
@@ -391,6 +417,18 @@ int32_t _mlir_ciface_llmcp_q8_linear(llmcp_memref_f32_2d *input,
                                      llmcp_memref_f32_2d *output,
                                      int32_t activation,
                                      int32_t execution_mode);
+/* The group entry in the two arities the model uses (q/k/v, qkv/z/a/b). */
+int32_t _mlir_ciface_llmcp_q8_linear_group3(
+    llmcp_memref_f32_2d *input, llmcp_memref_i8_1d *w0, llmcp_memref_i8_1d *w1,
+    llmcp_memref_i8_1d *w2, llmcp_memref_f32_2d *y0, llmcp_memref_f32_2d *y1,
+    llmcp_memref_f32_2d *y2, int32_t act0, int32_t act1, int32_t act2,
+    int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_linear_group4(
+    llmcp_memref_f32_2d *input, llmcp_memref_i8_1d *w0, llmcp_memref_i8_1d *w1,
+    llmcp_memref_i8_1d *w2, llmcp_memref_i8_1d *w3, llmcp_memref_f32_2d *y0,
+    llmcp_memref_f32_2d *y1, llmcp_memref_f32_2d *y2, llmcp_memref_f32_2d *y3,
+    int32_t act0, int32_t act1, int32_t act2, int32_t act3,
+    int32_t execution_mode);
 int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
                                      llmcp_memref_i8_1d *w_gate,
                                      llmcp_memref_i8_1d *w_up,

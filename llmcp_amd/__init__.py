@@ -80,6 +80,8 @@ EXPORTS = [
     "_mlir_ciface_llmcp_q8_lm_head_bf16", "_mlir_ciface_llmcp_q8_embedding_bf16",
     "llmcp_q8_linear_add", "llmcp_q8_linear_add_bf16",
     "_mlir_ciface_llmcp_q8_linear_add", "_mlir_ciface_llmcp_q8_linear_add_bf16",
+    "llmcp_q8_linear_group", "llmcp_q8_linear_group_bf16",
+    "_mlir_ciface_llmcp_q8_linear_group3", "_mlir_ciface_llmcp_q8_linear_group4",
 ]
 
 
@@ -159,6 +161,10 @@ def lib():
         "llmcp_q8_linear_add_bf16": (I, [P, P, P, P, P, I32]),
         "_mlir_ciface_llmcp_q8_linear_add": (I32, [P, P, P, P, I32]),
         "_mlir_ciface_llmcp_q8_linear_add_bf16": (I32, [P, P, P, P, I32]),
+        "llmcp_q8_linear_group": (I, [P, P, I32, P, P, P, I32]),
+        "llmcp_q8_linear_group_bf16": (I, [P, P, I32, P, P, P, I32]),
+        "_mlir_ciface_llmcp_q8_linear_group3": (I32, [P] * 7 + [I32] * 4),
+        "_mlir_ciface_llmcp_q8_linear_group4": (I32, [P] * 9 + [I32] * 5),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -380,6 +386,21 @@ class Context:
         check(self._entry("llmcp_q8_linear", dtype)(
             self.handle, ctypes.byref(xi), ctypes.byref(w.memref()),
             ctypes.byref(yo), ACT[activation], MODE[mode]))
+
+    def linear_group(self, x, weights, outputs, m, activations=None,
+                     mode="decode", dtype="f32"):
+        """Linears sharing the input x: outputs[i] = act_i(x . W_i^T)."""
+        n = len(weights)
+        k = weights[0].cols
+        xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, k)
+        ws = [w.memref() for w in weights]
+        ys = [f32_memref(y.ptr if hasattr(y, "ptr") else y, m, w.rows)
+              for y, w in zip(outputs, weights)]
+        wp = (ctypes.c_void_p * n)(*[ctypes.addressof(d) for d in ws])
+        yp = (ctypes.c_void_p * n)(*[ctypes.addressof(d) for d in ys])
+        acts = (ctypes.c_int32 * n)(*[ACT[a] for a in (activations or ["none"] * n)])
+        check(self._entry("llmcp_q8_linear_group", dtype)(
+            self.handle, ctypes.byref(xi), n, wp, yp, acts, MODE[mode]))
 
     def swiglu(self, x, wg, wu, h, m, mode="decode", dtype="f32"):
         xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, wg.cols)

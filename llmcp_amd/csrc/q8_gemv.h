@@ -9,6 +9,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "q8_device.h"
 #include "q8_kernels.h"
 
@@ -27,6 +29,17 @@ struct GemvArgs {
   int32_t blocks;
   int32_t passes;
   int32_t act;       // llmcp_q8_activation (one-matrix GEMVs)
+};
+
+// Grouped GEMV (V bit 5): the lane groups of up to kMaxGroup weights that
+// share the input row, one after another; lane group g belongs to weight i
+// when gstart[i] <= g < gstart[i + 1].
+struct GemvGroupArgs : GemvArgs {
+  int32_t nw;
+  int64_t gstart[kMaxGroup + 1];
+  const uint8_t *wt[kMaxGroup];
+  void *yt[kMaxGroup];
+  int32_t actt[kMaxGroup];
 };
 
 // Where the GEMV's input row comes from.
@@ -295,9 +308,12 @@ __host__ __device__ constexpr int row_slots(int pc, int w) {
 // the current chain(), so the dots overlap the serial DPP additions.
 // V packs the compile-time variant: bit 0 the input row is bf16 (IN_WG),
 // bit 1 the output is bf16, bit 2 a one-matrix GEMV applies a.act, bit 3 a
-// one-matrix GEMV adds the residual row a.r to its (rounded) result.
+// one-matrix GEMV adds the residual row a.r to its (rounded) result, bit 4
+// the fma epilogue, bit 5 a grouped GEMV (GemvGroupArgs: each wave takes its
+// weight, output and activation from the group table).
 template <int NMAT, bool ARGMAX, int IN, int W, int D, int PC, int V>
-__global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(64 * W) void gemv_kernel(
+    std::conditional_t<(V & 32) != 0, GemvGroupArgs, GemvArgs> a) {
   constexpr bool XB = (V & 1) != 0;
   constexpr bool YB = (V & 2) != 0;
   constexpr bool ACTV = (V & 4) != 0;
@@ -306,7 +322,9 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   // (Q8Decode.cpp:192-203); clear: the scalar path's acc + f32(I)*(sa*dw)
   // (Q8Scalar.cpp:192-199).
   constexpr bool FMA = (V & 16) != 0;
+  constexpr bool GROUP = (V & 32) != 0;
   static_assert(!ADD || (NMAT == 1 && !ARGMAX && !ACTV), "residual add variants");
+  static_assert(!GROUP || (NMAT == 1 && !ARGMAX && !ADD && IN == IN_WG), "grouped variants");
   extern __shared__ __align__(16) unsigned char lds[];  // IN_WG input row
   __shared__ unsigned long long key_l[W];
   const int passes = PC > 0 ? PC : a.passes;
@@ -356,8 +374,22 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
   // so that the loads below are unconditional: a branch around them would
   // make the compiler wait for the whole ring at the join.
   const int64_t gl = active ? g : a.groups - 1;
+  // Grouped: the weight of this wave's lane group (wave-uniform) and the
+  // lane group's index inside it.
+  int widx = 0;
+  int64_t lg = gl;
+  const uint8_t *w0 = nullptr;
+  if constexpr (GROUP) {
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i)
+      if (i < a.nw && gl >= a.gstart[i]) widx = i;
+    lg = gl - a.gstart[widx];
+    w0 = a.wt[widx];
+  } else {
+    w0 = a.w0;
+  }
   const unsigned char *base[NMAT];
-  base[0] = a.w0 + gl * passes * kPassBytes;
+  base[0] = w0 + lg * passes * kPassBytes;
   if (NMAT == 2) base[NMAT - 1] = a.w1 + gl * passes * kPassBytes;
 
   uint4 q0[NMAT][D], q1[NMAT][D], x0[D], x1[D];
@@ -623,7 +655,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  const int64_t row = g * kLanes + r;
+  const int64_t row = lg * kLanes + r;  // lg == g unless grouped (active waves)
   // Epilogue (MatmulLoweringCommon.cpp:78-103).  SwiGLU: h = silu(gate) *
   // up; with a bf16 result each linear's output is rounded to bf16 before
   // the bf16 multiply (FuseSiluMul: linear{silu} + mul on bf16 tensors).
@@ -634,8 +666,12 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
                        bf16_to_float(float_to_bf16(acc[NMAT - 1]))
                  : gs * acc[NMAT - 1];
   } else {
-    y = ACTV ? activate(acc[0], a.act) : acc[0];
+    int act = a.act;
+    if constexpr (GROUP) act = a.actt[widx];
+    y = ACTV ? activate(acc[0], act) : acc[0];
   }
+  void *yout = a.y;
+  if constexpr (GROUP) yout = a.yt[widx];
   const bool owner = active && j == kOwnerSlot;  // the lane holding the sum
   if (owner) {
     // residual add (AddOpLowering, LowerToLinalg.cpp:359-375): the linear's
@@ -647,9 +683,9 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         y = y + ((const float *)a.r)[row];
     }
     if constexpr (YB)
-      ((uint16_t *)a.y)[row] = float_to_bf16(y);
+      ((uint16_t *)yout)[row] = float_to_bf16(y);
     else
-      ((float *)a.y)[row] = y;
+      ((float *)yout)[row] = y;
   }
 
   if (ARGMAX) {
@@ -698,8 +734,8 @@ constexpr int ring_depth() {
   return PC > 0 ? (PC < dmax ? PC : dmax) : (NMAT == 2 ? 4 : 8);
 }
 
-template <int NMAT, bool ARGMAX, int IN, int W, int PC, int V>
-hipError_t launch_gemv_p(const GemvArgs &args, hipStream_t s) {
+template <int NMAT, bool ARGMAX, int IN, int W, int PC, int V, class A>
+hipError_t launch_gemv_p(const A &args, hipStream_t s) {
   constexpr int D = ring_depth<NMAT, IN, PC>();
   const unsigned grid = (unsigned)((args.groups + W - 1) / W);
   const size_t slots = PC > 0 ? row_slots(PC, W) : (size_t)args.passes * kPassBlocks;
@@ -711,8 +747,8 @@ hipError_t launch_gemv_p(const GemvArgs &args, hipStream_t s) {
 
 // IN_WG takes its workgroup width from wg_waves; IN_PRE (wide outputs)
 // runs four waves per workgroup.
-template <int NMAT, bool ARGMAX, int IN, int PC, int V>
-hipError_t launch_gemv_w(const GemvArgs &args, hipStream_t s) {
+template <int NMAT, bool ARGMAX, int IN, int PC, int V, class A>
+hipError_t launch_gemv_w(const A &args, hipStream_t s) {
   constexpr int W = IN == IN_WG ? wg_waves(NMAT, PC) : 4;
   return launch_gemv_p<NMAT, ARGMAX, IN, W, PC, V>(args, s);
 }
@@ -720,8 +756,8 @@ hipError_t launch_gemv_w(const GemvArgs &args, hipStream_t s) {
 // Pass counts with a fully unrolled kernel: K = 512, 1024, 1536, 2560
 // (hidden size), 4096 and 9216 (the MLP down projection).  Others take the
 // runtime loop.
-template <int NMAT, bool ARGMAX, int IN, int V>
-hipError_t launch_gemv_t(const GemvArgs &args, hipStream_t s) {
+template <int NMAT, bool ARGMAX, int IN, int V, class A = GemvArgs>
+hipError_t launch_gemv_t(const A &args, hipStream_t s) {
   switch (args.passes) {
     case 1: return launch_gemv_w<NMAT, ARGMAX, IN, 1, V>(args, s);
     case 2: return launch_gemv_w<NMAT, ARGMAX, IN, 2, V>(args, s);
@@ -775,6 +811,24 @@ hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
     case 6: return launch_gemv_t<1, false, IN, (6) | F>(a, s);
     case 8: return launch_gemv_t<1, false, IN, (8) | F>(a, s);
     case 10: return launch_gemv_t<1, false, IN, (10) | F>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Grouped GEMV variants: f32 or bf16 in and out, with or without runtime
+// activations (V bit 2 when any weight of the group has one).
+template <bool FMA>
+hipError_t launch_gemv_group(const GemvGroupArgs &a, const GemvLaunch &l,
+                             hipStream_t s) {
+  bool any_act = false;
+  for (int i = 0; i < l.ngroup; ++i) any_act |= l.gact[i] != 0;
+  const int v = (l.x_bf16 ? 1 : 0) | (l.y_bf16 ? 2 : 0) | (any_act ? 4 : 0);
+  constexpr int F = (FMA ? 16 : 0) | 32;
+  switch (v) {
+    case 0: return launch_gemv_t<1, false, IN_WG, 0 | F>(a, s);
+    case 3: return launch_gemv_t<1, false, IN_WG, 3 | F>(a, s);
+    case 4: return launch_gemv_t<1, false, IN_WG, 4 | F>(a, s);
+    case 7: return launch_gemv_t<1, false, IN_WG, 7 | F>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

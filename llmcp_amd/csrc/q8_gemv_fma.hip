@@ -11,4 +11,9 @@ hipError_t launch_gemv_fma(const GemvArgs &a, const GemvLaunch &l, bool in_wg,
                : launch_gemv_in<IN_PRE, true>(a, l, s);
 }
 
+hipError_t launch_gemv_group_fma(const GemvGroupArgs &a, const GemvLaunch &l,
+                                 hipStream_t s) {
+  return launch_gemv_group<true>(a, l, s);
+}
+
 }  // namespace llmcp_q8

@@ -34,6 +34,9 @@ hipError_t launch_selftest_quantizer(unsigned long long *bad, hipStream_t s);
 hipError_t launch_selftest_exp(unsigned long long *out, float *inputs,
                                uint32_t *results, uint32_t cap, hipStream_t s);
 
+// Most weights one grouped GEMV serves (llmcp_q8_linear_group).
+constexpr int kMaxGroup = 8;
+
 struct GemvLaunch {
   const void *x = nullptr;       // input row (f32 16 B / bf16 8 B aligned),
   bool x_bf16 = false;           // quantized once per workgroup into LDS
@@ -53,7 +56,16 @@ struct GemvLaunch {
                                        // y's element type (may alias y)
   unsigned long long *keys = nullptr;  // non-null: fused argmax into these
   int64_t *argmax_out = nullptr;       // kArgmaxSlots slots, zero on entry
-};                                     // and left zero
+                                       // and left zero
+  // ngroup > 0: one launch for ngroup weights that share the input row
+  // (same cols; w, y, rows, activation above unused): weight i, gw[i]
+  // [grows[i], cols], writes gy[i] with activation gact[i].
+  int ngroup = 0;
+  const uint8_t *gw[kMaxGroup] = {};
+  void *gy[kMaxGroup] = {};
+  int64_t grows[kMaxGroup] = {};
+  int32_t gact[kMaxGroup] = {};
+};
 
 // One-matrix GEMVs with at most this many lane groups quantize the input
 // row inside the kernel (once per workgroup); wider ones (every workgroup

@@ -29,6 +29,8 @@ namespace llmcp_q8 {
 // The fma-epilogue GEMVs (q8_gemv_fma.hip).
 hipError_t launch_gemv_fma(const GemvArgs &a, const GemvLaunch &l, bool in_wg,
                            hipStream_t s);
+hipError_t launch_gemv_group_fma(const GemvGroupArgs &a, const GemvLaunch &l,
+                                 hipStream_t s);
 
 namespace {
 
@@ -532,6 +534,26 @@ hipError_t launch_gemv(const GemvLaunch &l, hipStream_t s) {
   a.act = l.activation;
   const int in = l.x ? IN_WG : IN_PRE;
   if (l.x && (uintptr_t)l.x % (l.x_bf16 ? 8 : 16)) return hipErrorInvalidValue;
+  if (l.ngroup > 0) {
+    // grouped: the weights' lane groups back to back in one grid
+    if (!l.x || l.ngroup > kMaxGroup || l.keys || l.residual)
+      return hipErrorInvalidValue;
+    GemvGroupArgs ga;
+    static_cast<GemvArgs &>(ga) = a;
+    ga.nw = l.ngroup;
+    int64_t start = 0;
+    for (int i = 0; i < kMaxGroup; ++i) {
+      const bool used = i < l.ngroup;
+      ga.gstart[i] = start;
+      ga.wt[i] = used ? l.gw[i] : l.gw[0];
+      ga.yt[i] = used ? l.gy[i] : l.gy[0];
+      ga.actt[i] = used ? l.gact[i] : 0;
+      if (used) start += l.grows[i] / kLanes;
+    }
+    ga.gstart[kMaxGroup] = start;
+    ga.groups = start;
+    return l.fma ? launch_gemv_group_fma(ga, l, s) : launch_gemv_group<false>(ga, l, s);
+  }
   hipError_t e;
   if (l.fma)
     e = launch_gemv_fma(a, l, in == IN_WG, s);

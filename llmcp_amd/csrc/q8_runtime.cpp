@@ -29,6 +29,8 @@
 
 using namespace llmcp_q8;
 
+static_assert(LLMCP_Q8_MAX_GROUP == kMaxGroup, "group size of the C ABI");
+
 namespace {
 
 // A fixed buffer: recording an error never allocates (so it cannot throw).
@@ -1114,6 +1116,78 @@ static int linear_add_impl(llmcp_q8_ctx *ctx, const Rows &in,
   return gemm_launch(ctx, ws, m, w, out, LLMCP_Q8_ACT_NONE, nullptr, 0, &res);
 }
 
+// Linears that share one input (the model builder's in_proj_qkv/z/a/b and
+// q/k/v, ModelBuilder.cpp:229-236, :288-294): one input quantization and,
+// for one row, one GEMV launch over every weight's lane groups.  Results
+// equal the separate llmcp_q8_linear calls bit for bit.
+static int linear_group_impl(llmcp_q8_ctx *ctx, const Rows &in, int32_t count,
+                             const llmcp_memref_i8_1d *const *weights,
+                             const Rows *outs, const int32_t *acts,
+                             int32_t execution_mode) {
+  if (count < 1 || count > kMaxGroup)
+    return fail(LLMCP_Q8_EINVAL, "group of %d linears (1 to %d)", count,
+                kMaxGroup);
+  const Tensor *w[kMaxGroup];
+  for (int32_t i = 0; i < count; ++i) {
+    int rc = resolve_weight(ctx, weights[i], &w[i]);
+    if (rc) return rc;
+    if ((rc = check_linear_shapes(in, w[i], outs[i]))) return rc;
+    const int32_t act = acts ? acts[i] : LLMCP_Q8_ACT_NONE;
+    if (act < LLMCP_Q8_ACT_NONE || act > LLMCP_Q8_ACT_SOFTPLUS)
+      return fail(LLMCP_Q8_DECLINED, "unsupported activation %d", act);
+  }
+  int rc = check_mode(execution_mode);
+  if (rc) return rc;
+  const int64_t m = in.rows;
+  if (m == 0) return LLMCP_Q8_OK;
+  if ((rc = set_device(ctx))) return rc;
+  auto act_of = [&](int32_t i) { return acts ? acts[i] : LLMCP_Q8_ACT_NONE; };
+  if (m > 1) {
+    // one quantization of the input rows, then each weight's GEMM
+    Workspace ws = ctx_workspace(ctx);
+    if ((rc = gemm_quantize(ctx, in, w[0], ws))) return rc;
+    for (int32_t i = 0; i < count; ++i)
+      if ((rc = gemm_launch(ctx, ws, m, w[i], outs[i], act_of(i), nullptr, 0)))
+        return rc;
+    return LLMCP_Q8_OK;
+  }
+  int64_t groups = 0;
+  bool same_type = true;
+  for (int32_t i = 0; i < count; ++i) {
+    groups += w[i]->rows / kLanes;
+    same_type &= outs[i].bf16 == outs[0].bf16;
+  }
+  // One launch when every workgroup can quantize the row itself (aligned
+  // row, not wider than one-launch GEMVs quantize in-workgroup); otherwise
+  // each weight's GEMV in turn.
+  const bool one_launch = same_type && (uintptr_t)in.data % (in.bf16 ? 8 : 16) == 0 &&
+                          groups <= kInLoopQuantMaxGroups;
+  if (!one_launch || count == 1) {
+    for (int32_t i = 0; i < count; ++i)
+      if ((rc = gemv_common(ctx, in, w[i], nullptr, outs[i], act_of(i), nullptr)))
+        return rc;
+    return LLMCP_Q8_OK;
+  }
+  if ((rc = ensure_decode_scratch(ctx, w[0]->rows, w[0]->cols))) return rc;
+  GemvLaunch l;
+  l.x = in.data;
+  l.x_bf16 = in.bf16;
+  l.y_bf16 = outs[0].bf16;
+  l.rows = groups * kLanes;
+  l.cols = w[0]->cols;
+  l.fma = ctx->fma();
+  l.ngroup = count;
+  for (int32_t i = 0; i < count; ++i) {
+    l.gw[i] = w[i]->dev;
+    l.gy[i] = outs[i].data;
+    l.grows[i] = w[i]->rows;
+    l.gact[i] = act_of(i);
+  }
+  hipError_t e = launch_gemv(l, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "grouped gemv launch");
+  return LLMCP_Q8_OK;
+}
+
 static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
                        const llmcp_memref_i8_1d *w_gate,
                        const llmcp_memref_i8_1d *w_up, const Rows &out,
@@ -1349,6 +1423,45 @@ int llmcp_q8_linear_add_bf16(llmcp_q8_ctx *ctx,
         !view_of(output, true, out))
       return fail(LLMCP_Q8_DECLINED, kDenseMsg);
     return linear_add_impl(ctx, in, weight, res, out, execution_mode);
+  });
+}
+
+int llmcp_q8_linear_group(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                          int32_t count,
+                          const llmcp_memref_i8_1d *const *weights,
+                          llmcp_memref_f32_2d *const *outputs,
+                          const int32_t *activations, int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!ctx || !weights || !outputs) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (count < 1 || count > kMaxGroup)
+      return fail(LLMCP_Q8_EINVAL, "group of %d linears (1 to %d)", count, kMaxGroup);
+    Rows in, outs[kMaxGroup];
+    if (!view_of(input, false, in)) return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    for (int32_t i = 0; i < count; ++i)
+      if (!view_of(outputs[i], false, outs[i]))
+        return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return linear_group_impl(ctx, in, count, weights, outs, activations,
+                             execution_mode);
+  });
+}
+
+int llmcp_q8_linear_group_bf16(llmcp_q8_ctx *ctx,
+                               const llmcp_memref_bf16_2d *input, int32_t count,
+                               const llmcp_memref_i8_1d *const *weights,
+                               llmcp_memref_bf16_2d *const *outputs,
+                               const int32_t *activations,
+                               int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!ctx || !weights || !outputs) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (count < 1 || count > kMaxGroup)
+      return fail(LLMCP_Q8_EINVAL, "group of %d linears (1 to %d)", count, kMaxGroup);
+    Rows in, outs[kMaxGroup];
+    if (!view_of(input, true, in)) return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    for (int32_t i = 0; i < count; ++i)
+      if (!view_of(outputs[i], true, outs[i]))
+        return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    return linear_group_impl(ctx, in, count, weights, outs, activations,
+                             execution_mode);
   });
 }
 
@@ -1699,6 +1812,38 @@ int32_t _mlir_ciface_llmcp_q8_linear_add_bf16(llmcp_memref_bf16_2d *input,
     if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
     return llmcp_q8_linear_add_bf16(g_default_ctx, input, weight, residual,
                                     output, execution_mode);
+  });
+}
+
+// The model's two shared-input patterns as fixed-arity C-interface entries
+// (a lowered func.call passes each memref by descriptor): three linears
+// (q/k/v) and four (in_proj_qkv/z/a/b).
+int32_t _mlir_ciface_llmcp_q8_linear_group3(
+    llmcp_memref_f32_2d *input, llmcp_memref_i8_1d *w0, llmcp_memref_i8_1d *w1,
+    llmcp_memref_i8_1d *w2, llmcp_memref_f32_2d *y0, llmcp_memref_f32_2d *y1,
+    llmcp_memref_f32_2d *y2, int32_t act0, int32_t act1, int32_t act2,
+    int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    const llmcp_memref_i8_1d *w[3] = {w0, w1, w2};
+    llmcp_memref_f32_2d *y[3] = {y0, y1, y2};
+    const int32_t a[3] = {act0, act1, act2};
+    return llmcp_q8_linear_group(g_default_ctx, input, 3, w, y, a, execution_mode);
+  });
+}
+
+int32_t _mlir_ciface_llmcp_q8_linear_group4(
+    llmcp_memref_f32_2d *input, llmcp_memref_i8_1d *w0, llmcp_memref_i8_1d *w1,
+    llmcp_memref_i8_1d *w2, llmcp_memref_i8_1d *w3, llmcp_memref_f32_2d *y0,
+    llmcp_memref_f32_2d *y1, llmcp_memref_f32_2d *y2, llmcp_memref_f32_2d *y3,
+    int32_t act0, int32_t act1, int32_t act2, int32_t act3,
+    int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    const llmcp_memref_i8_1d *w[4] = {w0, w1, w2, w3};
+    llmcp_memref_f32_2d *y[4] = {y0, y1, y2, y3};
+    const int32_t a[4] = {act0, act1, act2, act3};
+    return llmcp_q8_linear_group(g_default_ctx, input, 4, w, y, a, execution_mode);
   });
 }
 
