@@ -384,63 +384,122 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   };
   const int bsw = (lane >> 2) & 3;  // swizzle of this lane's weight run
 
-  // Scale tiles of blocks kb+2k (lanes 0-31) and kb+2k+1 (lanes 32-63).
+  // Scale tiles of blocks kb+2k (lanes 0-31) and kb+2k+1 (lanes 32-63): the
+  // LDS reads (read_scales) and, one block later, the f16 half select and
+  // the outer-product MFMA (scale_tile).
   typedef float v32f __attribute__((ext_vector_type(32)));
-  auto scales = [&](int kb, St &buf, int k) __attribute__((always_inline)) -> v32f {
-    const float fa = buf.sa[wm][2 * k + lh][li];
-    uint32_t h;
+  struct ScaleRaw {
+    float fa;
+    uint32_t d;
+  };
+  auto read_scales = [&](int kb, St &buf, int k) __attribute__((always_inline)) -> ScaleRaw {
+    ScaleRaw r;
+    r.fa = buf.sa[wm][2 * k + lh][li];
     if constexpr (SEG == 1) {
       // this lane's row n = li of column tile wn: group li/4, row li%4; the
-      // f16 pair (2k, 2k+1) of the stage's slots, half lh
-      const uint32_t pair = ((const uint32_t *)buf.dw16[wn])[(li >> 2) * 32 + (li & 3) * 8 +
-                                                              ((kb & (kPassBlocks - 1)) >> 1) + k];
-      h = lh ? pair >> 16 : pair & 0xffffu;
+      // f16 pair (2k, 2k+1) of the stage's slots
+      r.d = ((const uint32_t *)buf.dw16[wn])[(li >> 2) * 32 + (li & 3) * 8 +
+                                             ((kb & (kPassBlocks - 1)) >> 1) + k];
+    } else {
+      r.d = buf.dw4[wn][k][lane];
+    }
+    return r;
+  };
+  auto scale_tile = [&](int kb, const ScaleRaw &r, int k) __attribute__((always_inline)) -> v32f {
+    uint32_t h;
+    if constexpr (SEG == 1) {
+      h = lh ? r.d >> 16 : r.d & 0xffffu;  // half lh of the pair
     } else if constexpr (SEG == 4) {
       // the stage's four blocks share one slot
-      const uint32_t dwp = buf.dw4[wn][k][lane];
       int64_t ub;
       int sb;
       locate<SEG>(kb, ub, sb);
-      h = (sb & 1) ? dwp >> 16 : dwp & 0xffffu;
+      h = (sb & 1) ? r.d >> 16 : r.d & 0xffffu;
     } else {
-      const uint32_t dwp = buf.dw4[wn][k][lane];
       const StagePos sp = stage_pos(kb);
-      h = ((sp.slot + Seg6::wrap(sp.r, 2 * k + lh)) & 1) ? dwp >> 16 : dwp & 0xffffu;
+      h = ((sp.slot + Seg6::wrap(sp.r, 2 * k + lh)) & 1) ? r.d >> 16 : r.d & 0xffffu;
     }
     const float fb = half_bits_to_float(h);
     const v32f z32 = {};
-    return __builtin_amdgcn_mfma_f32_32x32x1f32(fa, fb, z32, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x1f32(r.fa, fb, z32, 0, 0, 0);
   };
-  auto dots = [&](St &buf, int bb) __attribute__((always_inline)) -> v16i {
-    const v4i af = *(const v4i *)(buf.a[wm][bb] + lane * 16);
-    const v4i bf = *(const v4i *)(buf.b[wn] + lane * 64 + 16 * (bb ^ bsw));
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, zero, 0, 0, 0);
+  // A block's MFMA operands: the A piece (row tile wm) and B piece (column
+  // tile wn), read from LDS a block before the MFMA that takes them.
+  struct Frag {
+    v4i a, b;
   };
-  // Software-pipelined over the stage's blocks: block bb+1's MFMA (and the
-  // next pair's scale MFMA) issue before block bb's epilogue, so a wave has
-  // VALU work while its matrix ops run.
-  // The next stage's DMA ops (stage sn into buffer nbuf) are spread over
-  // the blocks, issued after each block's MFMAs: a burst of them right after
-  // the barrier would stall every wave on the load queue at once.
-  auto compute = [&](int s, St &buf, int sn, St &nbuf, const Offsets &of) __attribute__((always_inline)) {
+  auto read_frag = [&](St &buf, int bb) __attribute__((always_inline)) -> Frag {
+    Frag f;
+    f.a = *(const v4i *)(buf.a[wm][bb] + lane * 16);
+    f.b = *(const v4i *)(buf.b[wn] + lane * 64 + 16 * (bb ^ bsw));
+    return f;
+  };
+  auto dots = [&](const Frag &f) __attribute__((always_inline)) -> v16i {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a, f.b, zero, 0, 0, 0);
+  };
+
+  // The block pipeline.  Entering block g (stage s = g / 4, bb = g % 4) a
+  // wave holds block g's integer dots (c_cur), its pair's scale tile
+  // (f_cur), block g+1's operands (fr) and, for odd g, the raw scales of
+  // the pair g+1 starts (sr).  Block g then issues, in this order: block
+  // g+1's MFMA, for odd g the next pair's scale MFMA, the LDS reads of block
+  // g+2's operands (and, for even g, of the pair at g+2's scales) and its
+  // share of the DMA ops; only then its own epilogue, 32 VALU ops that
+  // cover the latency of everything just issued.  A scheduling barrier
+  // keeps that order.  Block g+2 lies in stage s+1 for bb >= 2, so the
+  // hand-off of stage s+1 (vmcnt wait, workgroup barrier) sits in block
+  // bb = 2, after that block's MFMA: every LDS read of stage s's buffer
+  // (the last at bb = 1, its operands taken by that MFMA) has then been
+  // waited on by its wave, so the buffer is free once the barrier is
+  // passed.  The DMA of stage s+4 into it starts right there: the first
+  // half of its ops goes out in blocks 2 and 3 of stage s, the second half
+  // in blocks 0 and 1 of stage s+1, 11-14 blocks before its hand-off.
+  // Waves must never pass a hand-off with a read of the freed buffer still
+  // outstanding.
+  v16i c_cur;
+  v32f f_cur;
+  Frag fr;
+  ScaleRaw sr;
+  // Ops j < kHalf of a stage form its first half.  At the hand-off of
+  // stage s+1, the ops of stages s+2 and s+3 may still be outstanding.
+  constexpr int kHalf = (St::OPS + 1) / 2;
+  constexpr int kMidOps = 2 * St::OPS;
+  // Stage s reads buffers buf (its own) and buf1 (stage s+1's) and issues
+  // the second half of stage sa (into abuf) and the first half of stage sb
+  // (into bbuf).
+  auto compute = [&](int s, St &buf, St &buf1, int sa, St &abuf, const Offsets &aof, int sb,
+                     St &bbuf, const Offsets &bof) __attribute__((always_inline)) {
     const int kb = s * kStageBlocks;
-    v32f fac[2];
-    fac[0] = scales(kb, buf, 0);
-    v16i c = dots(buf, 0);
     static_for<kStageBlocks>([&](auto BB) __attribute__((always_inline)) {
       constexpr int bb = decltype(BB)::value;
-      v16i cn = c;
-      if constexpr (bb + 1 < kStageBlocks) cn = dots(buf, bb + 1);
-      if constexpr (bb == 0) fac[1] = scales(kb, buf, 1);
+      const v16i c_next = dots(fr);
+      v32f f_next;
+      if constexpr ((bb & 1) != 0) f_next = scale_tile(bb == 1 ? kb : kb + kStageBlocks, sr, bb == 1 ? 1 : 0);
+      if constexpr (bb == 2) {
+        wait_vmcnt<kMidOps>();
+        stage_barrier();
+      }
+      if constexpr (bb < 2) {
+        fr = read_frag(buf, bb + 2);
+      } else {
+        fr = read_frag(buf1, bb - 2);
+      }
+      if constexpr (bb == 0) sr = read_scales(kb, buf, 1);
+      if constexpr (bb == 2) sr = read_scales(kb + kStageBlocks, buf1, 0);
       static_for<St::OPS>([&](auto J) __attribute__((always_inline)) {
-        if constexpr (decltype(J)::value * kStageBlocks / St::OPS == bb)
-          issue_op(sn, nbuf, J, of);
+        constexpr int j = decltype(J)::value;
+        if constexpr (j >= kHalf && bb < 2) {
+          if constexpr ((j - kHalf) * 2 / (St::OPS - kHalf) == bb) issue_op(sa, abuf, J, aof);
+        }
+        if constexpr (j < kHalf && bb >= 2) {
+          if constexpr (2 + j * 2 / kHalf == bb) issue_op(sb, bbuf, J, bof);
+        }
       });
-      const v32f &f2 = fac[bb >> 1];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float dotf = (float)c[v];
-        const float f = f2[16 * (bb & 1) + v];
+        const float dotf = (float)c_cur[v];
+        const float f = f_cur[16 * (bb & 1) + v];
         if (FMA) {
           acc[v] = __builtin_fmaf(dotf, f, acc[v]);
         } else {
@@ -453,21 +512,38 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
       // and pile up their results in registers.
 #pragma unroll
       for (int v = 0; v < 16; ++v) asm volatile("" : "+v"(acc[v]));
-      c = cn;
+      __builtin_amdgcn_sched_barrier(0);
+      c_cur = c_next;
+      if constexpr ((bb & 1) != 0) f_cur = f_next;
     });
   };
 
   // Every DMA is unconditional: a branch around one makes the compiler's
   // wait tracking merge states and wait for all loads before the next LDS
   // read.  The DMA stream runs on across tiles: the last group of stages
-  // issues the next tile's first NST - 1 stages, so their latency hides
-  // behind that group and this tile's epilogue.  After the last tile they
-  // reload the tile's own first stages into buffers nobody reads again.
+  // issues the next tile's first NST stages, so their latency hides behind
+  // that group and this tile's epilogue.  After the last tile they reload
+  // the tile's own last stage into buffers nobody reads again.
+  static_assert(NST == 4, "the block pipeline runs a ring of four stages");
   static_assert(kPassBlocks / kStageBlocks % NST == 0, "stages per unit");
   const int last = stages - 1;
   Offsets cur = tile_offsets(m_tile, n0);
 #pragma unroll
   for (int i = 0; i < NST - 1; ++i) issue(min(i, last), stage(i), cur);
+  static_for<kHalf>([&](auto J) __attribute__((always_inline)) {
+    issue_op(min(NST - 1, last), stage(NST - 1), J, cur);
+  });
+  // pipeline prologue: stage 0 handed off, block 0's MFMA and its pair's
+  // scale tile issued, block 1's operands read
+  wait_vmcnt<(NST - 2) * St::OPS + kHalf>();
+  stage_barrier();
+  {
+    const Frag f0 = read_frag(stage(0), 0);
+    fr = read_frag(stage(0), 1);
+    const ScaleRaw r0 = read_scales(0, stage(0), 0);
+    c_cur = dots(f0);
+    f_cur = scale_tile(0, r0, 0);
+  }
 
   for (;;) {
     const int id_next = PERSIST ? next_tile(id + G) : total;
@@ -479,7 +555,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
 
     // One group of NST stages (static buffer indices).  The last group is
-    // peeled off when it differs: with PERSIST its stages s + NST - 1 past
+    // peeled off when it differs: with PERSIST the stages it issues past
     // the end are the next tile's, and with the SwiGLU multiply it
     // prefetches the gate values.  Without PERSIST (one tile per
     // workgroup) those stages reload the tile's last stage into buffers
@@ -493,15 +569,19 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
 #pragma unroll
       for (int i = 0; i < NST; ++i) {
         const int s = s0 + i;
-        // NST - 2 stages were issued after stage s
-        wait_vmcnt<(NST - 2) * St::OPS>();
-        stage_barrier();
-        // every wave is past stage s-1: its buffer takes stage s+NST-1
-        St &nbuf = stage((i + NST - 1) % NST);
-        if (PERSIST && is_last && i > 0)
-          compute(s, stage(i), i - 1, nbuf, nxt);
-        else
-          compute(s, stage(i), min(s + NST - 1, last), nbuf, cur);
+        // stage s finishes stage s+3's DMA (into stage s-1's buffer) and
+        // starts stage s+4's (into its own)
+        St &abuf = stage((i + NST - 1) % NST);
+        St &buf1 = stage((i + 1) % NST);
+        if (PERSIST && is_last) {
+          if (i == 0)
+            compute(s, stage(i), buf1, last, abuf, cur, 0, stage(i), nxt);
+          else
+            compute(s, stage(i), buf1, i - 1, abuf, nxt, i, stage(i), nxt);
+        } else {
+          compute(s, stage(i), buf1, min(s + NST - 1, last), abuf, cur, min(s + NST, last),
+                  stage(i), cur);
+        }
       }
     };
     if constexpr (PERSIST || (EPI & 24) != 0) {
