@@ -41,10 +41,11 @@ extern "C" {
 
 /* Version of this C ABI (1: f32 entries; 2: bf16 twins and all four
  * activations; 3: linear + residual add; 4: reference platform switch,
- * weight budget, graph staleness check, grouped linears).  The model ABI of
+ * weight budget, graph staleness check, grouped linears; 5: RMSNorm and
+ * RMSNorm + grouped linears).  The model ABI of
  * the AOT library (llmcp_model_abi_version() == 2,
  * include/llmcp/Support/AotAbi.h:12) is not changed by this library. */
-#define LLMCP_Q8_ABI_VERSION 4
+#define LLMCP_Q8_ABI_VERSION 5
 
 enum llmcp_q8_status {
   LLMCP_Q8_OK = 0,
@@ -125,6 +126,24 @@ typedef struct {
   int64_t sizes[1];
   int64_t strides[1];
 } llmcp_memref_i64_1d;
+
+/* Norm weight vectors (memref<Hxf32> / memref<Hxbf16>, the arena's F32 and
+ * BF16 tensors). */
+typedef struct {
+  float *base;
+  float *data;
+  int64_t offset;
+  int64_t sizes[1];
+  int64_t strides[1];
+} llmcp_memref_f32_1d;
+
+typedef struct {
+  uint16_t *base;
+  uint16_t *data;
+  int64_t offset;
+  int64_t sizes[1];
+  int64_t strides[1];
+} llmcp_memref_bf16_1d;
 
 typedef struct llmcp_q8_ctx llmcp_q8_ctx;
 
@@ -257,6 +276,47 @@ int llmcp_q8_linear_group_bf16(llmcp_q8_ctx *ctx,
                                llmcp_memref_bf16_2d *const *outputs,
                                const int32_t *activations,
                                int32_t execution_mode);
+
+/* llmcp.rms_norm over the rows of x [M, H] (H % 32 == 0) with weight w [H],
+ * as the reference lowers it for decode rows (DecodeNormalization.cpp:71-154,
+ * :160-171) and for prefill (LowerToLinalg.cpp:245-300), bit for bit: per
+ * row, sum = sum + x*x in index order in f32, rstd = 1 / sqrt(sum / H + eps)
+ * (math.rsqrt as --convert-math-to-llvm lowers it), y = (x * rstd) * w, with
+ * w + 1 in place of w when zero_centered; a bf16 y is rounded to nearest
+ * even.  eps is the op's f64 attribute as f32.  The serial sum costs about
+ * one dependent add per element (rows run in parallel).  The weight must be
+ * 16 B aligned (8 B for bf16); declines otherwise. */
+int llmcp_q8_rmsnorm(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                     const llmcp_memref_f32_1d *weight, float eps,
+                     int32_t zero_centered, llmcp_memref_f32_2d *output);
+
+/* bf16 rows and weight (the real model's hidden state and norm tensors). */
+int llmcp_q8_rmsnorm_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                          const llmcp_memref_bf16_1d *weight, float eps,
+                          int32_t zero_centered, llmcp_memref_bf16_2d *output);
+
+/* The RMSNorm and the linears it feeds (input_layernorm -> in_proj_qkv/z/
+ * a/b or q/k/v, post_attention_layernorm -> gate/up; ModelBuilder.cpp:
+ * 225-236, :284-294): `normed` receives the norm's rows, then the group runs
+ * on them as llmcp_q8_linear_group does.  For several rows the norm also
+ * writes the rows' Q8_1 for the GEMMs (the activation quantization fused
+ * into the norm's epilogue, no separate quantization); one row goes to the
+ * grouped GEMV, which quantizes it inside each workgroup.  Results equal
+ * llmcp_q8_rmsnorm followed by llmcp_q8_linear_group bit for bit. */
+int llmcp_q8_rmsnorm_linear_group(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                                  const llmcp_memref_f32_1d *norm_weight, float eps,
+                                  int32_t zero_centered, llmcp_memref_f32_2d *normed,
+                                  int32_t count, const llmcp_memref_i8_1d *const *weights,
+                                  llmcp_memref_f32_2d *const *outputs,
+                                  const int32_t *activations, int32_t execution_mode);
+
+/* bf16 rows, norm weight, normed rows and outputs. */
+int llmcp_q8_rmsnorm_linear_group_bf16(
+    llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+    const llmcp_memref_bf16_1d *norm_weight, float eps, int32_t zero_centered,
+    llmcp_memref_bf16_2d *normed, int32_t count, const llmcp_memref_i8_1d *const *weights,
+    llmcp_memref_bf16_2d *const *outputs, const int32_t *activations,
+    int32_t execution_mode);
 
 /* Fused SwiGLU hidden: h = silu(x . Wg^T) * (x . Wu^T), the pair
  * `linear{activation=silu}` + `mul` that FuseSiluMul produces

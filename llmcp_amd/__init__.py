@@ -82,6 +82,8 @@ EXPORTS = [
     "_mlir_ciface_llmcp_q8_linear_add", "_mlir_ciface_llmcp_q8_linear_add_bf16",
     "llmcp_q8_linear_group", "llmcp_q8_linear_group_bf16",
     "_mlir_ciface_llmcp_q8_linear_group3", "_mlir_ciface_llmcp_q8_linear_group4",
+    "llmcp_q8_rmsnorm", "llmcp_q8_rmsnorm_bf16", "llmcp_q8_rmsnorm_linear_group",
+    "llmcp_q8_rmsnorm_linear_group_bf16",
 ]
 
 
@@ -165,6 +167,11 @@ def lib():
         "llmcp_q8_linear_group_bf16": (I, [P, P, I32, P, P, P, I32]),
         "_mlir_ciface_llmcp_q8_linear_group3": (I32, [P] * 7 + [I32] * 4),
         "_mlir_ciface_llmcp_q8_linear_group4": (I32, [P] * 9 + [I32] * 5),
+        "llmcp_q8_rmsnorm": (I, [P, P, P, ctypes.c_float, I32, P]),
+        "llmcp_q8_rmsnorm_bf16": (I, [P, P, P, ctypes.c_float, I32, P]),
+        "llmcp_q8_rmsnorm_linear_group": (I, [P, P, P, ctypes.c_float, I32, P, I32, P, P, P, I32]),
+        "llmcp_q8_rmsnorm_linear_group_bf16": (I, [P, P, P, ctypes.c_float, I32, P, I32, P, P,
+                                                   P, I32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -401,6 +408,34 @@ class Context:
         acts = (ctypes.c_int32 * n)(*[ACT[a] for a in (activations or ["none"] * n)])
         check(self._entry("llmcp_q8_linear_group", dtype)(
             self.handle, ctypes.byref(xi), n, wp, yp, acts, MODE[mode]))
+
+    def rmsnorm(self, x, w, y, m, h, eps=1e-6, zero_centered=False, dtype="f32"):
+        """y = RMSNorm(x) with weight w [h] (x, w and y of dtype)."""
+        xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, h)
+        yo = f32_memref(y.ptr if hasattr(y, "ptr") else y, m, h)
+        wv = i8_memref(w.ptr if hasattr(w, "ptr") else w, h)
+        check(self._entry("llmcp_q8_rmsnorm", dtype)(
+            self.handle, ctypes.byref(xi), ctypes.byref(wv), float(eps),
+            1 if zero_centered else 0, ctypes.byref(yo)))
+
+    def rmsnorm_linear_group(self, x, norm_w, normed, weights, outputs, m, eps=1e-6,
+                             zero_centered=False, activations=None, mode="decode",
+                             dtype="f32"):
+        """normed = RMSNorm(x); outputs[i] = act_i(normed . W_i^T)."""
+        n = len(weights)
+        k = weights[0].cols
+        xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, k)
+        no = f32_memref(normed.ptr if hasattr(normed, "ptr") else normed, m, k)
+        wv = i8_memref(norm_w.ptr if hasattr(norm_w, "ptr") else norm_w, k)
+        ws = [w.memref() for w in weights]
+        ys = [f32_memref(y.ptr if hasattr(y, "ptr") else y, m, w.rows)
+              for y, w in zip(outputs, weights)]
+        wp = (ctypes.c_void_p * n)(*[ctypes.addressof(d) for d in ws])
+        yp = (ctypes.c_void_p * n)(*[ctypes.addressof(d) for d in ys])
+        acts = (ctypes.c_int32 * n)(*[ACT[a] for a in (activations or ["none"] * n)])
+        check(self._entry("llmcp_q8_rmsnorm_linear_group", dtype)(
+            self.handle, ctypes.byref(xi), ctypes.byref(wv), float(eps),
+            1 if zero_centered else 0, ctypes.byref(no), n, wp, yp, acts, MODE[mode]))
 
     def swiglu(self, x, wg, wu, h, m, mode="decode", dtype="f32"):
         xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, wg.cols)

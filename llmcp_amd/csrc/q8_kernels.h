@@ -128,6 +128,17 @@ hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
                                  int64_t ldx, int64_t cols, int8_t *qa,
                                  float *sa, int64_t blocks_pad, hipStream_t s);
 
+// RMSNorm of m rows of width h (h % 32 == 0) with weight w [h]: y = (x *
+// rstd) * (w or w + 1), each row's sum of squares serial in index order.
+// x and y share their type (f32 or bf16); w is f32 or bf16.  qmode 1 also
+// writes y's Q8_1 in the dense layout (row r at r * blocks_pad * 32, scales
+// at r * blocks_pad), qmode 2 in the tiled layout of launch_quantize_tiled.
+hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
+                          int64_t h, const void *w, bool w_bf16, float eps,
+                          bool zero_centered, void *y, bool y_bf16, int64_t ldy,
+                          int8_t *qa, float *sa, int64_t blocks_pad, int qmode,
+                          hipStream_t s);
+
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             const uint8_t *table, int64_t rows, int64_t cols,
                             void *out, bool out_bf16, int64_t ldo,

@@ -289,6 +289,146 @@ __global__ __launch_bounds__(256) void quantize_tiles_kernel(
 }
 
 
+// RMSNorm of up to 64 rows per workgroup, each row on its own as the
+// reference reduces it (DecodeNormalization.cpp:93-107 and :124-154 for
+// decode rows, LowerToLinalg.cpp:245-300 for prefill: the same arithmetic):
+// sum = sum + x*x over the row in index order, each step rounded to f32;
+// rstd = 1 / sqrt(sum / H + eps) with an IEEE square root and division
+// (math.rsqrt under --convert-math-to-llvm); y = (x * rstd) * w', w' = w, or
+// w + 1 when zero-centered; bf16 outputs rounded to nearest even.
+//
+// The serial sum is one dependent add per element, in lane r of wave 0 for
+// row r.  Waves 1-3 stage the squares of the next 128-column chunk of the
+// 64 rows in LDS while wave 0 folds the current one (rows padded to 129
+// floats, so the 64 lanes read 64 banks).  Then all waves write y and,
+// with QMODE, its Q8_1 (the quantizer's arithmetic, quantize_block8, on
+// the values as stored): QMODE 1 the dense [m][blocks_pad * 32] layout,
+// QMODE 2 the GEMM's tiled layout (rows up to the 32-row tile's end and
+// blocks past H written as zeros).  Requires h % 32 == 0.
+constexpr int kNormRows = 64;
+constexpr int kNormChunk = 128;
+
+template <bool XB, bool WB, bool YB, int QMODE>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(
+    const void *__restrict__ x, int64_t ldx, const void *__restrict__ w,
+    float eps, int zero_centered, int64_t m, int32_t h, void *__restrict__ y,
+    int64_t ldy, int8_t *__restrict__ qa, float *__restrict__ sa,
+    int32_t blocks_pad, int aligned) {
+  __shared__ float sq[2][kNormRows][kNormChunk + 1];
+  __shared__ float rstd_s[kNormRows];
+  const int64_t row0 = (int64_t)blockIdx.x * kNormRows;
+  const int rows = (int)min<int64_t>(kNormRows, m - row0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int chunks = (h + kNormChunk - 1) / kNormChunk;
+  auto load1 = [&](const void *p, int64_t i) -> float {
+    if constexpr (XB) return bf16_to_float(((const uint16_t *)p)[i]);
+    else return ((const float *)p)[i];
+  };
+  // squares of chunk c into buffer b: threads t0.. of nt
+  auto stage = [&](int c, int b, int t0, int nt) {
+    const int c0 = c * kNormChunk, cw = min(kNormChunk, h - c0);
+    for (int e = (int)threadIdx.x - t0; e < rows * cw; e += nt) {
+      const int r = e / cw, j = e - r * cw;
+      const float v = load1(x, (row0 + r) * ldx + c0 + j);
+      sq[b][r][j] = v * v;
+    }
+  };
+  stage(0, 0, 0, 256);
+  __syncthreads();
+  float sum = 0.0f;
+  for (int c = 0; c < chunks; ++c) {
+    if (wave == 0) {
+      if (lane < rows) {
+        const int cw = min(kNormChunk, h - c * kNormChunk);
+        const float *q = sq[c & 1][lane];
+        int j = 0;
+        for (; j + 16 <= cw; j += 16) {
+          float t[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) t[u] = q[j + u];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) sum = sum + t[u];
+        }
+        for (; j < cw; ++j) sum = sum + q[j];
+      }
+    } else if (c + 1 < chunks) {
+      stage(c + 1, (c + 1) & 1, 64, 192);
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && lane < rows) {
+    const float mean = sum / (float)h;
+    const float var = mean + eps;
+    rstd_s[lane] = 1.0f / sqrtf(var);
+  }
+  __syncthreads();
+
+  // y and its Q8_1: 8 lanes per (row, block), the same trip count in every
+  // lane (quantize_block8 works across the wave)
+  const int blocks = h / kBlock;
+  const int64_t tile_end = (m + 31) / 32 * 32;
+  const int out_rows = QMODE == 2 ? (int)min<int64_t>(kNormRows, tile_end - row0) : rows;
+  const int nb = QMODE != 0 ? blocks_pad : blocks;
+  const int units = out_rows * nb;
+  const int p = threadIdx.x & 7;
+  for (int u0 = 0; u0 < units; u0 += 32) {
+    const int unit = u0 + (threadIdx.x >> 3);
+    const int r = min(unit / nb, max(out_rows - 1, 0));
+    const int b = unit - (unit / nb) * nb;
+    const int64_t row = row0 + r;
+    const bool live = unit < units;
+    const bool valid = live && r < rows && b < blocks;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) {
+      const float4 xv = load_act4(x, row * ldx + b * kBlock + 4 * p, XB, aligned != 0);
+      float4 wv = load_act4(w, (int64_t)b * kBlock + 4 * p, WB, true);
+      if (zero_centered) {
+        wv.x = wv.x + 1.0f;
+        wv.y = wv.y + 1.0f;
+        wv.z = wv.z + 1.0f;
+        wv.w = wv.w + 1.0f;
+      }
+      const float rs = rstd_s[r];
+      v.x = (xv.x * rs) * wv.x;
+      v.y = (xv.y * rs) * wv.y;
+      v.z = (xv.z * rs) * wv.z;
+      v.w = (xv.w * rs) * wv.w;
+      if constexpr (YB) {
+        const uint16_t b0 = float_to_bf16(v.x), b1 = float_to_bf16(v.y),
+                       b2 = float_to_bf16(v.z), b3 = float_to_bf16(v.w);
+        uint16_t *yp = (uint16_t *)y + row * ldy + b * kBlock + 4 * p;
+        yp[0] = b0;
+        yp[1] = b1;
+        yp[2] = b2;
+        yp[3] = b3;
+        v = make_float4(bf16_to_float(b0), bf16_to_float(b1), bf16_to_float(b2),
+                        bf16_to_float(b3));
+      } else {
+        float *yp = (float *)y + row * ldy + b * kBlock + 4 * p;
+        yp[0] = v.x;
+        yp[1] = v.y;
+        yp[2] = v.z;
+        yp[3] = v.w;
+      }
+    }
+    if constexpr (QMODE != 0) {
+      int32_t q;
+      float sc;
+      quantize_block8(v, valid, &q, &sc);
+      if (live) {
+        if constexpr (QMODE == 1) {
+          *(int32_t *)(qa + row * ((int64_t)blocks_pad * kBlock) + b * kBlock + 4 * p) = q;
+          if (p == 0) sa[row * blocks_pad + b] = sc;
+        } else {
+          const int64_t tile = (row >> 5) * blocks_pad + b;
+          *(int32_t *)(qa + tile * 1024 + (row & 31) * kBlock + 4 * p) = q;
+          if (p == 0) sa[tile * 32 + (row & 31)] = sc;
+        }
+      }
+    }
+  }
+}
+
 // First-maximum argmax of one f32 row already in HBM (the last row of a
 // prefill lm_head's logits): the same keys as the GEMV's fused argmax,
 // folded into the same slots, so argmax_reduce_kernel finishes it.  A grid
@@ -581,6 +721,35 @@ hipError_t launch_argmax_reduce(unsigned long long *slots, int64_t *out,
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(1024), 0, s, slots,
                      out);
   return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
+                          int64_t h, const void *w, bool w_bf16, float eps,
+                          bool zero_centered, void *y, bool y_bf16, int64_t ldy,
+                          int8_t *qa, float *sa, int64_t blocks_pad, int qmode,
+                          hipStream_t s) {
+  if (h % kBlock != 0 || m <= 0 || (qmode != 0 && blocks_pad * kBlock < h))
+    return hipErrorInvalidValue;
+  if ((uintptr_t)w % (w_bf16 ? 8 : 16) != 0) return hipErrorInvalidValue;
+  const int64_t esz = x_bf16 ? 2 : 4;
+  const int aligned = ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
+  const dim3 grid((unsigned)((m + kNormRows - 1) / kNormRows));
+  const int zc = zero_centered ? 1 : 0;
+  const int32_t hh = (int32_t)h, bp = (int32_t)blocks_pad;
+#define LLMCP_NORM(XB, WB, YB, Q)                                                         \
+  if (x_bf16 == XB && w_bf16 == WB && y_bf16 == YB && qmode == Q) {                       \
+    hipLaunchKernelGGL((rmsnorm_kernel<XB, WB, YB, Q>), grid, dim3(256), 0, s, x, ldx, w, \
+                       eps, zc, m, hh, y, ldy, qa, sa, bp, aligned);                      \
+    return hipGetLastError();                                                            \
+  }
+  LLMCP_NORM(false, false, false, 0) LLMCP_NORM(false, false, false, 1)
+  LLMCP_NORM(false, false, false, 2) LLMCP_NORM(true, true, true, 0)
+  LLMCP_NORM(true, true, true, 1) LLMCP_NORM(true, true, true, 2)
+  LLMCP_NORM(false, true, false, 0) LLMCP_NORM(false, true, false, 1)
+  LLMCP_NORM(false, true, false, 2) LLMCP_NORM(true, false, true, 0)
+  LLMCP_NORM(true, false, true, 1) LLMCP_NORM(true, false, true, 2)
+#undef LLMCP_NORM
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,

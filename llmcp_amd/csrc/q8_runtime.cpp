@@ -195,6 +195,23 @@ bool view_of(const M *d, bool bf16, Rows &r) {
   return true;
 }
 
+// A norm's weight vector (dense 1-D memref of f32 or bf16).
+struct NormWeight {
+  const void *data = nullptr;
+  int64_t len = 0;
+  bool bf16 = false;
+};
+
+template <class D>
+static bool norm_weight_of(const D *d, bool bf16, NormWeight &nw) {
+  if (!d || !d->data || d->sizes[0] < 0 || (d->sizes[0] > 1 && d->strides[0] != 1))
+    return false;
+  nw.data = d->data + d->offset;
+  nw.len = d->sizes[0];
+  nw.bf16 = bf16;
+  return true;
+}
+
 template <typename T>
 int grow(llmcp_q8_ctx *ctx, T *&ptr, uint64_t &have, uint64_t need,
          const char *what) {
@@ -1120,14 +1137,13 @@ static int linear_add_impl(llmcp_q8_ctx *ctx, const Rows &in,
 // q/k/v, ModelBuilder.cpp:229-236, :288-294): one input quantization and,
 // for one row, one GEMV launch over every weight's lane groups.  Results
 // equal the separate llmcp_q8_linear calls bit for bit.
-static int linear_group_impl(llmcp_q8_ctx *ctx, const Rows &in, int32_t count,
-                             const llmcp_memref_i8_1d *const *weights,
-                             const Rows *outs, const int32_t *acts,
-                             int32_t execution_mode) {
+static int linear_group_check(llmcp_q8_ctx *ctx, const Rows &in, int32_t count,
+                              const llmcp_memref_i8_1d *const *weights,
+                              const Rows *outs, const int32_t *acts,
+                              int32_t execution_mode, const Tensor **w) {
   if (count < 1 || count > kMaxGroup)
     return fail(LLMCP_Q8_EINVAL, "group of %d linears (1 to %d)", count,
                 kMaxGroup);
-  const Tensor *w[kMaxGroup];
   for (int32_t i = 0; i < count; ++i) {
     int rc = resolve_weight(ctx, weights[i], &w[i]);
     if (rc) return rc;
@@ -1136,16 +1152,22 @@ static int linear_group_impl(llmcp_q8_ctx *ctx, const Rows &in, int32_t count,
     if (act < LLMCP_Q8_ACT_NONE || act > LLMCP_Q8_ACT_SOFTPLUS)
       return fail(LLMCP_Q8_DECLINED, "unsupported activation %d", act);
   }
-  int rc = check_mode(execution_mode);
-  if (rc) return rc;
+  return check_mode(execution_mode);
+}
+
+// The checked group on the current device.  `prequantized`: for several
+// rows, the workspace already holds the rows' Q8_1 in the tiled layout
+// (written by the RMSNorm that produced them).
+static int linear_group_run(llmcp_q8_ctx *ctx, const Rows &in, int32_t count,
+                            const Tensor *const *w, const Rows *outs,
+                            const int32_t *acts, bool prequantized) {
   const int64_t m = in.rows;
-  if (m == 0) return LLMCP_Q8_OK;
-  if ((rc = set_device(ctx))) return rc;
+  int rc = LLMCP_Q8_OK;
   auto act_of = [&](int32_t i) { return acts ? acts[i] : LLMCP_Q8_ACT_NONE; };
   if (m > 1) {
     // one quantization of the input rows, then each weight's GEMM
     Workspace ws = ctx_workspace(ctx);
-    if ((rc = gemm_quantize(ctx, in, w[0], ws))) return rc;
+    if (!prequantized && (rc = gemm_quantize(ctx, in, w[0], ws))) return rc;
     for (int32_t i = 0; i < count; ++i)
       if ((rc = gemm_launch(ctx, ws, m, w[i], outs[i], act_of(i), nullptr, 0)))
         return rc;
@@ -1186,6 +1208,94 @@ static int linear_group_impl(llmcp_q8_ctx *ctx, const Rows &in, int32_t count,
   hipError_t e = launch_gemv(l, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "grouped gemv launch");
   return LLMCP_Q8_OK;
+}
+
+static int linear_group_impl(llmcp_q8_ctx *ctx, const Rows &in, int32_t count,
+                             const llmcp_memref_i8_1d *const *weights,
+                             const Rows *outs, const int32_t *acts,
+                             int32_t execution_mode) {
+  const Tensor *w[kMaxGroup];
+  int rc = linear_group_check(ctx, in, count, weights, outs, acts, execution_mode, w);
+  if (rc) return rc;
+  if (in.rows == 0) return LLMCP_Q8_OK;
+  if ((rc = set_device(ctx))) return rc;
+  return linear_group_run(ctx, in, count, w, outs, acts, false);
+}
+
+// ------------------------------------------------------------- RMSNorm --
+// The path's upstream neighbour: llmcp.rms_norm as the reference lowers it
+// for decode rows (DecodeNormalization.cpp:71-154, :160-171) and for
+// prefill (LowerToLinalg.cpp:245-300), one row at a time with a serial f32
+// sum of squares.  Bit-exact; the serial sum bounds it at about one
+// dependent add per element (rows run in parallel).
+
+
+static int check_norm(const Rows &in, const NormWeight &nw, const Rows &out) {
+  if (out.rows != in.rows || out.cols != in.cols)
+    return fail(LLMCP_Q8_DECLINED, "RMSNorm output must be [M, H] like its input");
+  if (nw.len != in.cols)
+    return fail(LLMCP_Q8_DECLINED, "RMSNorm weight has %lld values for H = %lld",
+                (long long)nw.len, (long long)in.cols);
+  if (in.cols % kBlock != 0)
+    return fail(LLMCP_Q8_DECLINED, "RMSNorm width %lld is not a multiple of 32",
+                (long long)in.cols);
+  if ((uintptr_t)nw.data % (nw.bf16 ? 8 : 16) != 0)
+    return fail(LLMCP_Q8_DECLINED, "RMSNorm weight must be %d B aligned",
+                nw.bf16 ? 8 : 16);
+  return LLMCP_Q8_OK;
+}
+
+static int rmsnorm_impl(llmcp_q8_ctx *ctx, const Rows &in, const NormWeight &nw,
+                        float eps, int32_t zero_centered, const Rows &out) {
+  int rc = check_norm(in, nw, out);
+  if (rc) return rc;
+  if (in.rows == 0) return LLMCP_Q8_OK;
+  if ((rc = set_device(ctx))) return rc;
+  hipError_t e = launch_rmsnorm(in.data, in.bf16, in.rows, in.ld, in.cols, nw.data,
+                                nw.bf16, eps, zero_centered != 0, out.data, out.bf16,
+                                out.ld, nullptr, nullptr, 0, 0, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
+  return LLMCP_Q8_OK;
+}
+
+// RMSNorm, then linears on the normed rows (the model builder's
+// input_layernorm -> in_proj_qkv/z/a/b or q/k/v, post_attention_layernorm
+// -> gate/up; ModelBuilder.cpp:225-236, :284-294).  For several rows the
+// norm's epilogue writes the rows' Q8_1 for the GEMMs (no separate
+// quantization); one row goes through the grouped GEMV, which quantizes
+// the normed row in each workgroup.  Bit-exact to llmcp_q8_rmsnorm followed
+// by llmcp_q8_linear_group.
+static int rmsnorm_group_impl(llmcp_q8_ctx *ctx, const Rows &in, const NormWeight &nw,
+                              float eps, int32_t zero_centered, const Rows &normed,
+                              int32_t count, const llmcp_memref_i8_1d *const *weights,
+                              const Rows *outs, const int32_t *acts,
+                              int32_t execution_mode) {
+  int rc = check_norm(in, nw, normed);
+  if (rc) return rc;
+  const Tensor *w[kMaxGroup];
+  if ((rc = linear_group_check(ctx, normed, count, weights, outs, acts, execution_mode, w)))
+    return rc;
+  const int64_t m = in.rows;
+  if (m == 0) return LLMCP_Q8_OK;
+  if ((rc = set_device(ctx))) return rc;
+  if (m == 1) {
+    hipError_t e = launch_rmsnorm(in.data, in.bf16, 1, in.ld, in.cols, nw.data, nw.bf16,
+                                  eps, zero_centered != 0, normed.data, normed.bf16,
+                                  normed.ld, nullptr, nullptr, 0, 0, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
+    return linear_group_run(ctx, normed, count, w, outs, acts, false);
+  }
+  const int64_t nblk = passes_for(in.cols) * kPassBlocks;
+  const int64_t row_tiles = (m + 31) / 32;
+  Workspace ws = ctx_workspace(ctx);
+  if ((rc = reserve(ctx, ws, (uint64_t)(row_tiles * 32 * nblk * kBlock),
+                    (uint64_t)(row_tiles * 32 * nblk * 4))))
+    return rc;
+  hipError_t e = launch_rmsnorm(in.data, in.bf16, m, in.ld, in.cols, nw.data, nw.bf16, eps,
+                                zero_centered != 0, normed.data, normed.bf16, normed.ld,
+                                ws.qa, ws.sa, nblk, 2, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
+  return linear_group_run(ctx, normed, count, w, outs, acts, true);
 }
 
 static int swiglu_impl(llmcp_q8_ctx *ctx, const Rows &in,
@@ -1462,6 +1572,82 @@ int llmcp_q8_linear_group_bf16(llmcp_q8_ctx *ctx,
         return fail(LLMCP_Q8_DECLINED, kDenseMsg);
     return linear_group_impl(ctx, in, count, weights, outs, activations,
                              execution_mode);
+  });
+}
+
+int llmcp_q8_rmsnorm(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                     const llmcp_memref_f32_1d *weight, float eps,
+                     int32_t zero_centered, llmcp_memref_f32_2d *output) {
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    NormWeight nw;
+    if (!view_of(input, false, in) || !view_of(output, false, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    if (!norm_weight_of(weight, false, nw))
+      return fail(LLMCP_Q8_DECLINED, "RMSNorm weight must be a dense vector");
+    return rmsnorm_impl(ctx, in, nw, eps, zero_centered, out);
+  });
+}
+
+int llmcp_q8_rmsnorm_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                          const llmcp_memref_bf16_1d *weight, float eps,
+                          int32_t zero_centered, llmcp_memref_bf16_2d *output) {
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, out;
+    NormWeight nw;
+    if (!view_of(input, true, in) || !view_of(output, true, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    if (!norm_weight_of(weight, true, nw))
+      return fail(LLMCP_Q8_DECLINED, "RMSNorm weight must be a dense vector");
+    return rmsnorm_impl(ctx, in, nw, eps, zero_centered, out);
+  });
+}
+
+int llmcp_q8_rmsnorm_linear_group(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                                  const llmcp_memref_f32_1d *norm_weight, float eps,
+                                  int32_t zero_centered, llmcp_memref_f32_2d *normed,
+                                  int32_t count, const llmcp_memref_i8_1d *const *weights,
+                                  llmcp_memref_f32_2d *const *outputs,
+                                  const int32_t *activations, int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!ctx || !weights || !outputs) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (count < 1 || count > kMaxGroup)
+      return fail(LLMCP_Q8_EINVAL, "group of %d linears (1 to %d)", count, kMaxGroup);
+    Rows in, nr, outs[kMaxGroup];
+    NormWeight nw;
+    if (!view_of(input, false, in) || !view_of(normed, false, nr))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    for (int32_t i = 0; i < count; ++i)
+      if (!view_of(outputs[i], false, outs[i])) return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    if (!norm_weight_of(norm_weight, false, nw))
+      return fail(LLMCP_Q8_DECLINED, "RMSNorm weight must be a dense vector");
+    return rmsnorm_group_impl(ctx, in, nw, eps, zero_centered, nr, count, weights, outs,
+                              activations, execution_mode);
+  });
+}
+
+int llmcp_q8_rmsnorm_linear_group_bf16(
+    llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+    const llmcp_memref_bf16_1d *norm_weight, float eps, int32_t zero_centered,
+    llmcp_memref_bf16_2d *normed, int32_t count, const llmcp_memref_i8_1d *const *weights,
+    llmcp_memref_bf16_2d *const *outputs, const int32_t *activations,
+    int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!ctx || !weights || !outputs) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (count < 1 || count > kMaxGroup)
+      return fail(LLMCP_Q8_EINVAL, "group of %d linears (1 to %d)", count, kMaxGroup);
+    Rows in, nr, outs[kMaxGroup];
+    NormWeight nw;
+    if (!view_of(input, true, in) || !view_of(normed, true, nr))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    for (int32_t i = 0; i < count; ++i)
+      if (!view_of(outputs[i], true, outs[i])) return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    if (!norm_weight_of(norm_weight, true, nw))
+      return fail(LLMCP_Q8_DECLINED, "RMSNorm weight must be a dense vector");
+    return rmsnorm_group_impl(ctx, in, nw, eps, zero_centered, nr, count, weights, outs,
+                              activations, execution_mode);
   });
 }
 

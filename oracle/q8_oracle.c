@@ -34,6 +34,11 @@
  *                       nearest even) on ties, subnormals, inf and NaN.
  *   argmax              numpy argmax (first maximum), std::max_element rule.
  *   embedding           exact dequantization from the unpacked matrix.
+ *   rmsnorm             the serial sum against numpy's sequential float32
+ *                       cumsum (the last partial sum), rstd against float32
+ *                       1/np.sqrt, constructed rows whose pairwise or float64
+ *                       sum differs from the serial one, and the closed form
+ *                       of a constant row (y = w * sign(x) within 1 ulp).
  */
 #include <math.h>
 #include <stdint.h>
@@ -123,6 +128,10 @@ uint16_t oracle_f32_to_bf16(float value) {
     return (uint16_t)((x >> 16) | 0x40u);
   uint32_t rounding = 0x7fffu + ((x >> 16) & 1u);
   return (uint16_t)((x + rounding) >> 16);
+}
+
+void oracle_f32_to_bf16_batch(const float *x, int64_t n, uint16_t *out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_bf16(x[i]);
 }
 
 /* ------------------------------------------------------- weight Q8_0 ---- */
@@ -432,6 +441,40 @@ void oracle_embedding(const int64_t *tokens, int64_t count, const uint8_t *p4,
       uint16_t dbits = (uint16_t)(p4[so] | (p4[so + 1] << 8));
       int8_t q = (int8_t)p4[oracle_p4_qs_offset(row, c, cols)];
       out[t * cols + c] = (float)q * oracle_f16_to_f32(dbits);
+    }
+  }
+}
+
+/* RMSNorm of `rows` rows of width h, each row on its own (decode:
+ * DecodeNormalization.cpp:71-154 with groupSize = hidden, :160-171; prefill:
+ * RmsNormOpLowering, LowerToLinalg.cpp:245-300 -- the same arithmetic):
+ *   sum  = 0; for d in 0..h-1: sum = sum + x_d * x_d   (each step rounded)
+ *   mean = sum / (float)h;  var = mean + eps
+ *   rstd = 1 / sqrt(var)    (math.rsqrt as --convert-math-to-llvm lowers it:
+ *                            an IEEE square root, then an IEEE division)
+ *   y_d  = (x_d * rstd) * w'_d,  w' = w, or w + 1 when zero-centered.
+ * x, w and y are f32 here (bf16 operands are widened exactly by the
+ * caller, a bf16 result is rounded by it).  rstd_out (nullable) receives
+ * each row's rstd. */
+void oracle_rmsnorm(const float *x, int64_t rows, int64_t h, const float *w,
+                    float eps, int zero_centered, float *y, float *rstd_out) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *xr = x + r * h;
+    float sum = 0.0f;
+    for (int64_t d = 0; d < h; ++d) {
+      float sq = xr[d] * xr[d];
+      sum = sum + sq;
+    }
+    float mean = sum / (float)h;
+    float var = mean + eps;
+    float root = sqrtf(var);
+    float rstd = 1.0f / root;
+    if (rstd_out)
+      rstd_out[r] = rstd;
+    for (int64_t d = 0; d < h; ++d) {
+      float wd = zero_centered ? w[d] + 1.0f : w[d];
+      float t = xr[d] * rstd;
+      y[r * h + d] = t * wd;
     }
   }
 }

@@ -48,6 +48,7 @@ def _declare(L):
     L.oracle_f16_to_f32_batch.argtypes = [P, I64, P]
     L.oracle_f32_to_bf16.restype = ctypes.c_uint16
     L.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+    L.oracle_f32_to_bf16_batch.argtypes = [P, I64, P]
     L.oracle_quantize_row_q8_0.argtypes = [P, I64, P, P]
     L.oracle_dequantize_row_q8_0.argtypes = [P, P, I64, P]
     L.oracle_p4_qs_offset.restype = I64
@@ -72,6 +73,7 @@ def _declare(L):
     L.oracle_embedding.argtypes = [P, I64, P, I64, P]
     L.oracle_max_threads.restype = I
     L.oracle_set_threads.argtypes = [I]
+    L.oracle_rmsnorm.argtypes = [P, I64, I64, P, ctypes.c_float, I, P, P]
 
 
 def _ptr(a):
@@ -180,9 +182,10 @@ def softplus(v):
 
 def f32_to_bf16_bits(v):
     """Round to nearest even f32 -> bf16 (raw uint16 bits)."""
-    f = lib().oracle_f32_to_bf16
     v = _c(np.atleast_1d(v), np.float32)
-    return np.array([f(float(a)) for a in v.ravel()], np.uint16).reshape(v.shape)
+    out = np.zeros(v.shape, np.uint16)
+    lib().oracle_f32_to_bf16_batch(_ptr(v), v.size, _ptr(out))
+    return out
 
 
 def bf16_bits_to_f32(b):
@@ -223,6 +226,25 @@ def embedding(tokens, p4, cols):
     lib().oracle_embedding(_ptr(t), t.size, _ptr(_c(p4, np.uint8)), cols,
                            _ptr(out))
     return out
+
+
+def rmsnorm(x, w, eps, zero_centered=False, out_bf16=False, with_rstd=False):
+    """The reference RMSNorm of each row of x [M, H] (f32, or bf16 bit
+    patterns as uint16) with weight w [H] (f32 or bf16 bits); the result is
+    f32, or its bf16 bits when out_bf16."""
+    def widen(a):
+        a = np.asarray(a)
+        return bf16_bits_to_f32(a) if a.dtype == np.uint16 else a
+    x = _c(np.atleast_2d(widen(x)), np.float32)
+    w = _c(widen(w).ravel(), np.float32)
+    m, h = x.shape
+    y = np.zeros((m, h), np.float32)
+    r = np.zeros(m, np.float32)
+    lib().oracle_rmsnorm(_ptr(x), m, h, _ptr(w), float(np.float32(eps)),
+                         1 if zero_centered else 0, _ptr(y), _ptr(r))
+    if out_bf16:
+        y = f32_to_bf16_bits(y)
+    return (y, r) if with_rstd else y
 
 
 def max_threads():

@@ -1,0 +1,131 @@
+"""llmcp_q8_rmsnorm and llmcp_q8_rmsnorm_linear_group: the RMSNorm in front
+of the path (DecodeNormalization.cpp:71-154 for decode rows,
+LowerToLinalg.cpp:245-300 for prefill -- the same per-row arithmetic) and
+its fusion with the linears it feeds (input_layernorm -> in_proj_qkv/z/a/b,
+post_attention_layernorm -> gate/up; ModelBuilder.cpp:225-236, :284-294).
+Norm outputs must equal the oracle bit for bit; the group's outputs must
+equal separate llmcp_q8_linear calls on the normed rows, and the oracle."""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    a = np.asarray(a)
+    return a.view(np.uint32) if a.dtype == np.float32 else a.view(np.uint16)
+
+
+def same(a, b):
+    """Bit equality, with any NaN equal to any NaN (0 * inf has a different
+    payload on the GPU and on x86)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a)
+    return np.array_equal(nan, np.isnan(b)) and np.array_equal(bits(a[~nan]), bits(b[~nan]))
+
+
+def rows_and_weight(rng, m, h, dtype, oracle, scale=1.0):
+    x = (rng.standard_normal((m, h)) * scale).astype(np.float32)
+    w = (rng.standard_normal(h) * 0.1 + 1.0).astype(np.float32)
+    if dtype == "bf16":
+        return oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w)
+    return x, w
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("m,h", [(1, 2560), (1, 32), (3, 128), (64, 256), (65, 2560),
+                                 (200, 96), (1, 9216)])
+@pytest.mark.parametrize("zc", [False, True])
+def test_rmsnorm_bitwise(ctx, oracle, dtype, m, h, zc):
+    rng = np.random.default_rng(m * 7 + h + zc)
+    x, w = rows_and_weight(rng, m, h, dtype, oracle, scale=3.0)
+    et = np.float32 if dtype == "f32" else np.uint16
+    xd, wd = ctx.to_device(x), ctx.to_device(w)
+    yd = ctx.alloc(x.nbytes)
+    ctx.rmsnorm(xd, wd, yd, m, h, eps=1e-6, zero_centered=zc, dtype=dtype)
+    ref = oracle.rmsnorm(x, w, 1e-6, zero_centered=zc, out_bf16=dtype == "bf16")
+    assert np.array_equal(bits(ctx.to_host(yd, (m, h), et)), bits(ref))
+
+
+def test_rmsnorm_edge_rows(ctx, oracle):
+    """A zero row (rstd = 1/sqrt(eps)), subnormal and huge values (the sum
+    overflows to inf: rstd 0), a row of one large value among tiny ones (the
+    serial sum absorbs them), in place (y aliases x)."""
+    h = 256
+    x = np.zeros((6, h), np.float32)
+    x[1] = 1e-40
+    x[2] = 3e38
+    x[3, :] = 2.0 ** -12
+    x[3, 0] = 1.0
+    x[4] = np.linspace(-1e-3, 1e-3, h)
+    x[5] = np.where(np.arange(h) % 2, 1e19, -1e19)
+    w = np.linspace(0.5, 1.5, h).astype(np.float32)
+    xd, wd = ctx.to_device(x), ctx.to_device(w)
+    for eps in (1e-6, 0.0, 1e-5):
+        yd = ctx.to_device(x)
+        ctx.rmsnorm(yd, wd, yd, 6, h, eps=eps)
+        ref = oracle.rmsnorm(x, w, eps)
+        assert same(ctx.to_host(yd, (6, h), np.float32), ref), eps
+
+
+def test_rmsnorm_declines(ctx, q8):
+    h = 96
+    xd, yd = ctx.alloc(h * 4), ctx.alloc(h * 4)
+    wd = ctx.alloc(h * 4 + 16)
+    with pytest.raises(q8.Declined):  # width not a multiple of 32
+        ctx.rmsnorm(xd, wd, yd, 1, 100)
+    L = q8.lib()
+    xi, yo = q8.f32_memref(xd.ptr, 1, h), q8.f32_memref(yd.ptr, 1, h)
+    wv = q8.i8_memref(wd.ptr + 4, h)  # misaligned weight
+    rc = L.llmcp_q8_rmsnorm(ctx.handle, ctypes.byref(xi), ctypes.byref(wv), 1e-6, 0,
+                            ctypes.byref(yo))
+    assert rc == q8.DECLINED
+    wv = q8.i8_memref(wd.ptr, 64)  # weight length != H
+    rc = L.llmcp_q8_rmsnorm(ctx.handle, ctypes.byref(xi), ctypes.byref(wv), 1e-6, 0,
+                            ctypes.byref(yo))
+    assert rc == q8.DECLINED
+
+
+LINEAR_ATTN = [(8192, 2560), (4096, 2560), (32, 2560), (32, 2560)]
+MLP_IN = [(9216, 2560), (9216, 2560)]
+
+
+@pytest.mark.parametrize("shapes,acts", [
+    (LINEAR_ATTN, ["none", "silu", "none", "softplus"]),
+    (MLP_IN, ["silu", "none"])])
+@pytest.mark.parametrize("m,mode,dtype", [(1, "decode", "bf16"), (1, "decode", "f32"),
+                                          (64, "prefill", "bf16"), (97, "prefill", "f32")])
+def test_rmsnorm_linear_group(ctx, oracle, shapes, acts, m, mode, dtype):
+    rng = np.random.default_rng(m + len(shapes))
+    k = shapes[0][1]
+    x, w = rows_and_weight(rng, m, k, dtype, oracle, scale=2.0)
+    ws = [(rng.standard_normal(s) * 0.02).astype(np.float32) for s in shapes]
+    p4 = [oracle.pack_q8_0_p4(a) for a in ws]
+    ts = [ctx.upload_p4(p, *s) for p, s in zip(p4, shapes)]
+    try:
+        esz, et = (4, np.float32) if dtype == "f32" else (2, np.uint16)
+        xd, wd = ctx.to_device(x), ctx.to_device(w)
+        nd = ctx.alloc(m * k * esz)
+        outs = [ctx.alloc(m * n * esz) for n, _ in shapes]
+        ctx.rmsnorm_linear_group(xd, wd, nd, ts, outs, m, eps=1e-6, zero_centered=True,
+                                 activations=acts, mode=mode, dtype=dtype)
+        normed = oracle.rmsnorm(x, w, 1e-6, zero_centered=True, out_bf16=dtype == "bf16")
+        assert np.array_equal(bits(ctx.to_host(nd, (m, k), et)), bits(normed))
+        nf = normed if dtype == "f32" else oracle.bf16_bits_to_f32(normed)
+        for i, ((n, _), t, o) in enumerate(zip(shapes, ts, outs)):
+            got = ctx.to_host(o, (m, n), et)
+            sep = ctx.alloc(m * n * esz)
+            ctx.linear(nd, t, sep, m, activation=acts[i], mode=mode, dtype=dtype)
+            assert np.array_equal(bits(got), bits(ctx.to_host(sep, (m, n), et))), i
+            rows = np.arange(m) if m <= 4 else np.array([0, m // 2, m - 1])
+            ref = oracle.linear(nf[rows], p4[i], n, activation=acts[i],
+                                epilogue=ctx.epilogue, colpar=True)
+            if dtype == "bf16":
+                ref = oracle.f32_to_bf16_bits(ref)
+            assert np.array_equal(bits(got[rows]), bits(ref)), i
+        assert ctx.check_flag() == 0
+    finally:
+        for t in ts:
+            ctx.release(t)

@@ -397,3 +397,71 @@ def test_activations_closed_form(oracle):
     assert np.isinf(oracle.softplus(np.array([89.0], np.float32))[0])
     assert oracle.softplus(np.array([88.0], np.float32))[0] == np.float32(
         np.log(np.float64(np.float32(1.0) + np.float32(np.exp(88.0)))))
+
+
+# ------------------------------------------------------------- RMSNorm --
+# DecodeNormalization.cpp:93-154 / LowerToLinalg.cpp:245-300: the serial sum
+# is pinned by numpy's sequential float32 cumsum (its last partial sum), a
+# different implementation of the same left-to-right fold.
+
+def _serial_rstd(x, eps):
+    s = np.cumsum((x * x).astype(np.float32), dtype=np.float32)[-1]
+    mean = np.float32(s) / np.float32(x.size)
+    var = np.float32(mean) + np.float32(eps)
+    return np.float32(1.0) / np.sqrt(np.float32(var))
+
+
+@pytest.mark.parametrize("h", [32, 128, 2560])
+def test_rmsnorm_sum_is_the_serial_fold(oracle, h):
+    rng = np.random.default_rng(h)
+    x = (rng.standard_normal((5, h)) * np.array([[1], [1e-3], [30], [1], [1]])).astype(np.float32)
+    x[3] = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(x[3]))
+    w = rng.standard_normal(h).astype(np.float32)
+    y, r = oracle.rmsnorm(x, w, 1e-6, with_rstd=True)
+    for i in range(x.shape[0]):
+        assert r[i].view(np.uint32) == _serial_rstd(x[i], 1e-6).view(np.uint32), i
+
+
+def test_rmsnorm_order_changes_the_result(oracle):
+    # 1 followed by 4095 squares of 2^-12 (each half an ulp of 1.0): the
+    # serial sum stays 1.0 (ties to even); a float64 or pairwise sum does not
+    x = np.full(4096, 2.0 ** -12, np.float32)
+    x[0] = 1.0
+    w = np.ones(4096, np.float32)
+    _, r = oracle.rmsnorm(x, w, 0.0, with_rstd=True)
+    assert r[0] == np.float32(1.0) / np.sqrt(np.float32(1.0 / 4096))
+    s64 = float(np.sum(x.astype(np.float64) ** 2))
+    assert np.float32(1.0 / np.sqrt(s64 / 4096)) != r[0]
+    assert np.float32(1.0) / np.sqrt(np.float32(np.sum(x * x) / 4096)) != r[0]
+
+
+def test_rmsnorm_constant_row_closed_form(oracle):
+    for c in (0.75, -3.0, 2.0 ** -10):  # squares and their sums exact in f32
+        x = np.full((1, 256), c, np.float32)
+        w = np.linspace(-2, 2, 256).astype(np.float32)
+        eps = 1e-6
+        y = oracle.rmsnorm(x, w, eps)[0]
+        exact = c / np.sqrt(c * c + eps) * w.astype(np.float64)
+        assert np.all(np.abs(y - exact) <= 4 * np.spacing(np.abs(exact).astype(np.float32)) + 1e-30)
+        # zero-centered: w + 1
+        y1 = oracle.rmsnorm(x, w, eps, zero_centered=True)[0]
+        exact1 = c / np.sqrt(c * c + eps) * (w.astype(np.float64) + 1.0)
+        assert np.all(np.abs(y1 - exact1) <= 4 * np.spacing(np.abs(exact1).astype(np.float32)) + 1e-30)
+
+
+def test_rmsnorm_reference_numeric_case(oracle):
+    # run_numeric.py:734-749: bf16 x [2, 8], bf16 w, eps 1e-6, bf16 out
+    # within (2e-2, 1e-2) of the torch formula, zero-centered and not
+    torch = pytest.importorskip("torch")
+    torch.manual_seed(0)
+    x = torch.randn(2, 8).to(torch.bfloat16)
+    w = torch.randn(8).to(torch.bfloat16)
+    xf = x.float()
+    rstd = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    wb = w.view(torch.int16).numpy().view(np.uint16)
+    for zc, wf in ((True, 1.0 + w.float()), (False, w.float())):
+        ref = (xf * rstd * wf).to(torch.bfloat16).float().numpy()
+        got = oracle.bf16_bits_to_f32(oracle.rmsnorm(xb, wb, 1e-6, zero_centered=zc,
+                                                    out_bf16=True))
+        np.testing.assert_allclose(got, ref, rtol=2e-2, atol=1e-2)
