@@ -333,6 +333,63 @@ def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320
     return out
 
 
+def bench_norms(ctx, q8, iters=50):
+    """The RMSNorm neighbour (llmcp_q8_rmsnorm, gated RMSNorm) at the 4B
+    model's shapes in bf16, and the fused RMSNorm + grouped linears against
+    the two calls apart.  Each figure is one graph of `iters` calls."""
+    rng = np.random.default_rng(12)
+    timer = Timer(ctx)
+
+    def timed(fn):
+        fn()
+        ctx.sync()
+        g = graph_of(ctx, lambda: [fn() for _ in range(iters)])
+        run_graph(ctx, timer, g, 1)
+        us = run_graph(ctx, timer, g, 3) * 1e3 / (3 * iters)
+        ctx.graph_destroy(g)
+        return round(us, 2)
+
+    out = {}
+    h = 2560
+    w = ctx.to_device((rng.standard_normal(h) * 0.1).astype(np.float32).view(np.uint32)
+                      .__rshift__(16).astype(np.uint16))
+    for m in (1, 1024):
+        x = ctx.to_device((rng.standard_normal((m, h)).astype(np.float32).view(np.uint32)
+                           >> 16).astype(np.uint16))
+        y = ctx.alloc(m * h * 2)
+        out["rmsnorm_bf16_m%d_us" % m] = timed(
+            lambda: ctx.rmsnorm(x, w, y, m, h, zero_centered=True, dtype="bf16"))
+    z = ctx.to_device((rng.standard_normal((1, 4096)).astype(np.float32).view(np.uint32)
+                       >> 16).astype(np.uint16))
+    gw = ctx.to_device((rng.standard_normal(128) * 0.1 + 1).astype(np.float32))
+    gy = ctx.alloc(4096 * 2)
+    out["gated_rmsnorm_bf16_m1_4096_us"] = timed(
+        lambda: ctx.gated_rmsnorm(z, z, gw, gy, 1, 4096, 128, dtype="bf16"))
+    shapes = [(8192, h), (4096, h), (32, h), (32, h)]
+    ws = []
+    for n, k in shapes:
+        d, _ = ctx.synthesize_p4(seed=n + 5, rows=n, cols=k)
+        ws.append((ctx.register_device_p4(d, n, k), d))
+    ts = [t for t, _ in ws]
+    for m in (1, 1024):
+        x = ctx.to_device((rng.standard_normal((m, h)).astype(np.float32).view(np.uint32)
+                           >> 16).astype(np.uint16))
+        nd = ctx.alloc(m * h * 2)
+        outs = [ctx.alloc(m * n * 2) for n, _ in shapes]
+        mode = "decode" if m == 1 else "prefill"
+        fused = timed(lambda: ctx.rmsnorm_linear_group(
+            x, w, nd, ts, outs, m, zero_centered=True, mode=mode, dtype="bf16"))
+
+        def apart():
+            ctx.rmsnorm(x, w, nd, m, h, zero_centered=True, dtype="bf16")
+            ctx.linear_group(nd, ts, outs, m, mode=mode, dtype="bf16")
+        out["norm_qkvzab_m%d" % m] = {"fused_us": fused, "separate_us": timed(apart)}
+    for t, d in ws:
+        ctx.release(t)
+        d.free()
+    return out
+
+
 def bench_arena(ctx, q8):
     """The real 4B-class model's arena (426 tensors: Q8_0 matmul weights and
     tied table, BF16/F32 norms and conv/gate parameters; 4.47 GB laid out as
@@ -372,6 +429,47 @@ def bench_arena(ctx, q8):
 
         outs = [ctx.alloc(8192 * 4) for _ in range(4)]
 
+        # bf16 decode layers as the model builder chains them
+        # (ModelBuilder.cpp:219-275, :280-340): input_layernorm fused with
+        # the shared-input linears, the gated norm before out_proj (linear
+        # attention), out_proj / o_proj with the residual add, the
+        # post-attention norm, the SwiGLU pair and down with the residual
+        # add.  The mixers' own ops (conv, delta rule, attention) are not
+        # Q8 linears and are stood in for by fixed inputs.
+        def bf16_of(a):
+            return (a.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        xb = ctx.to_device(bf16_of(rng.standard_normal((1, hidden))))
+        rb, nb = ctx.alloc(hidden * 2), ctx.alloc(hidden * 2)
+        vb = ctx.to_device(bf16_of(rng.standard_normal((1, 4096))))
+        gb = ctx.alloc(4096 * 2)
+        hb = ctx.alloc(cfg["intermediate"] * 2)
+        lnw = ctx.to_device(bf16_of(rng.standard_normal(hidden) * 0.1))
+        gnw = ctx.to_device((rng.standard_normal(128) * 0.1 + 1).astype(np.float32))
+        outs_b = [ctx.alloc(8192 * 2) for _ in range(4)]
+
+        def layer_step():
+            for layer in range(cfg["layers"]):
+                pre = "model.language_model.layers.%d." % layer
+                mix = [nm for nm in names if nm.startswith(pre) and ".mlp." not in nm]
+                shared = [nm for nm in mix if w[nm].cols == hidden]
+                ctx.rmsnorm_linear_group(xb, lnw, nb, [w[nm] for nm in shared],
+                                         outs_b[:len(shared)], 1, zero_centered=True,
+                                         dtype="bf16")
+                proj = [nm for nm in mix if w[nm].cols == 4096][0]
+                if "linear_attn" in proj:
+                    zi = shared.index(pre + "linear_attn.in_proj_z.weight")
+                    ctx.gated_rmsnorm(vb, outs_b[zi], gnw, gb, 1, 4096, 128, dtype="bf16")
+                    ctx.linear_add(gb, w[proj], xb, rb, 1, dtype="bf16")
+                else:
+                    ctx.linear_add(vb, w[proj], xb, rb, 1, dtype="bf16")
+                ctx.rmsnorm(rb, lnw, nb, 1, hidden, zero_centered=True, dtype="bf16")
+                ctx.swiglu(nb, w[pre + "mlp.gate_proj.weight"], w[pre + "mlp.up_proj.weight"],
+                           hb, 1, dtype="bf16")
+                ctx.linear_add(hb, w[pre + "mlp.down_proj.weight"], rb, xb, 1, dtype="bf16")
+            ctx.rmsnorm(xb, lnw, nb, 1, hidden, zero_centered=True, dtype="bf16")
+            ctx.lm_head(nb, w["model.language_model.embed_tokens.weight"], logits, 1,
+                        argmax=am, dtype="bf16")
+
         def step(grouped=False):
             for layer in range(cfg["layers"]):
                 pre = "model.language_model.layers.%d." % layer
@@ -390,10 +488,11 @@ def bench_arena(ctx, q8):
 
         timer = Timer(ctx)
         step_us = {}
-        for grouped in (False, True):
-            step(grouped)
+        for grouped in (False, True, "layers"):
+            fn = layer_step if grouped == "layers" else (lambda: step(grouped))
+            fn()
             ctx.sync()
-            g = graph_of(ctx, lambda: step(grouped))
+            g = graph_of(ctx, fn)
             run_graph(ctx, timer, g, 1)
             step_us[grouped] = run_graph(ctx, timer, g, 5) * 1e3 / 5
             ctx.graph_destroy(g)
@@ -411,7 +510,8 @@ def bench_arena(ctx, q8):
             "decode_step_us": round(step_us[False], 1),
             "decode_step_GB/s": round(q8_bytes / (step_us[False] * 1e-6) / 1e9, 1),
             "decode_step_grouped_us": round(step_us[True], 1),
-            "decode_step_grouped_GB/s": round(q8_bytes / (step_us[True] * 1e-6) / 1e9, 1)}
+            "decode_step_grouped_GB/s": round(q8_bytes / (step_us[True] * 1e-6) / 1e9, 1),
+            "decode_step_bf16_layers_with_norms_us": round(step_us["layers"], 1)}
 
 
 def host_description():
@@ -609,6 +709,7 @@ def main():
         seq = bench_sequence(ctx)
         repack["7680x2560"] = round(seq["_qkv_repack_ms"], 3)
         extra["sequence_32_layers"] = {k: v for k, v in seq.items() if not k.startswith("_")}
+        extra["rmsnorm"] = bench_norms(ctx, q8)
         if not args.no_arena:
             extra["arena_real_model_32_layers"] = bench_arena(ctx, q8)
     # the one-time device repack (unit layout) of one tensor of each shape,

@@ -41,8 +41,8 @@ extern "C" {
 
 /* Version of this C ABI (1: f32 entries; 2: bf16 twins and all four
  * activations; 3: linear + residual add; 4: reference platform switch,
- * weight budget, graph staleness check, grouped linears; 5: RMSNorm and
- * RMSNorm + grouped linears).  The model ABI of
+ * weight budget, graph staleness check, grouped linears; 5: RMSNorm, gated
+ * RMSNorm and RMSNorm + grouped linears).  The model ABI of
  * the AOT library (llmcp_model_abi_version() == 2,
  * include/llmcp/Support/AotAbi.h:12) is not changed by this library. */
 #define LLMCP_Q8_ABI_VERSION 5
@@ -294,6 +294,27 @@ int llmcp_q8_rmsnorm(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
 int llmcp_q8_rmsnorm_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
                           const llmcp_memref_bf16_1d *weight, float eps,
                           int32_t zero_centered, llmcp_memref_bf16_2d *output);
+
+/* llmcp.gated_rms_norm (the linear-attention output norm in front of
+ * out_proj, ModelBuilder.cpp:259-266; DecodeNormalization.cpp:124-147 and
+ * LowerToLinalg.cpp:574-720): each row of x [M, H] splits into groups of
+ * group_size values (a multiple of 32 dividing H); per group the serial sum
+ * and rstd of llmcp_q8_rmsnorm, then y = ((x * s) * w) * rstd with
+ * s = g * (1 / (1 + exp(-g))) of the gate [M, H], or s = g when
+ * gate_activated.  w [group_size] is f32 (the arena's F32 norm weight, 16 B
+ * aligned).  Dense rows only. */
+int llmcp_q8_gated_rmsnorm(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                           const llmcp_memref_f32_2d *gate,
+                           const llmcp_memref_f32_1d *weight, int64_t group_size,
+                           float eps, int32_t gate_activated,
+                           llmcp_memref_f32_2d *output);
+
+/* bf16 input, gate and output (the real graph's types), f32 weight. */
+int llmcp_q8_gated_rmsnorm_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                                const llmcp_memref_bf16_2d *gate,
+                                const llmcp_memref_f32_1d *weight, int64_t group_size,
+                                float eps, int32_t gate_activated,
+                                llmcp_memref_bf16_2d *output);
 
 /* The RMSNorm and the linears it feeds (input_layernorm -> in_proj_qkv/z/
  * a/b or q/k/v, post_attention_layernorm -> gate/up; ModelBuilder.cpp:

@@ -83,7 +83,8 @@ EXPORTS = [
     "llmcp_q8_linear_group", "llmcp_q8_linear_group_bf16",
     "_mlir_ciface_llmcp_q8_linear_group3", "_mlir_ciface_llmcp_q8_linear_group4",
     "llmcp_q8_rmsnorm", "llmcp_q8_rmsnorm_bf16", "llmcp_q8_rmsnorm_linear_group",
-    "llmcp_q8_rmsnorm_linear_group_bf16",
+    "llmcp_q8_rmsnorm_linear_group_bf16", "llmcp_q8_gated_rmsnorm",
+    "llmcp_q8_gated_rmsnorm_bf16",
 ]
 
 
@@ -170,6 +171,8 @@ def lib():
         "llmcp_q8_rmsnorm": (I, [P, P, P, ctypes.c_float, I32, P]),
         "llmcp_q8_rmsnorm_bf16": (I, [P, P, P, ctypes.c_float, I32, P]),
         "llmcp_q8_rmsnorm_linear_group": (I, [P, P, P, ctypes.c_float, I32, P, I32, P, P, P, I32]),
+        "llmcp_q8_gated_rmsnorm": (I, [P, P, P, P, I64, ctypes.c_float, I32, P]),
+        "llmcp_q8_gated_rmsnorm_bf16": (I, [P, P, P, P, I64, ctypes.c_float, I32, P]),
         "llmcp_q8_rmsnorm_linear_group_bf16": (I, [P, P, P, ctypes.c_float, I32, P, I32, P, P,
                                                    P, I32]),
     }
@@ -417,6 +420,18 @@ class Context:
         check(self._entry("llmcp_q8_rmsnorm", dtype)(
             self.handle, ctypes.byref(xi), ctypes.byref(wv), float(eps),
             1 if zero_centered else 0, ctypes.byref(yo)))
+
+    def gated_rmsnorm(self, x, gate, w, y, m, h, group, eps=1e-6, gate_activated=False,
+                      dtype="f32"):
+        """y = gated RMSNorm of x [m, h] with gate [m, h] in groups of `group`
+        (x, gate and y of dtype; w [group] f32)."""
+        xi = f32_memref(x.ptr if hasattr(x, "ptr") else x, m, h)
+        gi = f32_memref(gate.ptr if hasattr(gate, "ptr") else gate, m, h)
+        yo = f32_memref(y.ptr if hasattr(y, "ptr") else y, m, h)
+        wv = i8_memref(w.ptr if hasattr(w, "ptr") else w, group)
+        check(self._entry("llmcp_q8_gated_rmsnorm", dtype)(
+            self.handle, ctypes.byref(xi), ctypes.byref(gi), ctypes.byref(wv), int(group),
+            float(eps), 1 if gate_activated else 0, ctypes.byref(yo)))
 
     def rmsnorm_linear_group(self, x, norm_w, normed, weights, outputs, m, eps=1e-6,
                              zero_centered=False, activations=None, mode="decode",

@@ -139,6 +139,12 @@ hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
                           int8_t *qa, float *sa, int64_t blocks_pad, int qmode,
                           hipStream_t s);
 
+// Gated RMSNorm of `groups` dense groups of g values (g % 32 == 0): x, gate
+// and y share their type (f32 or bf16), w [g] is f32.
+hipError_t launch_gated_rmsnorm(const void *x, const void *gate, bool bf16,
+                                int64_t groups, int64_t g, const float *w, float eps,
+                                bool gate_activated, void *y, hipStream_t s);
+
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             const uint8_t *table, int64_t rows, int64_t cols,
                             void *out, bool out_bf16, int64_t ldo,

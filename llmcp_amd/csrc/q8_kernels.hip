@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256) void quantize_tiles_kernel(
 }
 
 
-// RMSNorm of up to 64 rows per workgroup, each row on its own as the
+// RMSNorm of up to 4 rows per workgroup, each row on its own as the
 // reference reduces it (DecodeNormalization.cpp:93-107 and :124-154 for
 // decode rows, LowerToLinalg.cpp:245-300 for prefill: the same arithmetic):
 // sum = sum + x*x over the row in index order, each step rounded to f32;
@@ -297,40 +297,49 @@ __global__ __launch_bounds__(256) void quantize_tiles_kernel(
 // (math.rsqrt under --convert-math-to-llvm); y = (x * rstd) * w', w' = w, or
 // w + 1 when zero-centered; bf16 outputs rounded to nearest even.
 //
-// The serial sum is one dependent add per element, in lane r of wave 0 for
-// row r.  Waves 1-3 stage the squares of the next 128-column chunk of the
-// 64 rows in LDS while wave 0 folds the current one (rows padded to 129
-// floats, so the 64 lanes read 64 banks).  Then all waves write y and,
-// with QMODE, its Q8_1 (the quantizer's arithmetic, quantize_block8, on
-// the values as stored): QMODE 1 the dense [m][blocks_pad * 32] layout,
-// QMODE 2 the GEMM's tiled layout (rows up to the 32-row tile's end and
-// blocks past H written as zeros).  Requires h % 32 == 0.
-constexpr int kNormRows = 64;
-constexpr int kNormChunk = 128;
+// The serial sum is one dependent add per element, the critical path: lane
+// r of wave 0 folds row r from LDS (four squares per ds_read_b128, rows
+// padded by 16 B so the lanes' reads fall in distinct banks), nothing
+// else in its instruction stream.  Waves 1-3 load the next 512-column
+// chunk of the workgroup's rows and store its squares in the other LDS
+// buffer meanwhile.  Then all waves write y and, with QMODE, its Q8_1 (the
+// quantizer's arithmetic, quantize_block8, on the values as stored): QMODE
+// 1 the dense [m][blocks_pad * 32] layout, QMODE 2 the GEMM's tiled layout
+// (blocks past H written as zeros; rows past m in the last tile are left
+// unwritten, as by launch_quantize_tiled: their results are never stored).
+// Requires h % 32 == 0.
+//
+// GATED: llmcp.gated_rms_norm, whose groups of h values are the rows here
+// (DecodeNormalization.cpp:124-147, GatedRmsNormOpLowering,
+// LowerToLinalg.cpp:574-720): the same sum and rstd over x, then
+// y = ((x * s) * w) * rstd with s = g * (1 / (1 + exp(-g))) of the gate
+// row g, or s = g when the gate is already activated.
+constexpr int kNormRows = 4;
+constexpr int kNormChunk = 512;
 
-template <bool XB, bool WB, bool YB, int QMODE>
+template <bool XB, bool WB, bool YB, int QMODE, bool GATED>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(
     const void *__restrict__ x, int64_t ldx, const void *__restrict__ w,
     float eps, int zero_centered, int64_t m, int32_t h, void *__restrict__ y,
     int64_t ldy, int8_t *__restrict__ qa, float *__restrict__ sa,
-    int32_t blocks_pad, int aligned) {
-  __shared__ float sq[2][kNormRows][kNormChunk + 1];
+    int32_t blocks_pad, int aligned, const void *__restrict__ gate, int64_t ldg,
+    int gate_activated) {
+  static_assert(!GATED || QMODE == 0, "a gated norm writes no Q8_1");
+  __shared__ __align__(16) float sq[2][kNormRows][kNormChunk + 4];
   __shared__ float rstd_s[kNormRows];
   const int64_t row0 = (int64_t)blockIdx.x * kNormRows;
   const int rows = (int)min<int64_t>(kNormRows, m - row0);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int chunks = (h + kNormChunk - 1) / kNormChunk;
-  auto load1 = [&](const void *p, int64_t i) -> float {
-    if constexpr (XB) return bf16_to_float(((const uint16_t *)p)[i]);
-    else return ((const float *)p)[i];
-  };
-  // squares of chunk c into buffer b: threads t0.. of nt
-  auto stage = [&](int c, int b, int t0, int nt) {
-    const int c0 = c * kNormChunk, cw = min(kNormChunk, h - c0);
-    for (int e = (int)threadIdx.x - t0; e < rows * cw; e += nt) {
-      const int r = e / cw, j = e - r * cw;
-      const float v = load1(x, (row0 + r) * ldx + c0 + j);
-      sq[b][r][j] = v * v;
+  // squares of chunk c into buffer b by threads t0.. (nt of them), four
+  // consecutive values per thread and step (h % 32 == 0: never a partial
+  // vector)
+  auto stage = [&](int c, int b, int t0, int nt) __attribute__((always_inline)) {
+    const int c0 = c * kNormChunk, cw = min(kNormChunk, h - c0), q = cw / 4;
+    for (int e = (int)threadIdx.x - t0; e < rows * q; e += nt) {
+      const int r = e / q, j = 4 * (e - r * q);
+      const float4 v = load_act4(x, (row0 + r) * ldx + c0 + j, XB, aligned != 0);
+      *(float4 *)&sq[b][r][j] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
     }
   };
   stage(0, 0, 0, 256);
@@ -341,15 +350,36 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
       if (lane < rows) {
         const int cw = min(kNormChunk, h - c * kNormChunk);
         const float *q = sq[c & 1][lane];
+        // the reads of the next 32 values go out before the adds of these
+        // (cw % 64 == 0 except for a final 32), kept in that order by
+        // scheduling barriers
+        float4 va[8], vb[8];
+        auto rd = [&](float4 (&v)[8], int j) __attribute__((always_inline)) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = *(const float4 *)(q + j + 4 * u);
+        };
+        auto add = [&](const float4 (&v)[8]) __attribute__((always_inline)) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            sum = sum + v[u].x;
+            sum = sum + v[u].y;
+            sum = sum + v[u].z;
+            sum = sum + v[u].w;
+          }
+        };
+        rd(va, 0);
         int j = 0;
-        for (; j + 16 <= cw; j += 16) {
-          float t[16];
-#pragma unroll
-          for (int u = 0; u < 16; ++u) t[u] = q[j + u];
-#pragma unroll
-          for (int u = 0; u < 16; ++u) sum = sum + t[u];
+        for (; j + 64 <= cw; j += 64) {
+          rd(vb, j + 32);
+          __builtin_amdgcn_sched_barrier(0);
+          add(va);
+          __builtin_amdgcn_sched_barrier(0);
+          rd(va, j + 64 < cw ? j + 64 : j);
+          __builtin_amdgcn_sched_barrier(0);
+          add(vb);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        for (; j < cw; ++j) sum = sum + q[j];
+        if (j < cw) add(va);
       }
     } else if (c + 1 < chunks) {
       stage(c + 1, (c + 1) & 1, 64, 192);
@@ -366,8 +396,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   // y and its Q8_1: 8 lanes per (row, block), the same trip count in every
   // lane (quantize_block8 works across the wave)
   const int blocks = h / kBlock;
-  const int64_t tile_end = (m + 31) / 32 * 32;
-  const int out_rows = QMODE == 2 ? (int)min<int64_t>(kNormRows, tile_end - row0) : rows;
+  const int out_rows = rows;
   const int nb = QMODE != 0 ? blocks_pad : blocks;
   const int units = out_rows * nb;
   const int p = threadIdx.x & 7;
@@ -389,10 +418,24 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
         wv.w = wv.w + 1.0f;
       }
       const float rs = rstd_s[r];
-      v.x = (xv.x * rs) * wv.x;
-      v.y = (xv.y * rs) * wv.y;
-      v.z = (xv.z * rs) * wv.z;
-      v.w = (xv.w * rs) * wv.w;
+      if constexpr (GATED) {
+        float4 g = load_act4(gate, row * ldg + b * kBlock + 4 * p, XB, aligned != 0);
+        if (!gate_activated) {
+          g.x = silu_f32(g.x);
+          g.y = silu_f32(g.y);
+          g.z = silu_f32(g.z);
+          g.w = silu_f32(g.w);
+        }
+        v.x = ((xv.x * g.x) * wv.x) * rs;
+        v.y = ((xv.y * g.y) * wv.y) * rs;
+        v.z = ((xv.z * g.z) * wv.z) * rs;
+        v.w = ((xv.w * g.w) * wv.w) * rs;
+      } else {
+        v.x = (xv.x * rs) * wv.x;
+        v.y = (xv.y * rs) * wv.y;
+        v.z = (xv.z * rs) * wv.z;
+        v.w = (xv.w * rs) * wv.w;
+      }
       if constexpr (YB) {
         const uint16_t b0 = float_to_bf16(v.x), b1 = float_to_bf16(v.y),
                        b2 = float_to_bf16(v.z), b3 = float_to_bf16(v.w);
@@ -738,8 +781,8 @@ hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
   const int32_t hh = (int32_t)h, bp = (int32_t)blocks_pad;
 #define LLMCP_NORM(XB, WB, YB, Q)                                                         \
   if (x_bf16 == XB && w_bf16 == WB && y_bf16 == YB && qmode == Q) {                       \
-    hipLaunchKernelGGL((rmsnorm_kernel<XB, WB, YB, Q>), grid, dim3(256), 0, s, x, ldx, w, \
-                       eps, zc, m, hh, y, ldy, qa, sa, bp, aligned);                      \
+    hipLaunchKernelGGL((rmsnorm_kernel<XB, WB, YB, Q, false>), grid, dim3(256), 0, s, x, ldx, \
+                       w, eps, zc, m, hh, y, ldy, qa, sa, bp, aligned, nullptr, 0, 0);   \
     return hipGetLastError();                                                            \
   }
   LLMCP_NORM(false, false, false, 0) LLMCP_NORM(false, false, false, 1)
@@ -750,6 +793,25 @@ hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
   LLMCP_NORM(true, false, true, 1) LLMCP_NORM(true, false, true, 2)
 #undef LLMCP_NORM
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gated_rmsnorm(const void *x, const void *gate, bool bf16,
+                                int64_t groups, int64_t g, const float *w, float eps,
+                                bool gate_activated, void *y, hipStream_t s) {
+  if (g % kBlock != 0 || groups <= 0 || (uintptr_t)w % 16 != 0) return hipErrorInvalidValue;
+  const int64_t esz = bf16 ? 2 : 4;
+  const int aligned = ((uintptr_t)x % (4 * esz) == 0) && ((uintptr_t)gate % (4 * esz) == 0) &&
+                              (g % 4 == 0) ? 1 : 0;
+  const dim3 grid((unsigned)((groups + kNormRows - 1) / kNormRows));
+  const int32_t gg = (int32_t)g;
+  const int ga = gate_activated ? 1 : 0;
+  if (bf16)
+    hipLaunchKernelGGL((rmsnorm_kernel<true, false, true, 0, true>), grid, dim3(256), 0, s, x, g,
+                       w, eps, 0, groups, gg, y, g, nullptr, nullptr, 0, aligned, gate, g, ga);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<false, false, false, 0, true>), grid, dim3(256), 0, s, x,
+                       g, w, eps, 0, groups, gg, y, g, nullptr, nullptr, 0, aligned, gate, g, ga);
+  return hipGetLastError();
 }
 
 hipError_t launch_embedding(const int64_t *tokens, int64_t count,

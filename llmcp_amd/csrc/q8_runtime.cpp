@@ -1258,6 +1258,36 @@ static int rmsnorm_impl(llmcp_q8_ctx *ctx, const Rows &in, const NormWeight &nw,
   return LLMCP_Q8_OK;
 }
 
+// llmcp.gated_rms_norm (the linear-attention output norm in front of
+// out_proj, ModelBuilder.cpp:259-266): groups of `group` values per row,
+// dense rows only.
+static int gated_rmsnorm_impl(llmcp_q8_ctx *ctx, const Rows &in, const Rows &gate,
+                              const NormWeight &nw, int64_t group, float eps,
+                              int32_t gate_activated, const Rows &out) {
+  if (out.rows != in.rows || out.cols != in.cols || gate.rows != in.rows ||
+      gate.cols != in.cols)
+    return fail(LLMCP_Q8_DECLINED, "gated RMSNorm input, gate and output must share [M, H]");
+  if (group <= 0 || group % kBlock != 0 || in.cols % group != 0)
+    return fail(LLMCP_Q8_DECLINED, "group size %lld must be a multiple of 32 dividing H",
+                (long long)group);
+  if (nw.len != group)
+    return fail(LLMCP_Q8_DECLINED, "gated RMSNorm weight has %lld values for groups of %lld",
+                (long long)nw.len, (long long)group);
+  if ((uintptr_t)nw.data % 16 != 0)
+    return fail(LLMCP_Q8_DECLINED, "gated RMSNorm weight must be 16 B aligned");
+  if ((in.rows > 1 && in.ld != in.cols) || (gate.rows > 1 && gate.ld != gate.cols) ||
+      (out.rows > 1 && out.ld != out.cols))
+    return fail(LLMCP_Q8_DECLINED, "gated RMSNorm rows must be dense");
+  if (in.rows == 0) return LLMCP_Q8_OK;
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  hipError_t e = launch_gated_rmsnorm(in.data, gate.data, in.bf16, in.rows * (in.cols / group),
+                                      group, (const float *)nw.data, eps, gate_activated != 0,
+                                      out.data, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "gated rmsnorm launch");
+  return LLMCP_Q8_OK;
+}
+
 // RMSNorm, then linears on the normed rows (the model builder's
 // input_layernorm -> in_proj_qkv/z/a/b or q/k/v, post_attention_layernorm
 // -> gate/up; ModelBuilder.cpp:225-236, :284-294).  For several rows the
@@ -1602,6 +1632,40 @@ int llmcp_q8_rmsnorm_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
     if (!norm_weight_of(weight, true, nw))
       return fail(LLMCP_Q8_DECLINED, "RMSNorm weight must be a dense vector");
     return rmsnorm_impl(ctx, in, nw, eps, zero_centered, out);
+  });
+}
+
+int llmcp_q8_gated_rmsnorm(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
+                           const llmcp_memref_f32_2d *gate,
+                           const llmcp_memref_f32_1d *weight, int64_t group_size,
+                           float eps, int32_t gate_activated,
+                           llmcp_memref_f32_2d *output) {
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, g, out;
+    NormWeight nw;
+    if (!view_of(input, false, in) || !view_of(gate, false, g) || !view_of(output, false, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    if (!norm_weight_of(weight, false, nw))
+      return fail(LLMCP_Q8_DECLINED, "RMSNorm weight must be a dense vector");
+    return gated_rmsnorm_impl(ctx, in, g, nw, group_size, eps, gate_activated, out);
+  });
+}
+
+int llmcp_q8_gated_rmsnorm_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *input,
+                                const llmcp_memref_bf16_2d *gate,
+                                const llmcp_memref_f32_1d *weight, int64_t group_size,
+                                float eps, int32_t gate_activated,
+                                llmcp_memref_bf16_2d *output) {
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    Rows in, g, out;
+    NormWeight nw;
+    if (!view_of(input, true, in) || !view_of(gate, true, g) || !view_of(output, true, out))
+      return fail(LLMCP_Q8_DECLINED, kDenseMsg);
+    if (!norm_weight_of(weight, false, nw))
+      return fail(LLMCP_Q8_DECLINED, "RMSNorm weight must be a dense vector");
+    return gated_rmsnorm_impl(ctx, in, g, nw, group_size, eps, gate_activated, out);
   });
 }
 

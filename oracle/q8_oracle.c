@@ -38,7 +38,10 @@
  *                       cumsum (the last partial sum), rstd against float32
  *                       1/np.sqrt, constructed rows whose pairwise or float64
  *                       sum differs from the serial one, and the closed form
- *                       of a constant row (y = w * sign(x) within 1 ulp).
+ *                       of a constant row (y = w * sign(x) within 4 ulp).
+ *   gated_rmsnorm       the per-group sums against the plain rmsnorm of the
+ *                       reshaped rows, the gate against oracle_silu, and an
+ *                       all-ones gate row (activated) against rmsnorm.
  */
 #include <math.h>
 #include <stdint.h>
@@ -477,6 +480,37 @@ void oracle_rmsnorm(const float *x, int64_t rows, int64_t h, const float *w,
       y[r * h + d] = t * wd;
     }
   }
+}
+
+/* Gated RMSNorm (DecodeNormalization.cpp:124-147 with gate,
+ * GatedRmsNormOpLowering, LowerToLinalg.cpp:574-720): each row splits into
+ * groups of g values; per group the serial sum of x*x, rstd as in
+ * oracle_rmsnorm with g in place of h, then
+ *   y_d = ((x_d * s_d) * w_{d mod g}) * rstd,
+ * s = silu(gate) (oracle_silu), or the gate itself when gate_activated. */
+void oracle_gated_rmsnorm(const float *x, const float *gate, int64_t rows, int64_t h,
+                          int64_t g, const float *w, float eps, int gate_activated,
+                          float *y) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c0 = 0; c0 < h; c0 += g) {
+      const float *xr = x + r * h + c0;
+      const float *gr = gate + r * h + c0;
+      float sum = 0.0f;
+      for (int64_t d = 0; d < g; ++d) {
+        float sq = xr[d] * xr[d];
+        sum = sum + sq;
+      }
+      float mean = sum / (float)g;
+      float var = mean + eps;
+      float root = sqrtf(var);
+      float rstd = 1.0f / root;
+      for (int64_t d = 0; d < g; ++d) {
+        float s = gate_activated ? gr[d] : oracle_silu(gr[d]);
+        float v = xr[d] * s;
+        v = v * w[d];
+        y[r * h + c0 + d] = v * rstd;
+      }
+    }
 }
 
 int oracle_max_threads(void) {

@@ -74,6 +74,7 @@ def _declare(L):
     L.oracle_max_threads.restype = I
     L.oracle_set_threads.argtypes = [I]
     L.oracle_rmsnorm.argtypes = [P, I64, I64, P, ctypes.c_float, I, P, P]
+    L.oracle_gated_rmsnorm.argtypes = [P, P, I64, I64, I64, P, ctypes.c_float, I, P]
 
 
 def _ptr(a):
@@ -245,6 +246,22 @@ def rmsnorm(x, w, eps, zero_centered=False, out_bf16=False, with_rstd=False):
     if out_bf16:
         y = f32_to_bf16_bits(y)
     return (y, r) if with_rstd else y
+
+
+def gated_rmsnorm(x, gate, w, group, eps, gate_activated=False, out_bf16=False):
+    """The reference gated RMSNorm of x [M, H] with gate [M, H] (f32, or bf16
+    bits as uint16) in groups of `group` values, f32 weight w [group]."""
+    def widen(a):
+        a = np.asarray(a)
+        return bf16_bits_to_f32(a) if a.dtype == np.uint16 else a
+    x = _c(np.atleast_2d(widen(x)), np.float32)
+    g = _c(np.atleast_2d(widen(gate)), np.float32)
+    w = _c(np.asarray(w).ravel(), np.float32)
+    m, h = x.shape
+    y = np.zeros((m, h), np.float32)
+    lib().oracle_gated_rmsnorm(_ptr(x), _ptr(g), m, h, group, _ptr(w),
+                               float(np.float32(eps)), 1 if gate_activated else 0, _ptr(y))
+    return f32_to_bf16_bits(y) if out_bf16 else y
 
 
 def max_threads():

@@ -129,3 +129,35 @@ def test_rmsnorm_linear_group(ctx, oracle, shapes, acts, m, mode, dtype):
     finally:
         for t in ts:
             ctx.release(t)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("m,h,group", [(1, 4096, 128), (5, 4096, 128), (70, 256, 64),
+                                       (1, 32, 32)])
+@pytest.mark.parametrize("activated", [False, True])
+def test_gated_rmsnorm_bitwise(ctx, oracle, dtype, m, h, group, activated):
+    """The linear-attention output norm: 32 value heads of 128 at the real
+    shape (ModelBuilder.cpp:259-266), f32 weight."""
+    rng = np.random.default_rng(m + h + group + activated)
+    x = (rng.standard_normal((m, h)) * 2).astype(np.float32)
+    z = (rng.standard_normal((m, h)) * 3).astype(np.float32)
+    w = (rng.standard_normal(group) * 0.1 + 1).astype(np.float32)
+    if dtype == "bf16":
+        x, z = oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(z)
+    et = np.float32 if dtype == "f32" else np.uint16
+    xd, zd, wd = ctx.to_device(x), ctx.to_device(z), ctx.to_device(w)
+    yd = ctx.alloc(x.nbytes)
+    ctx.gated_rmsnorm(xd, zd, wd, yd, m, h, group, eps=1e-6, gate_activated=activated,
+                      dtype=dtype)
+    ref = oracle.gated_rmsnorm(x, z, w, group, 1e-6, gate_activated=activated,
+                               out_bf16=dtype == "bf16")
+    assert np.array_equal(bits(ctx.to_host(yd, (m, h), et)), bits(ref))
+
+
+def test_gated_rmsnorm_declines(ctx, q8):
+    xd = ctx.alloc(256 * 4)
+    wd = ctx.alloc(128 * 4)
+    with pytest.raises(q8.Declined):  # group does not divide H
+        ctx.gated_rmsnorm(xd, xd, wd, xd, 1, 256, 96)
+    with pytest.raises(q8.Declined):  # group not a multiple of 32
+        ctx.gated_rmsnorm(xd, xd, wd, xd, 1, 256, 16)

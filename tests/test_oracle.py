@@ -465,3 +465,24 @@ def test_rmsnorm_reference_numeric_case(oracle):
         got = oracle.bf16_bits_to_f32(oracle.rmsnorm(xb, wb, 1e-6, zero_centered=zc,
                                                     out_bf16=True))
         np.testing.assert_allclose(got, ref, rtol=2e-2, atol=1e-2)
+
+
+def test_gated_rmsnorm_pins(oracle):
+    rng = np.random.default_rng(3)
+    m, groups, g = 3, 4, 128
+    x = rng.standard_normal((m, groups * g)).astype(np.float32)
+    z = (rng.standard_normal((m, groups * g)) * 2).astype(np.float32)
+    w = (rng.standard_normal(g) * 0.1 + 1).astype(np.float32)
+    # an all-ones activated gate reduces to the plain norm of the reshaped
+    # rows, whose ((x*1)*w)*rstd differs from (x*rstd)*w only in rounding
+    ones = np.ones_like(x)
+    yg = oracle.gated_rmsnorm(x, ones, w, g, 1e-6, gate_activated=True)
+    _, r = oracle.rmsnorm(x.reshape(-1, g), w, 1e-6, with_rstd=True)
+    assert np.array_equal(r, np.array([_serial_rstd(row, 1e-6) for row in x.reshape(-1, g)]))
+    expect = ((x.reshape(-1, g) * w) * r[:, None]).reshape(m, -1)
+    assert np.array_equal(yg.view(np.uint32), expect.astype(np.float32).view(np.uint32))
+    # the gate enters through the oracle's silu (float64 closed form within ulps)
+    y = oracle.gated_rmsnorm(x, z, w, g, 1e-6)
+    s64 = z.astype(np.float64) / (1 + np.exp(-z.astype(np.float64)))
+    ref = (x * s64).reshape(-1, g) * w * r[:, None]
+    np.testing.assert_allclose(y, ref.reshape(m, -1), rtol=3e-6, atol=1e-30)
