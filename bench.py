@@ -62,18 +62,34 @@ class Timer:
         return self.ctx.elapsed_ms(self.e0, self.e1)
 
 
+# --eager: every timed block runs as plain launches instead of a captured
+# graph (for kernel tracers, whose graph replay handling is not needed to
+# read per-kernel durations); the printed figures then include launch cost.
+EAGER = False
+
+
 def graph_of(ctx, fn):
+    if EAGER:
+        return fn
     ctx.sync()
     ctx.graph_begin()
     fn()
     return ctx.graph_end()
 
 
+def graph_free(ctx, graph):
+    if not EAGER:
+        ctx.graph_destroy(graph)
+
+
 def run_graph(ctx, timer, graph, launches):
     ctx.sync()
     timer.start()
     for _ in range(launches):
-        ctx.graph_launch(graph)
+        if EAGER:
+            graph()
+        else:
+            ctx.graph_launch(graph)
     ms = timer.stop_ms()
     ctx.sync()
     return ms
@@ -117,10 +133,10 @@ def bench_decode_mlp(ctx, q8, steps, warmup, hidden=2560, ffn=9216):
         if warmup:
             gw = graph_of(ctx, make(warmup))
             run_graph(ctx, timer, gw, 1)
-            ctx.graph_destroy(gw)
+            graph_free(ctx, gw)
         g = graph_of(ctx, make(steps))
         ms = run_graph(ctx, timer, g, 1)
-        ctx.graph_destroy(g)
+        graph_free(ctx, g)
         return ms
 
     ms = timed(mlp_steps)
@@ -317,7 +333,7 @@ def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320
             run_graph(ctx, timer, g, 1)
             reps = 10 if m == 1 else 3
             us = run_graph(ctx, timer, g, reps) * 1e3 / reps
-            ctx.graph_destroy(g)
+            graph_free(ctx, g)
             fig = {"us": round(us, 1), "GB/s": round(total / (us * 1e-6) / 1e9, 1),
                    "TOPS": round(ops / (us * 1e-6) / 1e12, 2)}
             if grouped:
@@ -346,7 +362,7 @@ def bench_norms(ctx, q8, iters=50):
         g = graph_of(ctx, lambda: [fn() for _ in range(iters)])
         run_graph(ctx, timer, g, 1)
         us = run_graph(ctx, timer, g, 3) * 1e3 / (3 * iters)
-        ctx.graph_destroy(g)
+        graph_free(ctx, g)
         return round(us, 2)
 
     out = {}
@@ -495,7 +511,7 @@ def bench_arena(ctx, q8):
             g = graph_of(ctx, fn)
             run_graph(ctx, timer, g, 1)
             step_us[grouped] = run_graph(ctx, timer, g, 5) * 1e3 / 5
-            ctx.graph_destroy(g)
+            graph_free(ctx, g)
         q8_bytes = sum(e["size"] for e in entries if e["dtype"] == "Q8_0")
         for wt in w.values():
             ctx.release(wt)
@@ -668,6 +684,9 @@ def main():
     ap.add_argument("--gemm-only", type=int, default=0, metavar="M",
                     help="time only config 4's prefill GEMM at M rows and print "
                          "its figures (a short run for counter collection)")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every timed block directly instead of replaying a "
+                         "captured graph (for kernel tracers; figures include launch cost)")
     ap.add_argument("--platform", choices=("aarch64", "x86"), default="aarch64",
                     help="reference arithmetic to reproduce: the SDOT paths' "
                          "fma epilogue (default) or the x86 scalar path's")
@@ -678,6 +697,8 @@ def main():
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import llmcp_amd as q8
+    global EAGER
+    EAGER = args.eager
     ctx = q8.Context(0)
     ctx.set_platform(args.platform)
     if args.copy_calibration:
