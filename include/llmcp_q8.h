@@ -580,6 +580,15 @@ int llmcp_q8_graph_destroy(void *graph_exec);
 /* Bytes the device copy of a registered weight occupies (0 if unknown). */
 uint64_t llmcp_q8_device_bytes(llmcp_q8_ctx *ctx, const void *key);
 
+/* ------------------------------------------------------------ testing -- */
+/* No counterpart in the reference.  For tests of the RMSNorm entries: rows
+ * of up to 12288 values have their serial sum of squares evaluated
+ * speculatively from predicted partial sums, with exact fallbacks; this
+ * offsets the predictions by `bits` f32 steps (process-wide, 0 = off) so
+ * that the fallbacks decide the results.  Results do not change.  Not for
+ * use while RMSNorm calls are in flight. */
+int llmcp_q8_test_rmsnorm_skew(int32_t bits);
+
 #ifdef __cplusplus
 }
 #endif

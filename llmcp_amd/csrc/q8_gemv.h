@@ -224,6 +224,36 @@ __device__ __forceinline__ float4 load_act4_t(const void *p, int64_t i) {
   }
 }
 
+// The bits of four consecutive values as they come from memory (bf16: two
+// dwords of packed halves; f32: four dwords), widened later by act4_of_raw,
+// so a batch of loads goes out before the first of them is waited for.
+template <bool BF16, bool ALIGNED>
+__device__ __forceinline__ uint4 load_raw4(const void *p, int64_t i) {
+  if constexpr (BF16) {
+    const uint16_t *h = (const uint16_t *)p + i;
+    if constexpr (ALIGNED) {
+      const uint2 w = *(const uint2 *)h;
+      return make_uint4(w.x, w.y, 0u, 0u);
+    }
+    return make_uint4((uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                      (uint32_t)h[2] | ((uint32_t)h[3] << 16), 0u, 0u);
+  } else {
+    const uint32_t *f = (const uint32_t *)p + i;
+    if constexpr (ALIGNED) return *(const uint4 *)f;
+    return make_uint4(f[0], f[1], f[2], f[3]);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float4 act4_of_raw(uint4 r) {
+  if constexpr (BF16)
+    return make_float4(bf16_to_float(r.x & 0xffffu), bf16_to_float(r.x >> 16),
+                       bf16_to_float(r.y & 0xffffu), bf16_to_float(r.y >> 16));
+  else
+    return make_float4(__uint_as_float(r.x), __uint_as_float(r.y),
+                       __uint_as_float(r.z), __uint_as_float(r.w));
+}
+
 // --------------------------------------------------------------- GEMV -- //
 
 

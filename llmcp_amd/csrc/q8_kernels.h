@@ -139,6 +139,12 @@ hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
                           int8_t *qa, float *sa, int64_t blocks_pad, int qmode,
                           hipStream_t s);
 
+// Tests only: offsets launch_rmsnorm's predicted partial sums (rows of up to
+// 12288 values, where the sum is evaluated speculatively) by `bits` f32
+// steps, so that the kernel's fallbacks decide the results; 0 restores it.
+// Results are the same either way.  Not synchronised with launches.
+void set_rmsnorm_spec_skew(int bits);
+
 // Gated RMSNorm of `groups` dense groups of g values (g % 32 == 0): x, gate
 // and y share their type (f32 or bf16), w [g] is f32.
 hipError_t launch_gated_rmsnorm(const void *x, const void *gate, bool bf16,

@@ -472,6 +472,326 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   }
 }
 
+// The serial f32 sum of n squares (n % 4 == 0) from LDS continued from s, in
+// order: one dependent add per element, the reads of the next 32 values out
+// before the adds of these (kept in that order by scheduling barriers).
+__device__ __forceinline__ float fold_serial(const float *q, int n, float s) {
+  float4 va[8], vb[8];
+  auto rd = [&](float4 (&v)[8], int j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = *(const float4 *)(q + j + 4 * u);
+  };
+  auto add = [&](const float4 (&v)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      s = s + v[u].x;
+      s = s + v[u].y;
+      s = s + v[u].z;
+      s = s + v[u].w;
+    }
+  };
+  const int n32 = n & ~31;
+  int j = 0;
+  if (n32 > 0) {
+    rd(va, 0);
+    for (; j + 64 <= n32; j += 64) {
+      rd(vb, j + 32);
+      __builtin_amdgcn_sched_barrier(0);
+      add(va);
+      __builtin_amdgcn_sched_barrier(0);
+      rd(va, j + 64 < n32 ? j + 64 : j);
+      __builtin_amdgcn_sched_barrier(0);
+      add(vb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (j < n32) {
+      add(va);
+      j += 32;
+    }
+  }
+  for (; j < n; j += 4) {
+    const float4 v = *(const float4 *)(q + j);
+    s = s + v.x;
+    s = s + v.y;
+    s = s + v.z;
+    s = s + v.w;
+  }
+  return s;
+}
+
+// RMSNorm of one row per workgroup with the serial sum evaluated
+// speculatively, for rows of up to kSpecMaxH values.  The result is the
+// serial sum itself, bit for bit; only the time depends on the data.
+//
+// The row's squares go to LDS, split into kSpecSegs segments (each a
+// multiple of 4 values), segment j owned by half j % 2 of wave j / 2, whose
+// lanes fold it serially, exactly as the serial sum would, each from its own
+// candidate start: 32 consecutive f32 bit patterns around a prediction of
+// the sum where the segment starts (clamped to [+0, +inf]).  The predictions
+// come in two passes.  Pass A takes the prefix of the segments' sums.
+// The serial sum drifts from the exact one by its rounding errors; a
+// segment's growth (end - start) from its pass-A centre start differs from
+// its growth from the true start by at most an ulp or two (the rounding of a
+// step depends on the start only through the binade and, at an exact tie,
+// the parity of the sum), so pass B predicts each start as the sum of the
+// pass-A growths of the segments before it, and folds its candidates around
+// that.
+// Then the segments are chained in order: the true start of segment 0 is
+// +0; the true start of segment j+1 is the end of segment j from the pass-B
+// lane whose candidate equals segment j's true start bit for bit (or the
+// pass-A lane), and where no candidate does, segment j is folded again from
+// its true start.  Every step of the result is thus the serial sum's own
+// step from the same operand bits.
+//
+// x and w are loaded once (4 values per thread and slot of 2048) and kept in
+// registers for the epilogue, which is rmsnorm_kernel's: y, and with QMODE
+// its Q8_1.  `aligned`: bit 0, rows of x start on 4-value boundaries; bit 1,
+// so do rows of y.  Dynamic LDS: 4 * h bytes.
+constexpr int kSpecSegs = 16;
+constexpr int kSpecCands = 32;
+constexpr int kSpecThreads = kSpecSegs * kSpecCands;
+constexpr int kSpecMaxH = 12288;
+constexpr int kSpecSlots = 7;  // covers h + 511 (Q8_1 blocks padded to 16)
+// float4s of a segment per lane in the exact sums, at most
+constexpr int kSpecRun4 = (kSpecMaxH / 4 / kSpecSegs + kSpecCands - 1) / kSpecCands;
+// bf16 rows up to which the one-row-per-workgroup kernel is used (four per
+// CU; half as many f32 rows, which hold twice the registers); more rows take
+// rmsnorm_kernel, four rows to a workgroup
+constexpr int64_t kSpecMaxRows = 1024;
+
+template <bool XB, bool WB, bool YB, int QMODE>
+__global__ __launch_bounds__(kSpecThreads) void rmsnorm_spec_kernel(
+    const void *__restrict__ x, int64_t ldx, const void *__restrict__ w,
+    float eps, int zero_centered, int32_t h, void *__restrict__ y,
+    int64_t ldy, int8_t *__restrict__ qa, float *__restrict__ sa,
+    int32_t blocks_pad, int aligned, int skew) {
+  extern __shared__ __align__(16) float spec_sq[];
+  // candidate starts and ends of passes A (0) and B (1)
+  __shared__ uint32_t cand_start[2][kSpecSegs][kSpecCands];
+  __shared__ uint32_t cand_end[2][kSpecSegs][kSpecCands];
+  __shared__ float seg_sum[kSpecSegs];
+  __shared__ double seg_grow[kSpecSegs];
+  __shared__ uint32_t seg_guess[kSpecSegs];  // pass B's predictions, as bits
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, p = t & 7;
+  const int seg = t / kSpecCands, c = t % kSpecCands;
+  const int blocks = h / kBlock;
+  const int nb = QMODE != 0 ? blocks_pad : blocks;
+  const int kx = (h + 2047) / 2048, kn = (nb * kBlock + 2047) / 2048;
+  // the arguments the epilogue needs, in registers from the start: a
+  // scalar load still in flight makes every LDS wait a full wait, and the
+  // compiler would otherwise issue them just before the folds
+  asm volatile("" ::"s"(y), "s"(ldy), "s"(qa), "s"(sa), "s"(eps), "s"(zero_centered));
+  uint4 rx[kSpecSlots], rw[kSpecSlots];
+  // slot k of thread t holds values 4t + 2048k .. +3 (past h: the row's last
+  // four, never used)
+  auto load = [&](auto al) __attribute__((always_inline)) {
+    constexpr bool AL = decltype(al)::value;
+#pragma unroll
+    for (int k = 0; k < kSpecSlots; ++k) {
+      if (k < kx) {
+        const int i = min(4 * t + 2048 * k, h - 4);
+        rx[k] = load_raw4<XB, AL>(x, row * ldx + i);
+        rw[k] = load_raw4<WB, true>(w, i);
+      }
+    }
+  };
+  if (aligned & 1)
+    load(std::true_type{});
+  else
+    load(std::false_type{});
+#pragma unroll
+  for (int k = 0; k < kSpecSlots; ++k) {
+    const int i = 4 * t + 2048 * k;
+    if (k < kx && i < h) {
+      const float4 v = act4_of_raw<XB>(rx[k]);
+      *(float4 *)&spec_sq[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+    }
+  }
+  __syncthreads();
+
+  // segment j: float4s [bound4(j), bound4(j + 1)); its sum in f32, in any
+  // order (lane c of the half adding float4s c, c + 32, ...): only pass A's
+  // starts come from these sums, and they need only be close
+  const int h4 = h / 4;
+  auto bound4 = [&](int j) __attribute__((always_inline)) {
+    return (int)(((int64_t)j * h4) / kSpecSegs);
+  };
+  const int f0 = bound4(seg), l4 = bound4(seg + 1) - f0;
+  float loc = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kSpecRun4; ++q) {
+    const int i = c + kSpecCands * q;
+    if (i < l4) {
+      const float4 v = ((const float4 *)spec_sq)[f0 + i];
+      loc += (v.x + v.y) + (v.z + v.w);
+    }
+  }
+#pragma unroll
+  for (int off = kSpecCands / 2; off > 0; off >>= 1) loc += __shfl_xor(loc, off, kSpecCands);
+  if (c == 0) seg_sum[seg] = loc;
+  __syncthreads();
+  float base = 0.0f;
+  {
+    float ss[kSpecSegs];
+#pragma unroll
+    for (int j = 0; j < kSpecSegs; ++j) ss[j] = seg_sum[j];
+#pragma unroll
+    for (int j = 0; j < kSpecSegs; ++j)
+      if (j < seg) base += ss[j];
+  }
+
+  // pass A; the segment's growth from its centre candidate
+  auto candidates = [&](int pass, float guess) __attribute__((always_inline)) {
+    const int cb = (int)min(__float_as_uint(guess), 0x7f800000u) + c - kSpecCands / 2;
+    const uint32_t start = (uint32_t)min(max(cb, 0), 0x7f800000);
+    const float end = fold_serial(spec_sq + 4 * f0, 4 * l4, __uint_as_float(start));
+    cand_start[pass][seg][c] = start;
+    cand_end[pass][seg][c] = __float_as_uint(end);
+    return end;
+  };
+  const float end_a = candidates(0, base);
+  if (c == kSpecCands / 2)
+    seg_grow[seg] = (double)end_a - (double)__uint_as_float(cand_start[0][seg][c]);
+  __syncthreads();
+  // pass B: the sum of the growths before the segment
+  double grown = 0.0;
+  {
+    double sg[kSpecSegs];
+#pragma unroll
+    for (int j = 0; j < kSpecSegs; ++j) sg[j] = seg_grow[j];
+#pragma unroll
+    for (int j = 0; j < kSpecSegs; ++j)
+      if (j < seg) grown += sg[j];
+  }
+  // (skew: a test's offset of the predictions past segment 0, in bits)
+  const int gb = min(max((int)min(__float_as_uint((float)grown), 0x7f800000u) +
+                             (seg > 0 ? skew : 0), 0), 0x7f800000);
+  candidates(1, __uint_as_float((uint32_t)gb));
+  if (c == 0) seg_guess[seg] = (uint32_t)gb;
+  __syncthreads();
+
+  // the chain (every wave, the same values).  A segment's pass-B candidates
+  // start at consecutive bits g - 16 + i (g: its prediction's bits), so the
+  // candidate whose start equals the end of candidate i of segment j is
+  // number end - (g' - 16) of segment j + 1, when in range: nx, one per lane
+  // and pair of segments in registers (lane l: candidate l % 32 of segment
+  // 2i + l / 32); segment 0 starts at +0 = candidate 16 (its prediction is
+  // +0).  The walk is then a chain of register reads.
+  constexpr int kPairs = kSpecSegs / 2;
+  uint32_t nx[kPairs], ce15;
+  {
+    uint32_t gn[kSpecSegs];
+#pragma unroll
+    for (int j = 0; j < kSpecSegs; ++j) gn[j] = seg_guess[j];
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+      const int j = 2 * i + (lane >> 5);
+      const uint32_t en = cand_end[1][j][lane & 31];
+      const uint32_t g1 = lane < 32 ? gn[2 * i + 1] : gn[min(2 * i + 2, kSpecSegs - 1)];
+      const uint32_t n = en - (g1 - kSpecCands / 2);
+      nx[i] = en <= 0x7f800000u && n < (uint32_t)kSpecCands ? n : (uint32_t)kSpecCands;
+    }
+    ce15 = cand_end[1][kSpecSegs - 1][lane & 31];
+  }
+  uint32_t e = 0u;
+  int next = 0;  // the first segment not yet chained
+  {
+    uint32_t idx = kSpecCands / 2, bad = seg_guess[0] != 0u ? 1u : 0u;
+#pragma unroll
+    for (int j = 0; j + 1 < kSpecSegs; ++j) {
+      idx = (uint32_t)__builtin_amdgcn_readlane((int)nx[j / 2], 32 * (j % 2) + (int)idx);
+      bad |= idx >> 5;
+      idx &= 31u;
+    }
+    if (!bad) {
+      e = (uint32_t)__builtin_amdgcn_readlane((int)ce15, 32 + (int)idx);
+      next = kSpecSegs;
+    }
+  }
+  // a segment whose start is not where expected among its pass-B candidates:
+  // any candidate of either pass, else fold it again; and the rest
+  for (; next < kSpecSegs; ++next) {
+    unsigned long long hit = __ballot(cand_start[lane >> 5][next][lane & 31] == e);
+    if (hit != 0ull) {
+      const int l = __ffsll((long long)hit) - 1;
+      e = cand_end[l >> 5][next][l & 31];
+    } else {
+      e = __float_as_uint(fold_serial(spec_sq + 4 * bound4(next),
+                                      4 * (bound4(next + 1) - bound4(next)),
+                                      __uint_as_float(e)));
+    }
+  }
+  const float sum = __uint_as_float(e);
+  const float mean = sum / (float)h;
+  const float var = mean + eps;
+  const float rs = 1.0f / sqrtf(var);
+
+#pragma unroll
+  for (int k = 0; k < kSpecSlots; ++k) {
+    if (k >= kn) continue;
+    const int i = 4 * t + 2048 * k;
+    const int b = i / kBlock;
+    const bool valid = k < kx && i < h, live = b < nb;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) {
+      const float4 xv = act4_of_raw<XB>(rx[k]);
+      float4 wv = act4_of_raw<WB>(rw[k]);
+      if (zero_centered) {
+        wv.x = wv.x + 1.0f;
+        wv.y = wv.y + 1.0f;
+        wv.z = wv.z + 1.0f;
+        wv.w = wv.w + 1.0f;
+      }
+      v.x = (xv.x * rs) * wv.x;
+      v.y = (xv.y * rs) * wv.y;
+      v.z = (xv.z * rs) * wv.z;
+      v.w = (xv.w * rs) * wv.w;
+      if constexpr (YB) {
+        const uint16_t h0 = float_to_bf16(v.x), h1 = float_to_bf16(v.y),
+                       h2 = float_to_bf16(v.z), h3 = float_to_bf16(v.w);
+        uint16_t *yp = (uint16_t *)y + row * ldy + i;
+        if (aligned & 2) {
+          *(uint2 *)yp = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16),
+                                    (uint32_t)h2 | ((uint32_t)h3 << 16));
+        } else {
+          yp[0] = h0;
+          yp[1] = h1;
+          yp[2] = h2;
+          yp[3] = h3;
+        }
+        v = make_float4(bf16_to_float(h0), bf16_to_float(h1), bf16_to_float(h2),
+                        bf16_to_float(h3));
+      } else {
+        float *yp = (float *)y + row * ldy + i;
+        if (aligned & 2) {
+          *(float4 *)yp = v;
+        } else {
+          yp[0] = v.x;
+          yp[1] = v.y;
+          yp[2] = v.z;
+          yp[3] = v.w;
+        }
+      }
+    }
+    if constexpr (QMODE != 0) {
+      int32_t q;
+      float sc;
+      quantize_block8(v, valid, &q, &sc);
+      if (live) {
+        if constexpr (QMODE == 1) {
+          *(int32_t *)(qa + row * ((int64_t)blocks_pad * kBlock) + b * kBlock + 4 * p) = q;
+          if (p == 0) sa[row * blocks_pad + b] = sc;
+        } else {
+          const int64_t tile = (row >> 5) * blocks_pad + b;
+          *(int32_t *)(qa + tile * 1024 + (row & 31) * kBlock + 4 * p) = q;
+          if (p == 0) sa[tile * 32 + (row & 31)] = sc;
+        }
+      }
+    }
+  }
+}
+
 // First-maximum argmax of one f32 row already in HBM (the last row of a
 // prefill lm_head's logits): the same keys as the GEMV's fused argmax,
 // folded into the same slots, so argmax_reduce_kernel finishes it.  A grid
@@ -766,6 +1086,12 @@ hipError_t launch_argmax_reduce(unsigned long long *slots, int64_t *out,
   return hipGetLastError();
 }
 
+// Offset (in f32 bits) added to rmsnorm_spec_kernel's pass-B predictions:
+// 0 except in tests, which move the predictions away to run the fallbacks.
+static int g_spec_skew = 0;
+
+void set_rmsnorm_spec_skew(int bits) { g_spec_skew = bits; }
+
 hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
                           int64_t h, const void *w, bool w_bf16, float eps,
                           bool zero_centered, void *y, bool y_bf16, int64_t ldy,
@@ -776,14 +1102,22 @@ hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
   if ((uintptr_t)w % (w_bf16 ? 8 : 16) != 0) return hipErrorInvalidValue;
   const int64_t esz = x_bf16 ? 2 : 4;
   const int aligned = ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
-  const dim3 grid((unsigned)((m + kNormRows - 1) / kNormRows));
   const int zc = zero_centered ? 1 : 0;
   const int32_t hh = (int32_t)h, bp = (int32_t)blocks_pad;
-#define LLMCP_NORM(XB, WB, YB, Q)                                                         \
-  if (x_bf16 == XB && w_bf16 == WB && y_bf16 == YB && qmode == Q) {                       \
-    hipLaunchKernelGGL((rmsnorm_kernel<XB, WB, YB, Q, false>), grid, dim3(256), 0, s, x, ldx, \
-                       w, eps, zc, m, hh, y, ldy, qa, sa, bp, aligned, nullptr, 0, 0);   \
-    return hipGetLastError();                                                            \
+  const bool spec = h <= kSpecMaxH && m <= (x_bf16 ? kSpecMaxRows : kSpecMaxRows / 2);
+  const int yal = ((uintptr_t)y % (y_bf16 ? 8 : 16) == 0) && (ldy % 4 == 0) ? 1 : 0;
+  const dim3 grid((unsigned)(spec ? m : (m + kNormRows - 1) / kNormRows));
+  const size_t lds = spec ? (size_t)h * sizeof(float) : 0;
+#define LLMCP_NORM(XB, WB, YB, Q)                                                          \
+  if (x_bf16 == XB && w_bf16 == WB && y_bf16 == YB && qmode == Q) {                        \
+    if (spec)                                                                              \
+      hipLaunchKernelGGL((rmsnorm_spec_kernel<XB, WB, YB, Q>), grid, dim3(kSpecThreads), lds, \
+                         s, x, ldx, w, eps, zc, hh, y, ldy, qa, sa, bp, aligned | (yal << 1), \
+                         g_spec_skew);                                                     \
+    else                                                                                   \
+      hipLaunchKernelGGL((rmsnorm_kernel<XB, WB, YB, Q, false>), grid, dim3(256), 0, s, x,  \
+                         ldx, w, eps, zc, m, hh, y, ldy, qa, sa, bp, aligned, nullptr, 0, 0); \
+    return hipGetLastError();                                                              \
   }
   LLMCP_NORM(false, false, false, 0) LLMCP_NORM(false, false, false, 1)
   LLMCP_NORM(false, false, false, 2) LLMCP_NORM(true, true, true, 0)

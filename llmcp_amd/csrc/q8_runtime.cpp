@@ -526,6 +526,11 @@ extern "C" {
 
 int32_t llmcp_q8_abi_version(void) { return LLMCP_Q8_ABI_VERSION; }
 
+int llmcp_q8_test_rmsnorm_skew(int32_t bits) {
+  set_rmsnorm_spec_skew(bits);
+  return LLMCP_Q8_OK;
+}
+
 const char *llmcp_q8_last_error(void) { return g_last_error; }
 
 int llmcp_q8_ctx_create(int device, llmcp_q8_ctx **out) {

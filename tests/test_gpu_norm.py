@@ -36,7 +36,7 @@ def rows_and_weight(rng, m, h, dtype, oracle, scale=1.0):
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("m,h", [(1, 2560), (1, 32), (3, 128), (64, 256), (65, 2560),
-                                 (200, 96), (1, 9216)])
+                                 (200, 96), (1, 9216), (2, 12288), (2, 12320), (1, 16384)])
 @pytest.mark.parametrize("zc", [False, True])
 def test_rmsnorm_bitwise(ctx, oracle, dtype, m, h, zc):
     rng = np.random.default_rng(m * 7 + h + zc)
@@ -68,6 +68,118 @@ def test_rmsnorm_edge_rows(ctx, oracle):
         ctx.rmsnorm(yd, wd, yd, 6, h, eps=eps)
         ref = oracle.rmsnorm(x, w, eps)
         assert same(ctx.to_host(yd, (6, h), np.float32), ref), eps
+
+
+def stalled_rows(h, dtype, oracle):
+    """Rows on which the serial sum stalls, so that any prediction of it from
+    the exact sum is far off: once the sum reaches 2^24, adding 1.0 is an
+    exact tie that rounds back to 2^24 (its even neighbour), while the exact
+    sum keeps growing by 1 per element.  Row 0 stalls from its first element,
+    row 1 half way, row 2 stalls and then meets values large enough to move
+    the sum again, row 3 is the same after a random prefix."""
+    rng = np.random.default_rng(h)
+    x = np.ones((4, h), np.float32)
+    x[0, 0] = 4096.0
+    x[1, : h // 2] = rng.standard_normal(h // 2)
+    x[1, h // 2] = 4096.0
+    x[2, 0] = 4096.0
+    x[2, h // 3 :: 7] = 3.0
+    x[3, : h // 4] = rng.standard_normal(h // 4) * 50
+    x[3, h // 4] = 4096.0
+    w = (rng.standard_normal(h) * 0.1 + 1.0).astype(np.float32)
+    if dtype == "bf16":
+        return oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w)
+    return x, w
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("h", [256, 2560, 9216])
+def test_rmsnorm_stalled_sums(ctx, oracle, dtype, h):
+    """Rows whose serial sum stalls far below the exact one (2^24 where the
+    exact sum is 2^24 + i): the speculative sum's first predictions, taken
+    from the exact partial sums, are far off, and the second pass has to
+    correct them.  The serial sum's value itself is checked against the
+    closed form for row 0."""
+    x, w = stalled_rows(h, dtype, oracle)
+    et = np.float32 if dtype == "f32" else np.uint16
+    xd, wd = ctx.to_device(x), ctx.to_device(w)
+    yd = ctx.alloc(x.nbytes)
+    ctx.rmsnorm(xd, wd, yd, 4, h, eps=1e-6, dtype=dtype)
+    ref, rstd = oracle.rmsnorm(x, w, 1e-6, out_bf16=dtype == "bf16", with_rstd=True)
+    assert rstd[0] == np.float32(1.0) / np.sqrt(np.float32(2.0 ** 24) / np.float32(h)
+                                                  + np.float32(1e-6))
+    assert np.array_equal(bits(ctx.to_host(yd, (4, h), et)), bits(ref))
+
+
+@pytest.mark.parametrize("skew", [64, -40, 20])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("m,h", [(1, 2560), (3, 256), (2, 9216), (1, 12288)])
+def test_rmsnorm_fallbacks(ctx, oracle, q8, skew, dtype, m, h):
+    """Rows of width <= 12288 run the speculative sum: lanes fold each
+    sixteenth of the row from 32 candidate starts around a predicted partial
+    sum, and the segments are chained through the candidates whose start is
+    the true one.  llmcp_q8_test_rmsnorm_skew moves the predictions by
+    `skew` f32 steps, so that the true start is found among the first
+    pass's candidates instead (f32 rows, whose prediction drift is small) or
+    nowhere and the segment is folded again; the results are unchanged."""
+    rng = np.random.default_rng(m + h + skew)
+    x, w = rows_and_weight(rng, m, h, dtype, oracle, scale=2.0)
+    et = np.float32 if dtype == "f32" else np.uint16
+    xd, wd = ctx.to_device(x), ctx.to_device(w)
+    yd = ctx.alloc(x.nbytes)
+    L = q8.lib()
+    assert L.llmcp_q8_test_rmsnorm_skew(skew) == 0
+    try:
+        ctx.rmsnorm(xd, wd, yd, m, h, eps=1e-6, zero_centered=True, dtype=dtype)
+        got = ctx.to_host(yd, (m, h), et)
+    finally:
+        L.llmcp_q8_test_rmsnorm_skew(0)
+    ref = oracle.rmsnorm(x, w, 1e-6, zero_centered=True, out_bf16=dtype == "bf16")
+    assert np.array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("h", [256, 2560, 12288])
+def test_rmsnorm_nan_rows(ctx, oracle, dtype, h):
+    """A NaN among the values makes the sum NaN from its segment on (the
+    speculative sum's chain falls back there); rows without one are
+    unaffected."""
+    m = 4
+    rng = np.random.default_rng(h)
+    x = rng.standard_normal((m, h)).astype(np.float32)
+    x[0, 0] = np.nan
+    x[1, h // 2 + 3] = np.nan
+    x[2, h - 1] = np.nan
+    w = (rng.standard_normal(h) * 0.1 + 1.0).astype(np.float32)
+    if dtype == "bf16":
+        x, w = oracle.f32_to_bf16_bits(x), oracle.f32_to_bf16_bits(w)
+    et = np.float32 if dtype == "f32" else np.uint16
+    xd, wd = ctx.to_device(x), ctx.to_device(w)
+    yd = ctx.alloc(x.nbytes)
+    ctx.rmsnorm(xd, wd, yd, m, h, eps=1e-6, dtype=dtype)
+    ref = oracle.rmsnorm(x, w, 1e-6, out_bf16=dtype == "bf16")
+    got = ctx.to_host(yd, (m, h), et)
+    if dtype == "bf16":
+        got, ref = oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref)
+    assert np.isnan(got[:3]).all()
+    assert same(got, ref)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("h", [2560, 16384])
+def test_rmsnorm_unaligned_rows(ctx, oracle, dtype, h):
+    """Rows that start one element past a vector boundary take the element
+    loads (both kernels)."""
+    m = 3
+    rng = np.random.default_rng(h + 5)
+    x, w = rows_and_weight(rng, m, h, dtype, oracle, scale=2.0)
+    esz, et = (4, np.float32) if dtype == "f32" else (2, np.uint16)
+    flat = np.concatenate([np.zeros(1, x.dtype), x.reshape(-1)])
+    xd, wd = ctx.to_device(flat), ctx.to_device(w)
+    yd = ctx.alloc(x.nbytes)
+    ctx.rmsnorm(xd.ptr + esz, wd, yd, m, h, eps=1e-6, zero_centered=True, dtype=dtype)
+    ref = oracle.rmsnorm(x, w, 1e-6, zero_centered=True, out_bf16=dtype == "bf16")
+    assert np.array_equal(bits(ctx.to_host(yd, (m, h), et)), bits(ref))
 
 
 def test_rmsnorm_declines(ctx, q8):
