@@ -523,13 +523,14 @@ __device__ __forceinline__ float fold_serial(const float *q, int n, float s) {
 // speculatively, for rows of up to kSpecMaxH values.  The result is the
 // serial sum itself, bit for bit; only the time depends on the data.
 //
-// The row's squares go to LDS, split into kSpecSegs segments (each a
-// multiple of 4 values), segment j owned by half j % 2 of wave j / 2, whose
+// The row's squares go to LDS, split into kSpecSegs segments of whole
+// 32-value blocks, segment j owned by half j % 2 of wave j / 2, whose
 // lanes fold it serially, exactly as the serial sum would, each from its own
 // candidate start: 32 consecutive f32 bit patterns around a prediction of
 // the sum where the segment starts (clamped to [+0, +inf]).  The predictions
-// come in two passes.  Pass A takes the prefix of the segments' sums.
-// The serial sum drifts from the exact one by its rounding errors; a
+// come in two passes.  Pass A takes the prefix of the segments' sums (f32,
+// any order).  The serial sum drifts from the exact one by its rounding
+// errors; a
 // segment's growth (end - start) from its pass-A centre start differs from
 // its growth from the true start by at most an ulp or two (the rounding of a
 // step depends on the start only through the binade and, at an exact tie,
@@ -543,16 +544,16 @@ __device__ __forceinline__ float fold_serial(const float *q, int n, float s) {
 // its true start.  Every step of the result is thus the serial sum's own
 // step from the same operand bits.
 //
-// x and w are loaded once (4 values per thread and slot of 2048) and kept in
-// registers for the epilogue, which is rmsnorm_kernel's: y, and with QMODE
-// its Q8_1.  `aligned`: bit 0, rows of x start on 4-value boundaries; bit 1,
-// so do rows of y.  Dynamic LDS: 4 * h bytes.
+// x and w are loaded once, each lane four values at a time from its own
+// segment, and kept in registers for the epilogue, which is
+// rmsnorm_kernel's: y, and with QMODE its Q8_1.  `aligned`: bit 0, rows of x
+// start on 4-value boundaries; bit 1, so do rows of y.  Dynamic LDS: 4 * h
+// bytes.
 constexpr int kSpecSegs = 16;
 constexpr int kSpecCands = 32;
 constexpr int kSpecThreads = kSpecSegs * kSpecCands;
 constexpr int kSpecMaxH = 12288;
-constexpr int kSpecSlots = 7;  // covers h + 511 (Q8_1 blocks padded to 16)
-// float4s of a segment per lane in the exact sums, at most
+// float4s of a segment per lane, at most
 constexpr int kSpecRun4 = (kSpecMaxH / 4 / kSpecSegs + kSpecCands - 1) / kSpecCands;
 // bf16 rows up to which the one-row-per-workgroup kernel is used (four per
 // CU; half as many f32 rows, which hold twice the registers); more rows take
@@ -576,23 +577,30 @@ __global__ __launch_bounds__(kSpecThreads) void rmsnorm_spec_kernel(
   const int t = threadIdx.x, lane = t & 63, p = t & 7;
   const int seg = t / kSpecCands, c = t % kSpecCands;
   const int blocks = h / kBlock;
-  const int nb = QMODE != 0 ? blocks_pad : blocks;
-  const int kx = (h + 2047) / 2048, kn = (nb * kBlock + 2047) / 2048;
   // the arguments the epilogue needs, in registers from the start: a
   // scalar load still in flight makes every LDS wait a full wait, and the
   // compiler would otherwise issue them just before the folds
   asm volatile("" ::"s"(y), "s"(ldy), "s"(qa), "s"(sa), "s"(eps), "s"(zero_centered));
-  uint4 rx[kSpecSlots], rw[kSpecSlots];
-  // slot k of thread t holds values 4t + 2048k .. +3 (past h: the row's last
-  // four, never used)
+  // segment j: whole 32-value blocks [lo, hi) with lo = j * blocks / 16, as
+  // float4s [8 lo, 8 hi); lane c of its half holds float4s f0 + c + 32 q of
+  // x and w in registers (whole blocks in eight consecutive lanes, as the
+  // quantizer wants them)
+  auto seg4 = [&](int j) __attribute__((always_inline)) {
+    return 8 * (int)(((int64_t)j * blocks) / kSpecSegs);
+  };
+  const int f0 = seg4(seg), l4 = seg4(seg + 1) - f0;
+  // float4s per lane in the longest segment (the same in every lane)
+  const int r4 = (8 * ((blocks + kSpecSegs - 1) / kSpecSegs) + kSpecCands - 1) / kSpecCands;
+  uint4 rx[kSpecRun4], rw[kSpecRun4];
   auto load = [&](auto al) __attribute__((always_inline)) {
     constexpr bool AL = decltype(al)::value;
 #pragma unroll
-    for (int k = 0; k < kSpecSlots; ++k) {
-      if (k < kx) {
-        const int i = min(4 * t + 2048 * k, h - 4);
-        rx[k] = load_raw4<XB, AL>(x, row * ldx + i);
-        rw[k] = load_raw4<WB, true>(w, i);
+    for (int q = 0; q < kSpecRun4; ++q) {
+      if (q < r4) {
+        // past the segment: its first float4 again, never used
+        const int i = 4 * (f0 + (c + kSpecCands * q < l4 ? c + kSpecCands * q : 0));
+        rx[q] = load_raw4<XB, AL>(x, row * ldx + min(i, h - 4));
+        rw[q] = load_raw4<WB, true>(w, min(i, h - 4));
       }
     }
   };
@@ -600,31 +608,16 @@ __global__ __launch_bounds__(kSpecThreads) void rmsnorm_spec_kernel(
     load(std::true_type{});
   else
     load(std::false_type{});
-#pragma unroll
-  for (int k = 0; k < kSpecSlots; ++k) {
-    const int i = 4 * t + 2048 * k;
-    if (k < kx && i < h) {
-      const float4 v = act4_of_raw<XB>(rx[k]);
-      *(float4 *)&spec_sq[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
-    }
-  }
-  __syncthreads();
-
-  // segment j: float4s [bound4(j), bound4(j + 1)); its sum in f32, in any
-  // order (lane c of the half adding float4s c, c + 32, ...): only pass A's
-  // starts come from these sums, and they need only be close
-  const int h4 = h / 4;
-  auto bound4 = [&](int j) __attribute__((always_inline)) {
-    return (int)(((int64_t)j * h4) / kSpecSegs);
-  };
-  const int f0 = bound4(seg), l4 = bound4(seg + 1) - f0;
+  // squares to LDS; the segment's sum in f32, in any order (only pass A's
+  // starts come from these sums, and they need only be close)
   float loc = 0.0f;
 #pragma unroll
   for (int q = 0; q < kSpecRun4; ++q) {
-    const int i = c + kSpecCands * q;
-    if (i < l4) {
-      const float4 v = ((const float4 *)spec_sq)[f0 + i];
-      loc += (v.x + v.y) + (v.z + v.w);
+    if (q < r4 && c + kSpecCands * q < l4) {
+      const float4 v = act4_of_raw<XB>(rx[q]);
+      const float4 sq = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+      *(float4 *)&spec_sq[4 * (f0 + c + kSpecCands * q)] = sq;
+      loc += (sq.x + sq.y) + (sq.z + sq.w);
     }
   }
 #pragma unroll
@@ -672,53 +665,58 @@ __global__ __launch_bounds__(kSpecThreads) void rmsnorm_spec_kernel(
   __syncthreads();
 
   // the chain (every wave, the same values).  A segment's pass-B candidates
-  // start at consecutive bits g - 16 + i (g: its prediction's bits), so the
-  // candidate whose start equals the end of candidate i of segment j is
-  // number end - (g' - 16) of segment j + 1, when in range: nx, one per lane
-  // and pair of segments in registers (lane l: candidate l % 32 of segment
-  // 2i + l / 32); segment 0 starts at +0 = candidate 16 (its prediction is
-  // +0).  The walk is then a chain of register reads.
-  constexpr int kPairs = kSpecSegs / 2;
-  uint32_t nx[kPairs], ce15;
+  // start at consecutive bits g - C/2 + i (g: its prediction's bits, C the
+  // candidates per segment), so the candidate whose start equals the end of
+  // candidate i of segment j is number end - (g' - C/2) of segment j + 1,
+  // when in range: nx, in registers (lane l: candidate l % C of segment
+  // G r + l / C in register r, G = 64 / C segments per wave); segment 0
+  // starts at +0 = candidate C/2 (its prediction is +0).  The walk is then a
+  // chain of register reads.
+  constexpr int kC = kSpecCands, kG = 64 / kSpecCands, kR = kSpecSegs / kG;
+  uint32_t nx[kR], ce_last;
   {
     uint32_t gn[kSpecSegs];
 #pragma unroll
     for (int j = 0; j < kSpecSegs; ++j) gn[j] = seg_guess[j];
 #pragma unroll
-    for (int i = 0; i < kPairs; ++i) {
-      const int j = 2 * i + (lane >> 5);
-      const uint32_t en = cand_end[1][j][lane & 31];
-      const uint32_t g1 = lane < 32 ? gn[2 * i + 1] : gn[min(2 * i + 2, kSpecSegs - 1)];
-      const uint32_t n = en - (g1 - kSpecCands / 2);
-      nx[i] = en <= 0x7f800000u && n < (uint32_t)kSpecCands ? n : (uint32_t)kSpecCands;
+    for (int r = 0; r < kR; ++r) {
+      const int j = kG * r + lane / kC;
+      const uint32_t en = cand_end[1][j][lane % kC];
+      uint32_t g1 = gn[min(kG * r + 1, kSpecSegs - 1)];
+#pragma unroll
+      for (int k = 1; k < kG; ++k)
+        if (lane / kC == k) g1 = gn[min(kG * r + k + 1, kSpecSegs - 1)];
+      const uint32_t n = en - (g1 - kC / 2);
+      nx[r] = en <= 0x7f800000u && n < (uint32_t)kC ? n : (uint32_t)kC;
     }
-    ce15 = cand_end[1][kSpecSegs - 1][lane & 31];
+    ce_last = cand_end[1][kSpecSegs - 1][lane % kC];
   }
   uint32_t e = 0u;
   int next = 0;  // the first segment not yet chained
   {
-    uint32_t idx = kSpecCands / 2, bad = seg_guess[0] != 0u ? 1u : 0u;
+    uint32_t idx = kC / 2, bad = seg_guess[0] != 0u ? 1u : 0u;
 #pragma unroll
     for (int j = 0; j + 1 < kSpecSegs; ++j) {
-      idx = (uint32_t)__builtin_amdgcn_readlane((int)nx[j / 2], 32 * (j % 2) + (int)idx);
-      bad |= idx >> 5;
-      idx &= 31u;
+      idx = (uint32_t)__builtin_amdgcn_readlane((int)nx[j / kG], kC * (j % kG) + (int)idx);
+      bad |= idx / kC;
+      idx &= kC - 1u;
     }
     if (!bad) {
-      e = (uint32_t)__builtin_amdgcn_readlane((int)ce15, 32 + (int)idx);
+      e = (uint32_t)__builtin_amdgcn_readlane((int)ce_last, (int)idx);
       next = kSpecSegs;
     }
   }
   // a segment whose start is not where expected among its pass-B candidates:
   // any candidate of either pass, else fold it again; and the rest
   for (; next < kSpecSegs; ++next) {
-    unsigned long long hit = __ballot(cand_start[lane >> 5][next][lane & 31] == e);
+    const unsigned long long hit =
+        __ballot(lane < 2 * kC && cand_start[lane / kC % 2][next][lane % kC] == e);
     if (hit != 0ull) {
       const int l = __ffsll((long long)hit) - 1;
-      e = cand_end[l >> 5][next][l & 31];
+      e = cand_end[l / kC][next][l % kC];
     } else {
-      e = __float_as_uint(fold_serial(spec_sq + 4 * bound4(next),
-                                      4 * (bound4(next + 1) - bound4(next)),
+      e = __float_as_uint(fold_serial(spec_sq + 4 * seg4(next),
+                                      4 * (seg4(next + 1) - seg4(next)),
                                       __uint_as_float(e)));
     }
   }
@@ -728,65 +726,73 @@ __global__ __launch_bounds__(kSpecThreads) void rmsnorm_spec_kernel(
   const float rs = 1.0f / sqrtf(var);
 
 #pragma unroll
-  for (int k = 0; k < kSpecSlots; ++k) {
-    if (k >= kn) continue;
-    const int i = 4 * t + 2048 * k;
-    const int b = i / kBlock;
-    const bool valid = k < kx && i < h, live = b < nb;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (valid) {
-      const float4 xv = act4_of_raw<XB>(rx[k]);
-      float4 wv = act4_of_raw<WB>(rw[k]);
-      if (zero_centered) {
-        wv.x = wv.x + 1.0f;
-        wv.y = wv.y + 1.0f;
-        wv.z = wv.z + 1.0f;
-        wv.w = wv.w + 1.0f;
-      }
-      v.x = (xv.x * rs) * wv.x;
-      v.y = (xv.y * rs) * wv.y;
-      v.z = (xv.z * rs) * wv.z;
-      v.w = (xv.w * rs) * wv.w;
-      if constexpr (YB) {
-        const uint16_t h0 = float_to_bf16(v.x), h1 = float_to_bf16(v.y),
-                       h2 = float_to_bf16(v.z), h3 = float_to_bf16(v.w);
-        uint16_t *yp = (uint16_t *)y + row * ldy + i;
-        if (aligned & 2) {
-          *(uint2 *)yp = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16),
-                                    (uint32_t)h2 | ((uint32_t)h3 << 16));
-        } else {
-          yp[0] = h0;
-          yp[1] = h1;
-          yp[2] = h2;
-          yp[3] = h3;
-        }
-        v = make_float4(bf16_to_float(h0), bf16_to_float(h1), bf16_to_float(h2),
-                        bf16_to_float(h3));
+  for (int q = 0; q < kSpecRun4; ++q) {
+    const int i4 = f0 + c + kSpecCands * q, i = 4 * i4, b = i4 / 8;
+    // whole blocks: the lane's 8-group agrees
+    if (q >= r4 || c + kSpecCands * q >= l4) continue;
+    const float4 xv = act4_of_raw<XB>(rx[q]);
+    float4 wv = act4_of_raw<WB>(rw[q]);
+    if (zero_centered) {
+      wv.x = wv.x + 1.0f;
+      wv.y = wv.y + 1.0f;
+      wv.z = wv.z + 1.0f;
+      wv.w = wv.w + 1.0f;
+    }
+    float4 v;
+    v.x = (xv.x * rs) * wv.x;
+    v.y = (xv.y * rs) * wv.y;
+    v.z = (xv.z * rs) * wv.z;
+    v.w = (xv.w * rs) * wv.w;
+    if constexpr (YB) {
+      const uint16_t h0 = float_to_bf16(v.x), h1 = float_to_bf16(v.y),
+                     h2 = float_to_bf16(v.z), h3 = float_to_bf16(v.w);
+      uint16_t *yp = (uint16_t *)y + row * ldy + i;
+      if (aligned & 2) {
+        *(uint2 *)yp = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16),
+                                  (uint32_t)h2 | ((uint32_t)h3 << 16));
       } else {
-        float *yp = (float *)y + row * ldy + i;
-        if (aligned & 2) {
-          *(float4 *)yp = v;
-        } else {
-          yp[0] = v.x;
-          yp[1] = v.y;
-          yp[2] = v.z;
-          yp[3] = v.w;
-        }
+        yp[0] = h0;
+        yp[1] = h1;
+        yp[2] = h2;
+        yp[3] = h3;
+      }
+      v = make_float4(bf16_to_float(h0), bf16_to_float(h1), bf16_to_float(h2),
+                      bf16_to_float(h3));
+    } else {
+      float *yp = (float *)y + row * ldy + i;
+      if (aligned & 2) {
+        *(float4 *)yp = v;
+      } else {
+        yp[0] = v.x;
+        yp[1] = v.y;
+        yp[2] = v.z;
+        yp[3] = v.w;
       }
     }
     if constexpr (QMODE != 0) {
-      int32_t q;
+      int32_t qv;
       float sc;
-      quantize_block8(v, valid, &q, &sc);
-      if (live) {
-        if constexpr (QMODE == 1) {
-          *(int32_t *)(qa + row * ((int64_t)blocks_pad * kBlock) + b * kBlock + 4 * p) = q;
-          if (p == 0) sa[row * blocks_pad + b] = sc;
-        } else {
-          const int64_t tile = (row >> 5) * blocks_pad + b;
-          *(int32_t *)(qa + tile * 1024 + (row & 31) * kBlock + 4 * p) = q;
-          if (p == 0) sa[tile * 32 + (row & 31)] = sc;
-        }
+      quantize_block8(v, true, &qv, &sc);
+      if constexpr (QMODE == 1) {
+        *(int32_t *)(qa + row * ((int64_t)blocks_pad * kBlock) + b * kBlock + 4 * p) = qv;
+        if (p == 0) sa[row * blocks_pad + b] = sc;
+      } else {
+        const int64_t tile = (row >> 5) * blocks_pad + b;
+        *(int32_t *)(qa + tile * 1024 + (row & 31) * kBlock + 4 * p) = qv;
+        if (p == 0) sa[tile * 32 + (row & 31)] = sc;
+      }
+    }
+  }
+  if constexpr (QMODE != 0) {
+    // blocks past H up to blocks_pad: zeros, as the quantizer gives them
+    for (int b = blocks + t / 8; b < blocks_pad; b += kSpecThreads / 8) {
+      if constexpr (QMODE == 1) {
+        *(int32_t *)(qa + row * ((int64_t)blocks_pad * kBlock) + b * kBlock + 4 * p) = 0;
+        if (p == 0) sa[row * blocks_pad + b] = 0.0f;
+      } else {
+        const int64_t tile = (row >> 5) * blocks_pad + b;
+        *(int32_t *)(qa + tile * 1024 + (row & 31) * kBlock + 4 * p) = 0;
+        if (p == 0) sa[tile * 32 + (row & 31)] = 0.0f;
       }
     }
   }
