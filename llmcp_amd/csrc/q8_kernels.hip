@@ -798,6 +798,137 @@ __global__ __launch_bounds__(kSpecThreads) void rmsnorm_spec_kernel(
   }
 }
 
+// Gated RMSNorm, four groups of g values (g % 32 == 0, g <= kGatedMaxG) per
+// 512-thread workgroup, two waves per group: wave j < 4 loads group j's x,
+// writes its squares to LDS and folds them serially (every lane the same
+// chain, from broadcast reads) into rstd; wave 4 + j meanwhile loads x,
+// the gate and the weight and forms p = (x * s) * w, s = silu(gate) or the
+// gate; after one barrier it writes y = p * rstd.  The gate's exp runs
+// beside the fold instead of after it.  `aligned`: bit 0, x and gate on
+// 4-value boundaries; bit 1, y.
+constexpr int kGatedMaxG = 2048;
+constexpr int kGatedSlots = kGatedMaxG / 256;  // float4s per lane
+
+template <bool XB>
+__global__ __launch_bounds__(512) void gated_rmsnorm_kernel(
+    const void *__restrict__ x, const void *__restrict__ gate, const float *__restrict__ w,
+    int64_t groups, int32_t g, float eps, int gate_activated, void *__restrict__ y,
+    int aligned) {
+  extern __shared__ __align__(16) float gated_sq[];
+  __shared__ float gated_rstd[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = wave & 3;
+  const int64_t grp = (int64_t)blockIdx.x * 4 + j;
+  const bool live = grp < groups;  // uniform per wave
+  const int g4 = g / 4, slots = (g4 + 63) / 64;
+  asm volatile("" ::"s"(y), "s"(eps), "s"(gate_activated));
+  float4 pv[kGatedSlots];
+  if (wave < 4) {
+    uint4 rx[kGatedSlots];
+    auto load = [&](auto al) __attribute__((always_inline)) {
+      constexpr bool AL = decltype(al)::value;
+#pragma unroll
+      for (int k = 0; k < kGatedSlots; ++k)
+        if (k < slots) rx[k] = load_raw4<XB, AL>(x, grp * g + 4 * min(lane + 64 * k, g4 - 1));
+    };
+    if (live) {
+      if (aligned & 1)
+        load(std::true_type{});
+      else
+        load(std::false_type{});
+      float *sq = gated_sq + j * g;
+#pragma unroll
+      for (int k = 0; k < kGatedSlots; ++k) {
+        if (k < slots && lane + 64 * k < g4) {
+          const float4 v = act4_of_raw<XB>(rx[k]);
+          *(float4 *)&sq[4 * (lane + 64 * k)] =
+              make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+        }
+      }
+      // the wave's own LDS rows, read back in order by the same wave
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      const float sum = fold_serial(sq, g, 0.0f);
+      const float mean = sum / (float)g;
+      const float var = mean + eps;
+      if (lane == 0) gated_rstd[j] = 1.0f / sqrtf(var);
+    }
+  } else if (live) {
+    uint4 rx[kGatedSlots], rg[kGatedSlots];
+    float4 wv[kGatedSlots];
+    auto load = [&](auto al) __attribute__((always_inline)) {
+      constexpr bool AL = decltype(al)::value;
+#pragma unroll
+      for (int k = 0; k < kGatedSlots; ++k) {
+        if (k < slots) {
+          const int i = 4 * min(lane + 64 * k, g4 - 1);
+          rx[k] = load_raw4<XB, AL>(x, grp * g + i);
+          rg[k] = load_raw4<XB, AL>(gate, grp * g + i);
+          wv[k] = *(const float4 *)(w + i);
+        }
+      }
+    };
+    if (aligned & 1)
+      load(std::true_type{});
+    else
+      load(std::false_type{});
+#pragma unroll
+    for (int k = 0; k < kGatedSlots; ++k) {
+      if (k < slots) {
+        const float4 xv = act4_of_raw<XB>(rx[k]);
+        float4 gv = act4_of_raw<XB>(rg[k]);
+        if (!gate_activated) {
+          gv.x = silu_f32(gv.x);
+          gv.y = silu_f32(gv.y);
+          gv.z = silu_f32(gv.z);
+          gv.w = silu_f32(gv.w);
+        }
+        pv[k].x = (xv.x * gv.x) * wv[k].x;
+        pv[k].y = (xv.y * gv.y) * wv[k].y;
+        pv[k].z = (xv.z * gv.z) * wv[k].z;
+        pv[k].w = (xv.w * gv.w) * wv[k].w;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave < 4 || !live) return;
+  const float rs = gated_rstd[j];
+#pragma unroll
+  for (int k = 0; k < kGatedSlots; ++k) {
+    if (k < slots && lane + 64 * k < g4) {
+      const int i = 4 * (lane + 64 * k);
+      float4 v;
+      v.x = pv[k].x * rs;
+      v.y = pv[k].y * rs;
+      v.z = pv[k].z * rs;
+      v.w = pv[k].w * rs;
+      if constexpr (XB) {
+        const uint16_t h0 = float_to_bf16(v.x), h1 = float_to_bf16(v.y),
+                       h2 = float_to_bf16(v.z), h3 = float_to_bf16(v.w);
+        uint16_t *yp = (uint16_t *)y + grp * g + i;
+        if (aligned & 2) {
+          *(uint2 *)yp = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16),
+                                    (uint32_t)h2 | ((uint32_t)h3 << 16));
+        } else {
+          yp[0] = h0;
+          yp[1] = h1;
+          yp[2] = h2;
+          yp[3] = h3;
+        }
+      } else {
+        float *yp = (float *)y + grp * g + i;
+        if (aligned & 2) {
+          *(float4 *)yp = v;
+        } else {
+          yp[0] = v.x;
+          yp[1] = v.y;
+          yp[2] = v.z;
+          yp[3] = v.w;
+        }
+      }
+    }
+  }
+}
+
 // First-maximum argmax of one f32 row already in HBM (the last row of a
 // prefill lm_head's logits): the same keys as the GEMV's fused argmax,
 // folded into the same slots, so argmax_reduce_kernel finishes it.  A grid
@@ -1145,6 +1276,17 @@ hipError_t launch_gated_rmsnorm(const void *x, const void *gate, bool bf16,
   const dim3 grid((unsigned)((groups + kNormRows - 1) / kNormRows));
   const int32_t gg = (int32_t)g;
   const int ga = gate_activated ? 1 : 0;
+  if (g <= kGatedMaxG) {
+    const int yal = (uintptr_t)y % (4 * esz) == 0 ? 2 : 0;
+    const size_t lds = (size_t)4 * g * sizeof(float);
+    if (bf16)
+      hipLaunchKernelGGL(gated_rmsnorm_kernel<true>, grid, dim3(512), lds, s, x, gate, w,
+                         groups, gg, eps, ga, y, aligned | yal);
+    else
+      hipLaunchKernelGGL(gated_rmsnorm_kernel<false>, grid, dim3(512), lds, s, x, gate, w,
+                         groups, gg, eps, ga, y, aligned | yal);
+    return hipGetLastError();
+  }
   if (bf16)
     hipLaunchKernelGGL((rmsnorm_kernel<true, false, true, 0, true>), grid, dim3(256), 0, s, x, g,
                        w, eps, 0, groups, gg, y, g, nullptr, nullptr, 0, aligned, gate, g, ga);

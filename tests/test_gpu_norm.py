@@ -245,11 +245,12 @@ def test_rmsnorm_linear_group(ctx, oracle, shapes, acts, m, mode, dtype):
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("m,h,group", [(1, 4096, 128), (5, 4096, 128), (70, 256, 64),
-                                       (1, 32, 32)])
+                                       (1, 32, 32), (3, 2048, 2048), (2, 8192, 4096)])
 @pytest.mark.parametrize("activated", [False, True])
 def test_gated_rmsnorm_bitwise(ctx, oracle, dtype, m, h, group, activated):
     """The linear-attention output norm: 32 value heads of 128 at the real
-    shape (ModelBuilder.cpp:259-266), f32 weight."""
+    shape (ModelBuilder.cpp:259-266), f32 weight; groups of up to 2048 take
+    the one-wave-per-group kernel, larger ones the four-rows kernel."""
     rng = np.random.default_rng(m + h + group + activated)
     x = (rng.standard_normal((m, h)) * 2).astype(np.float32)
     z = (rng.standard_normal((m, h)) * 3).astype(np.float32)
