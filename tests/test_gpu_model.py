@@ -171,3 +171,79 @@ def test_real_model_arena(q8, oracle):
         assert np.array_equal(ctx.to_host(emb, (1024, HIDDEN), np.uint16),
                               oracle.f32_to_bf16_bits(oracle.embedding(ids, p4, HIDDEN)))
         assert ctx.check_flag() == 0
+
+
+LA = {"qkv": (8192, HIDDEN), "z": (4096, HIDDEN), "a": (32, HIDDEN), "b": (32, HIDDEN),
+      "out": (HIDDEN, 4096), "gate": (FFN, HIDDEN), "up": (FFN, HIDDEN), "down": (HIDDEN, FFN)}
+
+
+def test_decode_layers_with_norms_bf16(ctx, oracle, q8):
+    """Two linear-attention layers of the real model in bf16 at one row, as
+    the model builder chains them around the Q8_0 linears
+    (ModelBuilder.cpp:225-236, :259-266, :271-294): input RMSNorm fused with
+    the in_proj qkv/z/a/b group; the gated RMSNorm of the value heads (a
+    fixed stand-in for the attention core, which is not on this path) with
+    z as the gate; out_proj with the residual; the post-attention RMSNorm;
+    the SwiGLU; down_proj with the residual.  Every tensor is compared with
+    the oracle's composition of the same steps, bit for bit."""
+    eps = 1e-6
+    rng = np.random.default_rng(505)
+    bf = lambda a: oracle.f32_to_bf16_bits(np.asarray(a, np.float32))
+    wf = oracle.bf16_bits_to_f32
+    layers, regs = [], []
+    for li in range(2):
+        w = {}
+        for j, (name, (n, k)) in enumerate(LA.items()):
+            d, _ = ctx.synthesize_p4(seed=9100 + 16 * li + j, rows=n, cols=k)
+            w[name] = ctx.to_host(d, (d.nbytes,), np.uint8)
+            d.free()
+        w["ln"] = bf(rng.standard_normal(HIDDEN) * 0.1)
+        w["post"] = bf(rng.standard_normal(HIDDEN) * 0.1)
+        w["gn"] = (rng.standard_normal(128) * 0.1 + 1.0).astype(np.float32)
+        layers.append(w)
+        regs.append({k: ctx.upload_p4(w[k], *LA[k]) for k in LA})
+    try:
+        x = bf(rng.standard_normal((1, HIDDEN)) * 2.0)
+        v = bf(rng.standard_normal((1, 4096)))
+        xd, vd = ctx.to_device(x), ctx.to_device(v)
+        nd, rd, n2d = ctx.alloc(HIDDEN * 2), ctx.alloc(HIDDEN * 2), ctx.alloc(HIDDEN * 2)
+        gd, hd = ctx.alloc(4096 * 2), ctx.alloc(FFN * 2)
+        group = ["qkv", "z", "a", "b"]
+        outs = [ctx.alloc(LA[k][0] * 2) for k in group]
+        epi = ctx.epilogue
+        for li, (w, t) in enumerate(zip(layers, regs)):
+            lnw, postw, gnw = ctx.to_device(w["ln"]), ctx.to_device(w["post"]), ctx.to_device(w["gn"])
+            ctx.rmsnorm_linear_group(xd, lnw, nd, [t[k] for k in group], outs, 1, eps=eps,
+                                     zero_centered=True, dtype="bf16")
+            ctx.gated_rmsnorm(vd, outs[1], gnw, gd, 1, 4096, 128, eps=eps, dtype="bf16")
+            ctx.linear_add(gd, t["out"], xd, rd, 1, dtype="bf16")
+            ctx.rmsnorm(rd, postw, n2d, 1, HIDDEN, eps=eps, zero_centered=True, dtype="bf16")
+            ctx.swiglu(n2d, t["gate"], t["up"], hd, 1, dtype="bf16")
+            ctx.linear_add(hd, t["down"], rd, xd, 1, dtype="bf16")
+
+            normed = oracle.rmsnorm(x, w["ln"], eps, zero_centered=True, out_bf16=True)
+            got = lambda d, n: ctx.to_host(d, (1, n), np.uint16)
+            assert np.array_equal(got(nd, HIDDEN), normed), li
+            ref = {k: bf(oracle.linear(wf(normed), w[k], LA[k][0], epilogue=epi))
+                   for k in group}
+            for k, o in zip(group, outs):
+                assert np.array_equal(got(o, LA[k][0]), ref[k]), (li, k)
+            gated = oracle.gated_rmsnorm(v, ref["z"], w["gn"], 128, eps, out_bf16=True)
+            assert np.array_equal(got(gd, 4096), gated), li
+            lin = bf(oracle.linear(wf(gated), w["out"], HIDDEN, epilogue=epi))
+            r = bf(wf(lin) + wf(x))
+            assert np.array_equal(got(rd, HIDDEN), r), li
+            n2 = oracle.rmsnorm(r, w["post"], eps, zero_centered=True, out_bf16=True)
+            assert np.array_equal(got(n2d, HIDDEN), n2), li
+            g = bf(oracle.linear(wf(n2), w["gate"], FFN, activation="silu", epilogue=epi))
+            u = bf(oracle.linear(wf(n2), w["up"], FFN, epilogue=epi))
+            h = bf(wf(g) * wf(u))
+            assert np.array_equal(got(hd, FFN), h), li
+            down = bf(oracle.linear(wf(h), w["down"], HIDDEN, epilogue=epi))
+            x = bf(wf(down) + wf(r))
+            assert np.array_equal(got(xd, HIDDEN), x), li
+        assert ctx.check_flag() == 0
+    finally:
+        for t in regs:
+            for wt in t.values():
+                ctx.release(wt)
