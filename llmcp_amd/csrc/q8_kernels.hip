@@ -524,25 +524,24 @@ __device__ __forceinline__ float fold_serial(const float *q, int n, float s) {
 // serial sum itself, bit for bit; only the time depends on the data.
 //
 // The row's squares go to LDS, split into kSpecSegs segments of whole
-// 32-value blocks, segment j owned by half j % 2 of wave j / 2, whose
-// lanes fold it serially, exactly as the serial sum would, each from its own
+// 32-value blocks, segment j owned by half j % 2 of wave j / 2, whose lanes
+// fold it serially, exactly as the serial sum would, each from its own
 // candidate start: 32 consecutive f32 bit patterns around a prediction of
-// the sum where the segment starts (clamped to [+0, +inf]).  The predictions
-// come in two passes.  Pass A takes the prefix of the segments' sums (f32,
-// any order).  The serial sum drifts from the exact one by its rounding
-// errors; a
-// segment's growth (end - start) from its pass-A centre start differs from
-// its growth from the true start by at most an ulp or two (the rounding of a
-// step depends on the start only through the binade and, at an exact tie,
-// the parity of the sum), so pass B predicts each start as the sum of the
-// pass-A growths of the segments before it, and folds its candidates around
-// that.
-// Then the segments are chained in order: the true start of segment 0 is
-// +0; the true start of segment j+1 is the end of segment j from the pass-B
-// lane whose candidate equals segment j's true start bit for bit (or the
-// pass-A lane), and where no candidate does, segment j is folded again from
-// its true start.  Every step of the result is thus the serial sum's own
-// step from the same operand bits.
+// the sum where the segment starts (clamped to [+0, +inf]).  The
+// predictions come in two passes.  Pass A takes the prefix of the segments'
+// sums (f32, any order).  The serial sum drifts from the exact one by its
+// rounding errors, but a segment's growth (end - start) from its pass-A
+// centre start differs from its growth from the true start by an ulp or two
+// at most (the rounding of a step depends on the start only through the
+// binade and, at an exact tie, the parity of the sum); so pass B predicts
+// each start as the sum of the pass-A growths of the segments before it,
+// and folds its candidates around that.  Then the segments are chained in
+// order: the true start of segment 0 is +0; the true start of segment j+1
+// is the end of segment j from a lane (of pass B, else of pass A) whose
+// candidate equals segment j's true start bit for bit, and where no
+// candidate does, segment j is folded again from its true start.  Every
+// step of the result is thus the serial sum's own step from the same
+// operand bits.
 //
 // x and w are loaded once, each lane four values at a time from its own
 // segment, and kept in registers for the epilogue, which is
