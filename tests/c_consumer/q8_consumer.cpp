@@ -225,6 +225,74 @@ int main(int argc, char **argv) {
                 (long long)token, (double)hv[0], (double)lv[0], (long long)best);
     for (void *p : {tok, hid, lg, am}) llmcp_q8_dev_free(ctx, p);
   }
+  // The norms in front of the linears, on rows with closed-form results: a
+  // row of 2.0 has the serial sum 4 H exactly, so rstd = 1 / sqrt(4) = 0.5
+  // (eps 0) and y = (2 * 0.5) * (w + 1) = 1.5 for a zero-centered w of 0.5;
+  // the gated norm of groups of 128 twos with an activated gate of 1.0 and a
+  // weight of 1.0 gives 1.0.  The fused norm + group on the decode weight
+  // must equal a plain linear of the normed row.
+  {
+    const int64_t hdim = cols[1], n = rows[1];
+    MemRef<int8_t, 1> w{(int8_t *)(file + off[1]), (int8_t *)(file + off[1]), 0,
+                        {n * (hdim + hdim / 16)}, {1}};
+    void *xd = nullptr, *wd = nullptr, *yd = nullptr, *gd = nullptr, *gw = nullptr,
+         *o1 = nullptr, *o2 = nullptr;
+    if (llmcp_q8_dev_alloc(ctx, (uint64_t)hdim * 2, &xd) ||
+        llmcp_q8_dev_alloc(ctx, (uint64_t)hdim * 2, &wd) ||
+        llmcp_q8_dev_alloc(ctx, (uint64_t)hdim * 2, &yd) ||
+        llmcp_q8_dev_alloc(ctx, (uint64_t)hdim * 2, &gd) ||
+        llmcp_q8_dev_alloc(ctx, 128 * 4, &gw) ||
+        llmcp_q8_dev_alloc(ctx, (uint64_t)n * 2, &o1) ||
+        llmcp_q8_dev_alloc(ctx, (uint64_t)n * 2, &o2))
+      return fail("alloc");
+    const std::vector<uint16_t> xb(hdim, f32_to_bf16(2.0f)), wb(hdim, f32_to_bf16(0.5f)),
+        ones(hdim, f32_to_bf16(1.0f));
+    const std::vector<float> gwf(128, 1.0f);
+    llmcp_q8_memcpy_h2d(ctx, xd, xb.data(), (uint64_t)hdim * 2);
+    llmcp_q8_memcpy_h2d(ctx, wd, wb.data(), (uint64_t)hdim * 2);
+    llmcp_q8_memcpy_h2d(ctx, gd, ones.data(), (uint64_t)hdim * 2);
+    llmcp_q8_memcpy_h2d(ctx, gw, gwf.data(), 128 * 4);
+    MemRef<uint16_t, 2> xm{(uint16_t *)xd, (uint16_t *)xd, 0, {1, hdim}, {hdim, 1}};
+    MemRef<uint16_t, 2> ym{(uint16_t *)yd, (uint16_t *)yd, 0, {1, hdim}, {hdim, 1}};
+    MemRef<uint16_t, 2> gm{(uint16_t *)gd, (uint16_t *)gd, 0, {1, hdim}, {hdim, 1}};
+    MemRef<uint16_t, 1> wm{(uint16_t *)wd, (uint16_t *)wd, 0, {hdim}, {1}};
+    MemRef<float, 1> gwm{(float *)gw, (float *)gw, 0, {128}, {1}};
+    std::vector<uint16_t> yb(hdim);
+    if (llmcp_q8_rmsnorm_bf16(ctx, (llmcp_memref_bf16_2d *)&xm, (llmcp_memref_bf16_1d *)&wm, 0.0f,
+                              1, (llmcp_memref_bf16_2d *)&ym))
+      return fail("rmsnorm_bf16");
+    llmcp_q8_memcpy_d2h(ctx, yb.data(), yd, (uint64_t)hdim * 2);
+    for (int64_t i = 0; i < hdim; ++i) bad += yb[i] != f32_to_bf16(1.5f);
+    if (llmcp_q8_gated_rmsnorm_bf16(ctx, (llmcp_memref_bf16_2d *)&xm, (llmcp_memref_bf16_2d *)&gm,
+                                    (llmcp_memref_f32_1d *)&gwm, 128, 0.0f, 1,
+                                    (llmcp_memref_bf16_2d *)&ym))
+      return fail("gated_rmsnorm_bf16");
+    llmcp_q8_memcpy_d2h(ctx, yb.data(), yd, (uint64_t)hdim * 2);
+    for (int64_t i = 0; i < hdim; ++i) bad += yb[i] != f32_to_bf16(1.0f);
+    MemRef<uint16_t, 2> om1{(uint16_t *)o1, (uint16_t *)o1, 0, {1, n}, {n, 1}};
+    MemRef<uint16_t, 2> om2{(uint16_t *)o2, (uint16_t *)o2, 0, {1, n}, {n, 1}};
+    const llmcp_memref_i8_1d *ws[1] = {(const llmcp_memref_i8_1d *)&w};
+    llmcp_memref_bf16_2d *os[1] = {(llmcp_memref_bf16_2d *)&om1};
+    const int32_t acts[1] = {LLMCP_Q8_ACT_NONE};
+    if (llmcp_q8_rmsnorm_linear_group_bf16(ctx, (llmcp_memref_bf16_2d *)&xm,
+                                           (llmcp_memref_bf16_1d *)&wm, 0.0f, 1,
+                                           (llmcp_memref_bf16_2d *)&ym, 1, ws, os, acts,
+                                           LLMCP_Q8_DECODE))
+      return fail("rmsnorm_linear_group_bf16");
+    if (_mlir_ciface_llmcp_q8_linear_bf16((llmcp_memref_bf16_2d *)&ym, (llmcp_memref_i8_1d *)&w,
+                                          (llmcp_memref_bf16_2d *)&om2, LLMCP_Q8_ACT_NONE,
+                                          LLMCP_Q8_DECODE))
+      return fail("linear_bf16 of the normed row");
+    std::vector<uint16_t> r1(n), r2(n);
+    llmcp_q8_memcpy_d2h(ctx, yb.data(), yd, (uint64_t)hdim * 2);
+    llmcp_q8_memcpy_d2h(ctx, r1.data(), o1, (uint64_t)n * 2);
+    llmcp_q8_memcpy_d2h(ctx, r2.data(), o2, (uint64_t)n * 2);
+    for (int64_t i = 0; i < hdim; ++i) bad += yb[i] != f32_to_bf16(1.5f);
+    for (int64_t i = 0; i < n; ++i) bad += r1[i] != r2[i];
+    std::printf("q8_consumer: norms: rmsnorm %.4g, gated 1, group output %.6g\n",
+                (double)bf16_to_f32(f32_to_bf16(1.5f)), (double)bf16_to_f32(r1[0]));
+    for (void *q : {xd, wd, yd, gd, gw, o1, o2}) llmcp_q8_dev_free(ctx, q);
+  }
   llmcp_q8_ctx_destroy(ctx);
   munmap(map, fsize);
   if (bad) {
