@@ -138,6 +138,22 @@ def test_rmsnorm_fallbacks(ctx, oracle, q8, skew, dtype, m, h):
     assert np.array_equal(bits(got), bits(ref))
 
 
+@pytest.mark.parametrize("dtype,m,h", [("bf16", 1024, 2560), ("bf16", 1025, 2560),
+                                       ("f32", 512, 2560), ("f32", 513, 1024),
+                                       ("bf16", 700, 12288)])
+def test_rmsnorm_many_rows(ctx, oracle, dtype, m, h):
+    """Row counts at the kernels' hand-over: up to 1024 bf16 rows (512 f32)
+    run one row per workgroup, more run four rows per workgroup."""
+    rng = np.random.default_rng(m + h)
+    x, w = rows_and_weight(rng, m, h, dtype, oracle, scale=1.5)
+    et = np.float32 if dtype == "f32" else np.uint16
+    xd, wd = ctx.to_device(x), ctx.to_device(w)
+    yd = ctx.alloc(x.nbytes)
+    ctx.rmsnorm(xd, wd, yd, m, h, eps=1e-6, zero_centered=True, dtype=dtype)
+    ref = oracle.rmsnorm(x, w, 1e-6, zero_centered=True, out_bf16=dtype == "bf16")
+    assert np.array_equal(bits(ctx.to_host(yd, (m, h), et)), bits(ref))
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("h", [256, 2560, 12288])
 def test_rmsnorm_nan_rows(ctx, oracle, dtype, h):
