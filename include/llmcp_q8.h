@@ -42,10 +42,11 @@ extern "C" {
 /* Version of this C ABI (1: f32 entries; 2: bf16 twins and all four
  * activations; 3: linear + residual add; 4: reference platform switch,
  * weight budget, graph staleness check, grouped linears; 5: RMSNorm, gated
- * RMSNorm and RMSNorm + grouped linears).  The model ABI of
+ * RMSNorm and RMSNorm + grouped linears; 6: their MLIR C-interface entries
+ * and the bf16 group entries).  The model ABI of
  * the AOT library (llmcp_model_abi_version() == 2,
  * include/llmcp/Support/AotAbi.h:12) is not changed by this library. */
-#define LLMCP_Q8_ABI_VERSION 5
+#define LLMCP_Q8_ABI_VERSION 6
 
 enum llmcp_q8_status {
   LLMCP_Q8_OK = 0,
@@ -509,6 +510,54 @@ int32_t _mlir_ciface_llmcp_q8_linear_group4(
     llmcp_memref_i8_1d *w2, llmcp_memref_i8_1d *w3, llmcp_memref_f32_2d *y0,
     llmcp_memref_f32_2d *y1, llmcp_memref_f32_2d *y2, llmcp_memref_f32_2d *y3,
     int32_t act0, int32_t act1, int32_t act2, int32_t act3,
+    int32_t execution_mode);
+/* bf16 twins of the group entries (the real graph's types). */
+int32_t _mlir_ciface_llmcp_q8_linear_group3_bf16(
+    llmcp_memref_bf16_2d *input, llmcp_memref_i8_1d *w0, llmcp_memref_i8_1d *w1,
+    llmcp_memref_i8_1d *w2, llmcp_memref_bf16_2d *y0, llmcp_memref_bf16_2d *y1,
+    llmcp_memref_bf16_2d *y2, int32_t act0, int32_t act1, int32_t act2,
+    int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_linear_group4_bf16(
+    llmcp_memref_bf16_2d *input, llmcp_memref_i8_1d *w0, llmcp_memref_i8_1d *w1,
+    llmcp_memref_i8_1d *w2, llmcp_memref_i8_1d *w3, llmcp_memref_bf16_2d *y0,
+    llmcp_memref_bf16_2d *y1, llmcp_memref_bf16_2d *y2, llmcp_memref_bf16_2d *y3,
+    int32_t act0, int32_t act1, int32_t act2, int32_t act3,
+    int32_t execution_mode);
+/* What the rms_norm / gated_rms_norm patterns call in place of the loop nests
+ * of DecodeNormalization.cpp:71-171 and LowerToLinalg.cpp:245-300, :574-720
+ * (llmcp_q8_rmsnorm and llmcp_q8_gated_rmsnorm on the default context). */
+int32_t _mlir_ciface_llmcp_q8_rmsnorm(llmcp_memref_f32_2d *input, llmcp_memref_f32_1d *weight,
+                                      float eps, int32_t zero_centered,
+                                      llmcp_memref_f32_2d *output);
+int32_t _mlir_ciface_llmcp_q8_rmsnorm_bf16(llmcp_memref_bf16_2d *input,
+                                           llmcp_memref_bf16_1d *weight, float eps,
+                                           int32_t zero_centered,
+                                           llmcp_memref_bf16_2d *output);
+int32_t _mlir_ciface_llmcp_q8_gated_rmsnorm(llmcp_memref_f32_2d *input,
+                                            llmcp_memref_f32_2d *gate,
+                                            llmcp_memref_f32_1d *weight, int64_t group_size,
+                                            float eps, int32_t gate_activated,
+                                            llmcp_memref_f32_2d *output);
+int32_t _mlir_ciface_llmcp_q8_gated_rmsnorm_bf16(llmcp_memref_bf16_2d *input,
+                                                 llmcp_memref_bf16_2d *gate,
+                                                 llmcp_memref_f32_1d *weight,
+                                                 int64_t group_size, float eps,
+                                                 int32_t gate_activated,
+                                                 llmcp_memref_bf16_2d *output);
+/* The norm feeding the q/k/v (3) or qkv/z/a/b (4) group, bf16
+ * (llmcp_q8_rmsnorm_linear_group_bf16 on the default context). */
+int32_t _mlir_ciface_llmcp_q8_rmsnorm_linear_group3_bf16(
+    llmcp_memref_bf16_2d *input, llmcp_memref_bf16_1d *norm_weight, float eps,
+    int32_t zero_centered, llmcp_memref_bf16_2d *normed, llmcp_memref_i8_1d *w0,
+    llmcp_memref_i8_1d *w1, llmcp_memref_i8_1d *w2, llmcp_memref_bf16_2d *y0,
+    llmcp_memref_bf16_2d *y1, llmcp_memref_bf16_2d *y2, int32_t act0, int32_t act1,
+    int32_t act2, int32_t execution_mode);
+int32_t _mlir_ciface_llmcp_q8_rmsnorm_linear_group4_bf16(
+    llmcp_memref_bf16_2d *input, llmcp_memref_bf16_1d *norm_weight, float eps,
+    int32_t zero_centered, llmcp_memref_bf16_2d *normed, llmcp_memref_i8_1d *w0,
+    llmcp_memref_i8_1d *w1, llmcp_memref_i8_1d *w2, llmcp_memref_i8_1d *w3,
+    llmcp_memref_bf16_2d *y0, llmcp_memref_bf16_2d *y1, llmcp_memref_bf16_2d *y2,
+    llmcp_memref_bf16_2d *y3, int32_t act0, int32_t act1, int32_t act2, int32_t act3,
     int32_t execution_mode);
 int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
                                      llmcp_memref_i8_1d *w_gate,

@@ -85,6 +85,11 @@ EXPORTS = [
     "llmcp_q8_rmsnorm", "llmcp_q8_rmsnorm_bf16", "llmcp_q8_rmsnorm_linear_group",
     "llmcp_q8_rmsnorm_linear_group_bf16", "llmcp_q8_gated_rmsnorm",
     "llmcp_q8_gated_rmsnorm_bf16", "llmcp_q8_test_rmsnorm_skew",
+    "_mlir_ciface_llmcp_q8_linear_group3_bf16", "_mlir_ciface_llmcp_q8_linear_group4_bf16",
+    "_mlir_ciface_llmcp_q8_rmsnorm", "_mlir_ciface_llmcp_q8_rmsnorm_bf16",
+    "_mlir_ciface_llmcp_q8_gated_rmsnorm", "_mlir_ciface_llmcp_q8_gated_rmsnorm_bf16",
+    "_mlir_ciface_llmcp_q8_rmsnorm_linear_group3_bf16",
+    "_mlir_ciface_llmcp_q8_rmsnorm_linear_group4_bf16",
 ]
 
 
@@ -176,6 +181,17 @@ def lib():
         "llmcp_q8_gated_rmsnorm_bf16": (I, [P, P, P, P, I64, ctypes.c_float, I32, P]),
         "llmcp_q8_rmsnorm_linear_group_bf16": (I, [P, P, P, ctypes.c_float, I32, P, I32, P, P,
                                                    P, I32]),
+        "_mlir_ciface_llmcp_q8_linear_group3_bf16": (I32, [P] * 7 + [I32] * 4),
+        "_mlir_ciface_llmcp_q8_linear_group4_bf16": (I32, [P] * 9 + [I32] * 5),
+        "_mlir_ciface_llmcp_q8_rmsnorm": (I32, [P, P, ctypes.c_float, I32, P]),
+        "_mlir_ciface_llmcp_q8_rmsnorm_bf16": (I32, [P, P, ctypes.c_float, I32, P]),
+        "_mlir_ciface_llmcp_q8_gated_rmsnorm": (I32, [P, P, P, I64, ctypes.c_float, I32, P]),
+        "_mlir_ciface_llmcp_q8_gated_rmsnorm_bf16": (I32, [P, P, P, I64, ctypes.c_float, I32,
+                                                           P]),
+        "_mlir_ciface_llmcp_q8_rmsnorm_linear_group3_bf16": (
+            I32, [P, P, ctypes.c_float, I32, P] + [P] * 6 + [I32] * 4),
+        "_mlir_ciface_llmcp_q8_rmsnorm_linear_group4_bf16": (
+            I32, [P, P, ctypes.c_float, I32, P] + [P] * 8 + [I32] * 5),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -2102,6 +2102,114 @@ int32_t _mlir_ciface_llmcp_q8_linear_group4(
   });
 }
 
+int32_t _mlir_ciface_llmcp_q8_linear_group3_bf16(
+    llmcp_memref_bf16_2d *input, llmcp_memref_i8_1d *w0, llmcp_memref_i8_1d *w1,
+    llmcp_memref_i8_1d *w2, llmcp_memref_bf16_2d *y0, llmcp_memref_bf16_2d *y1,
+    llmcp_memref_bf16_2d *y2, int32_t act0, int32_t act1, int32_t act2,
+    int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    const llmcp_memref_i8_1d *w[3] = {w0, w1, w2};
+    llmcp_memref_bf16_2d *y[3] = {y0, y1, y2};
+    const int32_t a[3] = {act0, act1, act2};
+    return llmcp_q8_linear_group_bf16(g_default_ctx, input, 3, w, y, a, execution_mode);
+  });
+}
+
+int32_t _mlir_ciface_llmcp_q8_linear_group4_bf16(
+    llmcp_memref_bf16_2d *input, llmcp_memref_i8_1d *w0, llmcp_memref_i8_1d *w1,
+    llmcp_memref_i8_1d *w2, llmcp_memref_i8_1d *w3, llmcp_memref_bf16_2d *y0,
+    llmcp_memref_bf16_2d *y1, llmcp_memref_bf16_2d *y2, llmcp_memref_bf16_2d *y3,
+    int32_t act0, int32_t act1, int32_t act2, int32_t act3,
+    int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    const llmcp_memref_i8_1d *w[4] = {w0, w1, w2, w3};
+    llmcp_memref_bf16_2d *y[4] = {y0, y1, y2, y3};
+    const int32_t a[4] = {act0, act1, act2, act3};
+    return llmcp_q8_linear_group_bf16(g_default_ctx, input, 4, w, y, a, execution_mode);
+  });
+}
+
+int32_t _mlir_ciface_llmcp_q8_rmsnorm(llmcp_memref_f32_2d *input, llmcp_memref_f32_1d *weight,
+                                      float eps, int32_t zero_centered,
+                                      llmcp_memref_f32_2d *output) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_rmsnorm(g_default_ctx, input, weight, eps, zero_centered, output);
+  });
+}
+
+int32_t _mlir_ciface_llmcp_q8_rmsnorm_bf16(llmcp_memref_bf16_2d *input,
+                                           llmcp_memref_bf16_1d *weight, float eps,
+                                           int32_t zero_centered,
+                                           llmcp_memref_bf16_2d *output) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_rmsnorm_bf16(g_default_ctx, input, weight, eps, zero_centered, output);
+  });
+}
+
+int32_t _mlir_ciface_llmcp_q8_gated_rmsnorm(llmcp_memref_f32_2d *input,
+                                            llmcp_memref_f32_2d *gate,
+                                            llmcp_memref_f32_1d *weight, int64_t group_size,
+                                            float eps, int32_t gate_activated,
+                                            llmcp_memref_f32_2d *output) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_gated_rmsnorm(g_default_ctx, input, gate, weight, group_size, eps,
+                                  gate_activated, output);
+  });
+}
+
+int32_t _mlir_ciface_llmcp_q8_gated_rmsnorm_bf16(llmcp_memref_bf16_2d *input,
+                                                 llmcp_memref_bf16_2d *gate,
+                                                 llmcp_memref_f32_1d *weight,
+                                                 int64_t group_size, float eps,
+                                                 int32_t gate_activated,
+                                                 llmcp_memref_bf16_2d *output) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    return llmcp_q8_gated_rmsnorm_bf16(g_default_ctx, input, gate, weight, group_size, eps,
+                                       gate_activated, output);
+  });
+}
+
+int32_t _mlir_ciface_llmcp_q8_rmsnorm_linear_group3_bf16(
+    llmcp_memref_bf16_2d *input, llmcp_memref_bf16_1d *norm_weight, float eps,
+    int32_t zero_centered, llmcp_memref_bf16_2d *normed, llmcp_memref_i8_1d *w0,
+    llmcp_memref_i8_1d *w1, llmcp_memref_i8_1d *w2, llmcp_memref_bf16_2d *y0,
+    llmcp_memref_bf16_2d *y1, llmcp_memref_bf16_2d *y2, int32_t act0, int32_t act1,
+    int32_t act2, int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    const llmcp_memref_i8_1d *w[3] = {w0, w1, w2};
+    llmcp_memref_bf16_2d *y[3] = {y0, y1, y2};
+    const int32_t a[3] = {act0, act1, act2};
+    return llmcp_q8_rmsnorm_linear_group_bf16(g_default_ctx, input, norm_weight, eps,
+                                              zero_centered, normed, 3, w, y, a,
+                                              execution_mode);
+  });
+}
+
+int32_t _mlir_ciface_llmcp_q8_rmsnorm_linear_group4_bf16(
+    llmcp_memref_bf16_2d *input, llmcp_memref_bf16_1d *norm_weight, float eps,
+    int32_t zero_centered, llmcp_memref_bf16_2d *normed, llmcp_memref_i8_1d *w0,
+    llmcp_memref_i8_1d *w1, llmcp_memref_i8_1d *w2, llmcp_memref_i8_1d *w3,
+    llmcp_memref_bf16_2d *y0, llmcp_memref_bf16_2d *y1, llmcp_memref_bf16_2d *y2,
+    llmcp_memref_bf16_2d *y3, int32_t act0, int32_t act1, int32_t act2, int32_t act3,
+    int32_t execution_mode) {
+  return guarded([&]() -> int {
+    if (!g_default_ctx) return fail(LLMCP_Q8_EINVAL, "no default context");
+    const llmcp_memref_i8_1d *w[4] = {w0, w1, w2, w3};
+    llmcp_memref_bf16_2d *y[4] = {y0, y1, y2, y3};
+    const int32_t a[4] = {act0, act1, act2, act3};
+    return llmcp_q8_rmsnorm_linear_group_bf16(g_default_ctx, input, norm_weight, eps,
+                                              zero_centered, normed, 4, w, y, a,
+                                              execution_mode);
+  });
+}
+
 int32_t _mlir_ciface_llmcp_q8_swiglu(llmcp_memref_f32_2d *input,
                                      llmcp_memref_i8_1d *w_gate,
                                      llmcp_memref_i8_1d *w_up,

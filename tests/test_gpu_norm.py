@@ -290,3 +290,90 @@ def test_gated_rmsnorm_declines(ctx, q8):
         ctx.gated_rmsnorm(xd, xd, wd, xd, 1, 256, 96)
     with pytest.raises(q8.Declined):  # group not a multiple of 32
         ctx.gated_rmsnorm(xd, xd, wd, xd, 1, 256, 16)
+
+
+def test_norm_mlir_interface(ctx, oracle, q8):
+    """The _mlir_ciface_ entries a lowering hook calls (default context):
+    each equals the context entry it wraps, bit for bit."""
+    rng = np.random.default_rng(44)
+    L = q8.lib()
+    h = 2560
+    shapes = LINEAR_ATTN
+    p4 = [oracle.pack_q8_0_p4((rng.standard_normal(s) * 0.02).astype(np.float32))
+          for s in shapes]
+    ts = [ctx.upload_p4(p, *s) for p, s in zip(p4, shapes)]
+    ref = lambda r: q8.f32_memref(r.ptr, 1, r.nbytes // 2)
+    try:
+        L.llmcp_q8_set_default_ctx(ctx.handle)
+        x, w = rows_and_weight(rng, 1, h, "bf16", oracle, scale=2.0)
+        xd, wd = ctx.to_device(x), ctx.to_device(w)
+        xi, wv = q8.f32_memref(xd.ptr, 1, h), q8.i8_memref(wd.ptr, h)
+        y1, y2 = ctx.alloc(h * 2), ctx.alloc(h * 2)
+        ctx.rmsnorm(xd, wd, y1, 1, h, eps=1e-6, zero_centered=True, dtype="bf16")
+        yo = q8.f32_memref(y2.ptr, 1, h)
+        assert L._mlir_ciface_llmcp_q8_rmsnorm_bf16(ctypes.byref(xi), ctypes.byref(wv), 1e-6, 1,
+                                                    ctypes.byref(yo)) == q8.OK, q8.last_error()
+        assert np.array_equal(ctx.to_host(y1, (1, h), np.uint16), ctx.to_host(y2, (1, h), np.uint16))
+        # f32 rows and weight
+        xf, wf = rows_and_weight(rng, 3, h, "f32", oracle)
+        xfd, wfd = ctx.to_device(xf), ctx.to_device(wf)
+        f1, f2 = ctx.alloc(xf.nbytes), ctx.alloc(xf.nbytes)
+        ctx.rmsnorm(xfd, wfd, f1, 3, h)
+        xfi, wfv, fo = (q8.f32_memref(xfd.ptr, 3, h), q8.i8_memref(wfd.ptr, h),
+                        q8.f32_memref(f2.ptr, 3, h))
+        assert L._mlir_ciface_llmcp_q8_rmsnorm(ctypes.byref(xfi), ctypes.byref(wfv), 1e-6, 0,
+                                               ctypes.byref(fo)) == q8.OK, q8.last_error()
+        assert np.array_equal(bits(ctx.to_host(f1, (3, h), np.float32)),
+                              bits(ctx.to_host(f2, (3, h), np.float32)))
+        # gated, bf16 and f32
+        g = 4096
+        gw = ctx.to_device((rng.standard_normal(128) * 0.1 + 1).astype(np.float32))
+        gv = q8.i8_memref(gw.ptr, 128)
+        for dt, esz, et, fn in (("bf16", 2, np.uint16, L._mlir_ciface_llmcp_q8_gated_rmsnorm_bf16),
+                                ("f32", 4, np.float32, L._mlir_ciface_llmcp_q8_gated_rmsnorm)):
+            v = (rng.standard_normal((1, g)) * 2).astype(np.float32)
+            z = (rng.standard_normal((1, g)) * 3).astype(np.float32)
+            if dt == "bf16":
+                v, z = oracle.f32_to_bf16_bits(v), oracle.f32_to_bf16_bits(z)
+            vd, zd = ctx.to_device(v), ctx.to_device(z)
+            o1, o2 = ctx.alloc(g * esz), ctx.alloc(g * esz)
+            ctx.gated_rmsnorm(vd, zd, gw, o1, 1, g, 128, dtype=dt)
+            vi, zi, oo = (q8.f32_memref(vd.ptr, 1, g), q8.f32_memref(zd.ptr, 1, g),
+                          q8.f32_memref(o2.ptr, 1, g))
+            assert fn(ctypes.byref(vi), ctypes.byref(zi), ctypes.byref(gv), 128, 1e-6, 0,
+                      ctypes.byref(oo)) == q8.OK, q8.last_error()
+            assert np.array_equal(bits(ctx.to_host(o1, (1, g), et)),
+                                  bits(ctx.to_host(o2, (1, g), et)))
+        # the norm feeding qkv/z/a/b (4) and q/k/v-like (3), and the plain groups
+        acts = [0, 1, 0, 3]
+        for cnt, fn, gfn in ((4, L._mlir_ciface_llmcp_q8_rmsnorm_linear_group4_bf16,
+                              L._mlir_ciface_llmcp_q8_linear_group4_bf16),
+                             (3, L._mlir_ciface_llmcp_q8_rmsnorm_linear_group3_bf16,
+                              L._mlir_ciface_llmcp_q8_linear_group3_bf16)):
+            names = ["none", "silu", "none", "softplus"][:cnt]
+            nd1, nd2 = ctx.alloc(h * 2), ctx.alloc(h * 2)
+            o1 = [ctx.alloc(n * 2) for n, _ in shapes[:cnt]]
+            o2 = [ctx.alloc(n * 2) for n, _ in shapes[:cnt]]
+            o3 = [ctx.alloc(n * 2) for n, _ in shapes[:cnt]]
+            ctx.rmsnorm_linear_group(xd, wd, nd1, ts[:cnt], o1, 1, zero_centered=True,
+                                     activations=names, dtype="bf16")
+            ws = [t.memref() for t in ts[:cnt]]
+            ys = [ref(o) for o in o2]
+            ndi = q8.f32_memref(nd2.ptr, 1, h)
+            assert fn(ctypes.byref(xi), ctypes.byref(wv), 1e-6, 1, ctypes.byref(ndi),
+                      *[ctypes.byref(d) for d in ws], *[ctypes.byref(d) for d in ys],
+                      *acts[:cnt], q8.MODE["decode"]) == q8.OK, q8.last_error()
+            assert np.array_equal(ctx.to_host(nd1, (1, h), np.uint16),
+                                  ctx.to_host(nd2, (1, h), np.uint16))
+            ys3 = [ref(o) for o in o3]
+            assert gfn(ctypes.byref(ndi), *[ctypes.byref(d) for d in ws],
+                       *[ctypes.byref(d) for d in ys3], *acts[:cnt],
+                       q8.MODE["decode"]) == q8.OK, q8.last_error()
+            for (n, _), a, b, c in zip(shapes[:cnt], o1, o2, o3):
+                ra = ctx.to_host(a, (1, n), np.uint16)
+                assert np.array_equal(ra, ctx.to_host(b, (1, n), np.uint16))
+                assert np.array_equal(ra, ctx.to_host(c, (1, n), np.uint16))
+    finally:
+        L.llmcp_q8_set_default_ctx(None)
+        for t in ts:
+            ctx.release(t)
