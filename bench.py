@@ -684,6 +684,9 @@ def main():
     ap.add_argument("--gemm-only", type=int, default=0, metavar="M",
                     help="time only config 4's prefill GEMM at M rows and print "
                          "its figures (a short run for counter collection)")
+    ap.add_argument("--norm-only", action="store_true",
+                    help="time only the RMSNorm neighbour (extra.rmsnorm) and print "
+                         "its figures (a short run for kernel traces)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every timed block directly instead of replaying a "
                          "captured graph (for kernel tracers; figures include launch cost)")
@@ -706,6 +709,9 @@ def main():
     if args.gemm_only:
         r = bench_gemm(ctx, args.gemm_only)
         print(json.dumps({"gemm_m%d_n9216_k2560" % args.gemm_only: r}), flush=True)
+        return
+    if args.norm_only:
+        print(json.dumps({"rmsnorm": bench_norms(ctx, q8)}), flush=True)
         return
     res = bench_decode_mlp(ctx, q8, args.steps, args.warmup)
     extra = {"platform": args.platform}
