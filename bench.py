@@ -743,7 +743,7 @@ def main():
     # timed with HIP events on its own, outside every timed step
     extra["repack_ms"] = repack
     cpu = None if args.no_cpu or c1 is None else cpu_baseline(res, c1, c3, seq)
-    fv = 16 if args.platform == "aarch64" else 0
+    fv = 80 if args.platform == "aarch64" else 64
     line = {
         "metric": "Q8_0 linear: M=1 GEMV HBM GB/s (% peak); M=1024 GEMM int8 TOPS (% peak)",
         "value": round(res["gb_s"], 1),
@@ -768,9 +768,10 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": (load_traffic() or {}).get("hbm_bytes_per_launch"),
-                     "kernel": "gemv_kernel<2,false,1,4,4,5,%d> (fused gate/up SwiGLU, "
-                               "4-wave workgroups, input row quantized per workgroup; "
-                               "timed alone via llmcp_q8_swiglu, %d launches)"
+                     "kernel": "gemv_kernel<false,1,4,4,5,%d> (SwiGLU: gate and up "
+                               "streamed by the two waves of a pair, 4-wave workgroups, "
+                               "input row quantized per workgroup; timed alone via "
+                               "llmcp_q8_swiglu, %d launches)"
                                % (fv, res["steps"]),
                      "launch_us": round(res["gu_launch_us"], 3),
                      "algorithmic_bytes": res["gu_bytes"],

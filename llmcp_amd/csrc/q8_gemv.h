@@ -315,7 +315,7 @@ __device__ __forceinline__ void argmax_fold(unsigned long long *slots,
 // lane), so wider workgroups share that work.  Four for every shape: at
 // K = 9216 two and eight were 30 % and 13 % slower, at K = 2560 two was 3 %
 // slower (one matrix) and three 1 % slower (gate/up).
-__host__ __device__ constexpr int wg_waves(int /*nmat*/, int /*pc*/) { return 4; }
+__host__ __device__ constexpr int wg_waves(int /*pc*/) { return 4; }
 __host__ __device__ constexpr int row_rounds(int pc, int w) {
   return (2 * pc + w - 1) / w;
 }
@@ -337,11 +337,11 @@ __host__ __device__ constexpr int row_slots(int pc, int w) {
 // them in block order; the next pass's prepare() is scheduled together with
 // the current chain(), so the dots overlap the serial DPP additions.
 // V packs the compile-time variant: bit 0 the input row is bf16 (IN_WG),
-// bit 1 the output is bf16, bit 2 a one-matrix GEMV applies a.act, bit 3 a
-// one-matrix GEMV adds the residual row a.r to its (rounded) result, bit 4
-// the fma epilogue, bit 5 a grouped GEMV (GemvGroupArgs: each wave takes its
-// weight, output and activation from the group table).
-template <int NMAT, bool ARGMAX, int IN, int W, int D, int PC, int V>
+// bit 1 the output is bf16, bit 2 the GEMV applies a.act, bit 3 it adds the
+// residual row a.r to its (rounded) result, bit 4 the fma epilogue, bit 5 a
+// grouped GEMV (GemvGroupArgs: each wave takes its weight, output and
+// activation from the group table), bit 6 the SwiGLU (gate a.w0, up a.w1).
+template <bool ARGMAX, int IN, int W, int D, int PC, int V>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(
     std::conditional_t<(V & 32) != 0, GemvGroupArgs, GemvArgs> a) {
   constexpr bool XB = (V & 1) != 0;
@@ -353,15 +353,24 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
   // (Q8Scalar.cpp:192-199).
   constexpr bool FMA = (V & 16) != 0;
   constexpr bool GROUP = (V & 32) != 0;
-  static_assert(!ADD || (NMAT == 1 && !ARGMAX && !ACTV), "residual add variants");
-  static_assert(!GROUP || (NMAT == 1 && !ARGMAX && !ADD && IN == IN_WG), "grouped variants");
+  // bit 6: SwiGLU by wave pairs.  The even wave of a pair streams the gate
+  // matrix, the odd one up, for the same lane group (one wave streaming
+  // both measured 7 % slower on the gate/up GEMV); the up wave hands its
+  // sums to the gate wave through LDS.
+  constexpr bool PAIR = (V & 64) != 0;
+  static_assert(!PAIR || (!ARGMAX && !ACTV && !ADD && !GROUP && IN == IN_WG && (W % 2) == 0),
+                "SwiGLU variants");
+  static_assert(!ADD || (!ARGMAX && !ACTV), "residual add variants");
+  static_assert(!GROUP || (!ARGMAX && !ADD && IN == IN_WG), "grouped variants");
   extern __shared__ __align__(16) unsigned char lds[];  // IN_WG input row
   __shared__ unsigned long long key_l[W];
+  __shared__ float pair_l[PAIR ? W / 2 : 1][kLanes];
   const int passes = PC > 0 ? PC : a.passes;
   const int nblk = passes * kPassBlocks;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t g = (int64_t)blockIdx.x * W + wave;
+  const int64_t g = PAIR ? (int64_t)blockIdx.x * (W / 2) + (wave >> 1)
+                         : (int64_t)blockIdx.x * W + wave;
   const bool active = g < a.groups;
   const int j = lane & 15;
   const int r = lane >> 4;
@@ -416,24 +425,19 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
     lg = gl - a.gstart[widx];
     w0 = a.wt[widx];
   } else {
-    w0 = a.w0;
+    w0 = (PAIR && (wave & 1)) ? a.w1 : a.w0;
   }
-  const unsigned char *base[NMAT];
-  base[0] = w0 + lg * passes * kPassBytes;
-  if (NMAT == 2) base[NMAT - 1] = a.w1 + gl * passes * kPassBytes;
+  const unsigned char *base = w0 + lg * passes * kPassBytes;
 
-  uint4 q0[NMAT][D], q1[NMAT][D], x0[D], x1[D];
-  uint32_t sc[NMAT][D];
+  uint4 q0[D], q1[D], x0[D], x1[D];
+  uint32_t sc[D];
   float xs[D];
   auto issue = [&](int slot, int p) {
     const int pc = p < passes ? p : passes - 1;
-#pragma unroll
-    for (int mm = 0; mm < NMAT; ++mm) {
-      const unsigned char *pb = base[mm] + (int64_t)pc * kPassBytes;
-      q0[mm][slot] = load_stream16(pb + lane * 16);
-      q1[mm][slot] = load_stream16(pb + 1024 + lane * 16);
-      sc[mm][slot] = *(const uint16_t *)(pb + kPassQs + lane * 2);
-    }
+    const unsigned char *pb = base + (int64_t)pc * kPassBytes;
+    q0[slot] = load_stream16(pb + lane * 16);
+    q1[slot] = load_stream16(pb + 1024 + lane * 16);
+    sc[slot] = *(const uint16_t *)(pb + kPassQs + lane * 2);
     // Raw loads only: any use of the loaded values here (even a select)
     // would make the wave wait for them and drain the ring.  Padded blocks
     // (blk >= blocks) are masked in prepare().
@@ -515,9 +519,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
     __syncthreads();
   }
 
-  float acc[NMAT];
-#pragma unroll
-  for (int mm = 0; mm < NMAT; ++mm) acc[mm] = 0.0f;
+  float acc = 0.0f;
 
   // Contributions of unit u (ring slot d): exact block dots (two
   // independent dot4 chains; integer sums are order-free), then
@@ -528,7 +530,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
   struct Next {
     uint4 a0, a1;
     float s_a;
-    int d0[NMAT], d1[NMAT];
+    int d0, d1;
   };
   auto load_act = [&](int d, int u, Next &n) {
     const int blk = block_of(u);
@@ -541,34 +543,25 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
       n.a1 = *(const uint4 *)(qa_l + blk * kBlock + 16);
       n.s_a = sa_l[blk];
     }
-#pragma unroll
-    for (int mm = 0; mm < NMAT; ++mm) n.d0[mm] = n.d1[mm] = 0;
+    n.d0 = n.d1 = 0;
   };
   auto dot_part = [&](int d, int k, Next &n) {
-#pragma unroll
-    for (int mm = 0; mm < NMAT; ++mm) {
-      n.d0[mm] = __builtin_amdgcn_sdot4((int)word(q0[mm][d], k),
-                                        (int)word(n.a0, k), n.d0[mm], false);
-      n.d1[mm] = __builtin_amdgcn_sdot4((int)word(q1[mm][d], k),
-                                        (int)word(n.a1, k), n.d1[mm], false);
-    }
+    n.d0 = __builtin_amdgcn_sdot4((int)word(q0[d], k), (int)word(n.a0, k), n.d0, false);
+    n.d1 = __builtin_amdgcn_sdot4((int)word(q1[d], k), (int)word(n.a1, k), n.d1, false);
   };
-  auto finish = [&](int d, Next &n, float (&c)[NMAT], float (&cf)[NMAT]) {
-#pragma unroll
-    for (int mm = 0; mm < NMAT; ++mm) {
-      const int dot = n.d0[mm] + n.d1[mm];
-      const float factor = n.s_a * half_bits_to_float(sc[mm][d]);
-      if constexpr (FMA) {
-        c[mm] = (float)dot;
-        cf[mm] = factor;
-      } else {
-        c[mm] = (float)dot * factor;
-        cf[mm] = 0.0f;
-      }
+  auto finish = [&](int d, Next &n, float &c, float &cf) {
+    const int dot = n.d0 + n.d1;
+    const float factor = n.s_a * half_bits_to_float(sc[d]);
+    if constexpr (FMA) {
+      c = (float)dot;
+      cf = factor;
+    } else {
+      c = (float)dot * factor;
+      cf = 0.0f;
     }
   };
   // All S units of pass p.
-  auto prepare = [&](int p, float (&c)[S][NMAT], float (&cf)[S][NMAT]) {
+  auto prepare = [&](int p, float (&c)[S], float (&cf)[S]) {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int u = p * S + i;
@@ -610,9 +603,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
   // pinned between chain additions (whose dependent latency they hide) by
   // sched_barrier.  The dots wait for the next pass's weights inside this
   // chain, which costs nothing once the ring has landed.
-  auto chain_with = [&](const float (&c)[S][NMAT], const float (&cf)[S][NMAT],
-                        bool has_next, int pn, float (&cn)[S][NMAT],
-                        float (&cfn)[S][NMAT]) {
+  auto chain_with = [&](const float (&c)[S], const float (&cf)[S], bool has_next,
+                        int pn, float (&cn)[S], float (&cfn)[S]) {
     Next n[S];
     if (has_next) {
 #pragma unroll
@@ -621,11 +613,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
 #pragma unroll
     for (int t = 0; t < kPassBlocks; ++t) {
 #pragma unroll
-      for (int i = 0; i < S; ++i) {
-#pragma unroll
-        for (int mm = 0; mm < NMAT; ++mm)
-          acc[mm] = step(acc[mm], c[i][mm], cf[i][mm], t, i == 0);
-      }
+      for (int i = 0; i < S; ++i) acc = step(acc, c[i], cf[i], t, i == 0);
       if (has_next) {
 #pragma unroll
         for (int o = 0; o < 5 * S; ++o) {
@@ -643,7 +631,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
   };
 
   if (active) {
-    float cur[S][NMAT], nxt[S][NMAT], curf[S][NMAT], nxtf[S][NMAT];
+    float cur[S], nxt[S], curf[S], nxtf[S];
     prepare(0, cur, curf);
     if constexpr (PC > 0) {
       constexpr int NP = PC / S;
@@ -658,12 +646,10 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
         __builtin_amdgcn_sched_barrier(0);
         chain_with(cur, curf, p + 1 < NP, p + 1, nxt, nxtf);
 #pragma unroll
-        for (int i = 0; i < S; ++i)
-#pragma unroll
-          for (int mm = 0; mm < NMAT; ++mm) {
-            cur[i][mm] = nxt[i][mm];
-            curf[i][mm] = nxtf[i][mm];
-          }
+        for (int i = 0; i < S; ++i) {
+          cur[i] = nxt[i];
+          curf[i] = nxtf[i];
+        }
       }
     } else {
       for (int p0 = 0; p0 < passes; p0 += D) {
@@ -674,11 +660,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
             issue(d, p + D);
             __builtin_amdgcn_sched_barrier(0);
             chain_with(cur, curf, p + 1 < passes, p + 1, nxt, nxtf);
-#pragma unroll
-            for (int mm = 0; mm < NMAT; ++mm) {
-              cur[0][mm] = nxt[0][mm];
-              curf[0][mm] = nxtf[0][mm];
-            }
+            cur[0] = nxt[0];
+            curf[0] = nxtf[0];
           }
         }
       }
@@ -690,19 +673,23 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
   // up; with a bf16 result each linear's output is rounded to bf16 before
   // the bf16 multiply (FuseSiluMul: linear{silu} + mul on bf16 tensors).
   float y;
-  if (NMAT == 2) {
-    const float gs = silu_f32(acc[0]);
-    y = YB ? bf16_to_float(float_to_bf16(gs)) *
-                       bf16_to_float(float_to_bf16(acc[NMAT - 1]))
-                 : gs * acc[NMAT - 1];
+  if constexpr (PAIR) {
+    // every wave reaches the barrier, active or not
+    if (active && (wave & 1) && j == kOwnerSlot) pair_l[wave >> 1][r] = acc;
+    __syncthreads();
+    const float up = pair_l[wave >> 1][r];
+    const float gs = silu_f32(acc);
+    y = YB ? bf16_to_float(float_to_bf16(gs)) * bf16_to_float(float_to_bf16(up))
+           : gs * up;
   } else {
     int act = a.act;
     if constexpr (GROUP) act = a.actt[widx];
-    y = ACTV ? activate(acc[0], act) : acc[0];
+    y = ACTV ? activate(acc, act) : acc;
   }
   void *yout = a.y;
   if constexpr (GROUP) yout = a.yt[widx];
-  const bool owner = active && j == kOwnerSlot;  // the lane holding the sum
+  // the lane holding the sum (PAIR: of the gate wave)
+  const bool owner = active && j == kOwnerSlot && !(PAIR && (wave & 1));
   if (owner) {
     // residual add (AddOpLowering, LowerToLinalg.cpp:359-375): the linear's
     // result as stored, plus r, in f32; bf16 rounds once more
@@ -746,56 +733,56 @@ inline unsigned grid_for(int64_t threads, int block) {
   return (unsigned)((threads + block - 1) / block);
 }
 
-// Ring depth: passes in flight per wave.  Two matrices: 4 (72 VGPRs; at
-// K = 2560 the fifth pass is issued as the first one is consumed, which
-// measured about 1 % faster on the decode MLP than all 5 at once).  One
-// matrix from LDS: 4 up to K = 2560 (the 2560 x 2560 GEMV: 3.71 us against
-// 3.86 with all 5), else 13 (117 VGPRs; at K = 9216 the down GEMV measured
-// 7.46 us against 8.05 with all 18 passes in flight, 7.74 with 12 and
-// 7.65-7.82 with 14-16).  One matrix with a pre-quantized row: 12 passes of
-// weights + input.
-template <int NMAT, int IN, int PC>
+// Ring depth: passes in flight per wave.  From LDS: 4 up to K = 2560 (the
+// 2560 x 2560 GEMV: 3.71 us against 3.86 with all 5; the SwiGLU's gate/up
+// waves measured the same with 2, 3 or 5), else 13 (117 VGPRs; at K = 9216
+// the down GEMV measured 7.46 us against 8.05 with all 18 passes in flight,
+// 7.74 with 12 and 7.65-7.82 with 14-16).  With a pre-quantized row: 12
+// passes of weights + input.
+template <int IN, int PC>
 constexpr int ring_depth() {
   // at least two passes of units, so the next pass is in flight while the
   // current one chains
   constexpr int two = 2 * seg_for(PC);
-  constexpr int base = NMAT == 2 ? 4 : (IN == IN_WG ? (PC <= 5 ? 4 : 13) : 12);
+  constexpr int base = IN == IN_WG ? (PC <= 5 ? 4 : 13) : 12;
   constexpr int dmax = base > two ? base : two;
-  return PC > 0 ? (PC < dmax ? PC : dmax) : (NMAT == 2 ? 4 : 8);
+  return PC > 0 ? (PC < dmax ? PC : dmax) : 8;
 }
 
-template <int NMAT, bool ARGMAX, int IN, int W, int PC, int V, class A>
+template <bool ARGMAX, int IN, int W, int PC, int V, class A>
 hipError_t launch_gemv_p(const A &args, hipStream_t s) {
-  constexpr int D = ring_depth<NMAT, IN, PC>();
-  const unsigned grid = (unsigned)((args.groups + W - 1) / W);
+  constexpr int D = ring_depth<IN, PC>();
+  constexpr int GW = (V & 64) != 0 ? W / 2 : W;  // lane groups per workgroup
+  const unsigned grid = (unsigned)((args.groups + GW - 1) / GW);
   const size_t slots = PC > 0 ? row_slots(PC, W) : (size_t)args.passes * kPassBlocks;
   const size_t lds = IN == IN_WG ? slots * (kBlock + 4) : 0;
-  hipLaunchKernelGGL((gemv_kernel<NMAT, ARGMAX, IN, W, D, PC, V>),
+  hipLaunchKernelGGL((gemv_kernel<ARGMAX, IN, W, D, PC, V>),
                      dim3(grid), dim3(64 * W), lds, s, args);
   return hipGetLastError();
 }
 
-// IN_WG takes its workgroup width from wg_waves; IN_PRE (wide outputs)
-// runs four waves per workgroup.
-template <int NMAT, bool ARGMAX, int IN, int PC, int V, class A>
+// IN_WG takes its workgroup width from wg_waves (the SwiGLU: two lane groups
+// per four-wave workgroup; six and eight waves measured 10 % and 9 % slower,
+// two 2 % slower); IN_PRE (wide outputs) runs four waves per workgroup.
+template <bool ARGMAX, int IN, int PC, int V, class A>
 hipError_t launch_gemv_w(const A &args, hipStream_t s) {
-  constexpr int W = IN == IN_WG ? wg_waves(NMAT, PC) : 4;
-  return launch_gemv_p<NMAT, ARGMAX, IN, W, PC, V>(args, s);
+  constexpr int W = IN == IN_WG ? wg_waves(PC) : 4;
+  return launch_gemv_p<ARGMAX, IN, W, PC, V>(args, s);
 }
 
 // Pass counts with a fully unrolled kernel: K = 512, 1024, 1536, 2560
 // (hidden size), 4096 and 9216 (the MLP down projection).  Others take the
 // runtime loop.
-template <int NMAT, bool ARGMAX, int IN, int V, class A = GemvArgs>
+template <bool ARGMAX, int IN, int V, class A = GemvArgs>
 hipError_t launch_gemv_t(const A &args, hipStream_t s) {
   switch (args.passes) {
-    case 1: return launch_gemv_w<NMAT, ARGMAX, IN, 1, V>(args, s);
-    case 2: return launch_gemv_w<NMAT, ARGMAX, IN, 2, V>(args, s);
-    case 3: return launch_gemv_w<NMAT, ARGMAX, IN, 3, V>(args, s);
-    case 5: return launch_gemv_w<NMAT, ARGMAX, IN, 5, V>(args, s);
-    case 8: return launch_gemv_w<NMAT, ARGMAX, IN, 8, V>(args, s);
-    case 18: return launch_gemv_w<NMAT, ARGMAX, IN, 18, V>(args, s);
-    default: return launch_gemv_w<NMAT, ARGMAX, IN, 0, V>(args, s);
+    case 1: return launch_gemv_w<ARGMAX, IN, 1, V>(args, s);
+    case 2: return launch_gemv_w<ARGMAX, IN, 2, V>(args, s);
+    case 3: return launch_gemv_w<ARGMAX, IN, 3, V>(args, s);
+    case 5: return launch_gemv_w<ARGMAX, IN, 5, V>(args, s);
+    case 8: return launch_gemv_w<ARGMAX, IN, 8, V>(args, s);
+    case 18: return launch_gemv_w<ARGMAX, IN, 18, V>(args, s);
+    default: return launch_gemv_w<ARGMAX, IN, 0, V>(args, s);
   }
 }
 
@@ -814,33 +801,36 @@ hipError_t launch_gemv_in(const GemvArgs &a, const GemvLaunch &l,
   const int v = xb | yb | av | ad;
   constexpr int F = FMA ? 16 : 0;
   if (l.nmat == 2) {
-    if (v == 0) return launch_gemv_t<2, false, IN, (0) | F>(a, s);
-    if (v == (IN == IN_WG ? 3 : 2)) return launch_gemv_t<2, false, IN, (IN == IN_WG ? 3 : 2) | F>(a, s);
+    // the SwiGLU quantizes its row in-workgroup (gemv_quantizes_input)
+    if constexpr (IN == IN_WG) {
+      if (v == 0) return launch_gemv_t<false, IN, (64) | F>(a, s);
+      if (v == 3) return launch_gemv_t<false, IN, (3 | 64) | F>(a, s);
+    }
     return hipErrorInvalidValue;
   }
   if (l.keys) {
-    if (v == 0) return launch_gemv_t<1, true, IN, (0) | F>(a, s);
-    if (IN == IN_WG && v == 1) return launch_gemv_t<1, true, IN, (1) | F>(a, s);
+    if (v == 0) return launch_gemv_t<true, IN, (0) | F>(a, s);
+    if (IN == IN_WG && v == 1) return launch_gemv_t<true, IN, (1) | F>(a, s);
     return hipErrorInvalidValue;
   }
   if (IN == IN_WG) {
     switch (v) {
-      case 0: return launch_gemv_t<1, false, IN, (0) | F>(a, s);
-      case 3: return launch_gemv_t<1, false, IN, (3) | F>(a, s);
-      case 4: return launch_gemv_t<1, false, IN, (4) | F>(a, s);
-      case 7: return launch_gemv_t<1, false, IN, (7) | F>(a, s);
-      case 8: return launch_gemv_t<1, false, IN, (8) | F>(a, s);
-      case 11: return launch_gemv_t<1, false, IN, (11) | F>(a, s);
+      case 0: return launch_gemv_t<false, IN, (0) | F>(a, s);
+      case 3: return launch_gemv_t<false, IN, (3) | F>(a, s);
+      case 4: return launch_gemv_t<false, IN, (4) | F>(a, s);
+      case 7: return launch_gemv_t<false, IN, (7) | F>(a, s);
+      case 8: return launch_gemv_t<false, IN, (8) | F>(a, s);
+      case 11: return launch_gemv_t<false, IN, (11) | F>(a, s);
       default: return hipErrorInvalidValue;
     }
   }
   switch (v) {
-    case 0: return launch_gemv_t<1, false, IN, (0) | F>(a, s);
-    case 2: return launch_gemv_t<1, false, IN, (2) | F>(a, s);
-    case 4: return launch_gemv_t<1, false, IN, (4) | F>(a, s);
-    case 6: return launch_gemv_t<1, false, IN, (6) | F>(a, s);
-    case 8: return launch_gemv_t<1, false, IN, (8) | F>(a, s);
-    case 10: return launch_gemv_t<1, false, IN, (10) | F>(a, s);
+    case 0: return launch_gemv_t<false, IN, (0) | F>(a, s);
+    case 2: return launch_gemv_t<false, IN, (2) | F>(a, s);
+    case 4: return launch_gemv_t<false, IN, (4) | F>(a, s);
+    case 6: return launch_gemv_t<false, IN, (6) | F>(a, s);
+    case 8: return launch_gemv_t<false, IN, (8) | F>(a, s);
+    case 10: return launch_gemv_t<false, IN, (10) | F>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -855,10 +845,10 @@ hipError_t launch_gemv_group(const GemvGroupArgs &a, const GemvLaunch &l,
   const int v = (l.x_bf16 ? 1 : 0) | (l.y_bf16 ? 2 : 0) | (any_act ? 4 : 0);
   constexpr int F = (FMA ? 16 : 0) | 32;
   switch (v) {
-    case 0: return launch_gemv_t<1, false, IN_WG, 0 | F>(a, s);
-    case 3: return launch_gemv_t<1, false, IN_WG, 3 | F>(a, s);
-    case 4: return launch_gemv_t<1, false, IN_WG, 4 | F>(a, s);
-    case 7: return launch_gemv_t<1, false, IN_WG, 7 | F>(a, s);
+    case 0: return launch_gemv_t<false, IN_WG, 0 | F>(a, s);
+    case 3: return launch_gemv_t<false, IN_WG, 3 | F>(a, s);
+    case 4: return launch_gemv_t<false, IN_WG, 4 | F>(a, s);
+    case 7: return launch_gemv_t<false, IN_WG, 7 | F>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
