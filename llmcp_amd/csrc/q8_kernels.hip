@@ -973,66 +973,82 @@ __global__ __launch_bounds__(1024) void argmax_reduce_kernel(
 
 // ---------------------------------------------------------- embedding -- //
 
-// One thread per (token, 16 columns), a flat grid over tokens x chunks so
+// One thread per (token, V columns), a flat grid over tokens x chunks so
 // that every lane has work -- LowerToLinalg.cpp:435-531 gathered from the
-// pass layout.  out = f32(q) * f32(d), exact.
+// unit layout.  out = f32(q) * f32(d), exact.  V = 4 for f32 rows (one 4 B
+// word of quants) and 8 for bf16 rows (two words), so that every lane
+// stores 16 B and a wave's stores form one contiguous run; the rows are
+// written once, so the stores are non-temporal.  (One thread per 16
+// columns, 64 B of plain stores per lane, took 6.4 us for 1024 ids of the
+// 248320 x 2560 table against 3.8 us for this form.)
+template <bool BF16>
 __global__ void embedding_kernel(const int64_t *__restrict__ tokens,
                                  int64_t count, const uint8_t *__restrict__ t,
                                  int64_t rows, int64_t passes, int64_t chunks,
-                                 void *__restrict__ out, int out_bf16,
-                                 int64_t ldo, int32_t *err, int aligned) {
+                                 void *__restrict__ out, int64_t ldo,
+                                 int32_t *err, int aligned) {
+  constexpr int V = BF16 ? 8 : 4;
   const int64_t th = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t ti = th / chunks;
-  const int64_t c16 = th - ti * chunks;
+  const int64_t c = th - ti * chunks;
   if (ti >= count) return;
   const int64_t tok = tokens[ti];
-  float v[16];
+  float v[V];
   if (tok < 0 || tok >= rows) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) v[e] = 0.0f;
-    if (c16 == 0) atomicOr(err, 1);
+    for (int e = 0; e < V; ++e) v[e] = 0.0f;
+    if (c == 0) atomicOr(err, 1);
   } else {
     const int64_t g = tok >> 2;
     const int r = (int)(tok & 3);
-    const int64_t b = c16 >> 1;
-    const int h = (int)(c16 & 1);
+    const int64_t col = c * V;
+    const int64_t b = col >> 5;             // block
+    const int h = (int)((col >> 4) & 1);    // its 16-value half
+    const int off = (int)(col & 15);        // first value within the half
     int64_t u;
     int j;
     locate_seg(b, seg_for(passes), u, j);
     const uint8_t *pass = t + (g * passes + u) * kPassBytes;
-    const uint4 q = *(const uint4 *)(pass + h * 1024 + r * 256 + j * 16);
+    const uint8_t *qp = pass + h * 1024 + r * 256 + j * 16 + off;
+    uint32_t w[V / 4];
+    if constexpr (BF16) {
+      const uint2 q = *(const uint2 *)qp;
+      w[0] = q.x;
+      w[1] = q.y;
+    } else {
+      w[0] = *(const uint32_t *)qp;
+    }
     const float d = half_bits_to_float(
         *(const uint16_t *)(pass + kPassQs + 2 * (16 * r + j)));
-    const uint32_t words[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-      v[e] = (float)(int8_t)(words[e >> 2] >> (8 * (e & 3))) * d;
+    for (int e = 0; e < V; ++e)
+      v[e] = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * d;
   }
-  if (out_bf16) {
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  if constexpr (BF16) {
     // truncf to a bf16 result (LowerToLinalg.cpp:435-531)
-    uint16_t *o = (uint16_t *)out + ti * ldo + c16 * 16;
-    uint32_t p[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      p[e] = (uint32_t)float_to_bf16(v[2 * e]) |
-             ((uint32_t)float_to_bf16(v[2 * e + 1]) << 16);
+    uint16_t *o = (uint16_t *)out + ti * ldo + c * V;
     if (aligned) {
-      *(uint4 *)o = make_uint4(p[0], p[1], p[2], p[3]);
-      *(uint4 *)(o + 8) = make_uint4(p[4], p[5], p[6], p[7]);
+      v4u p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        p[e] = (uint32_t)float_to_bf16(v[2 * e]) |
+               ((uint32_t)float_to_bf16(v[2 * e + 1]) << 16);
+      __builtin_nontemporal_store(p, (v4u *)o);
     } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[e] = float_to_bf16(v[e]);
+      for (int e = 0; e < V; ++e) o[e] = float_to_bf16(v[e]);
     }
-    return;
-  }
-  float *o = (float *)out + ti * ldo + c16 * 16;
-  if (aligned) {
-#pragma unroll
-    for (int e = 0; e < 16; e += 4)
-      *(float4 *)(o + e) = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
   } else {
+    float *o = (float *)out + ti * ldo + c * V;
+    if (aligned) {
+      const v4u p = {__float_as_uint(v[0]), __float_as_uint(v[1]),
+                     __float_as_uint(v[2]), __float_as_uint(v[3])};
+      __builtin_nontemporal_store(p, (v4u *)o);
+    } else {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) o[e] = v[e];
+      for (int e = 0; e < V; ++e) o[e] = v[e];
+    }
   }
 }
 
@@ -1300,15 +1316,19 @@ hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             void *out, bool out_bf16, int64_t ldo,
                             int32_t *err_flag, hipStream_t s) {
   if (count == 0) return hipSuccess;
-  const int64_t chunks = cols / 16;
+  const int64_t chunks = cols / (out_bf16 ? 8 : 4);
   const int aligned = out_bf16
       ? ((uintptr_t)out % 16 == 0) && (ldo % 8 == 0)
       : ((uintptr_t)out % 16 == 0) && (ldo % 4 == 0);
-  hipLaunchKernelGGL(embedding_kernel,
-                     dim3(grid_for(chunks * count, 256)), dim3(256),
-                     0, s, tokens, count, table, rows, passes_for(cols),
-                     chunks, out, out_bf16 ? 1 : 0, ldo, err_flag,
-                     aligned ? 1 : 0);
+  const dim3 grid(grid_for(chunks * count, 256));
+  if (out_bf16)
+    hipLaunchKernelGGL((embedding_kernel<true>), grid, dim3(256), 0, s, tokens,
+                       count, table, rows, passes_for(cols), chunks, out, ldo,
+                       err_flag, aligned ? 1 : 0);
+  else
+    hipLaunchKernelGGL((embedding_kernel<false>), grid, dim3(256), 0, s, tokens,
+                       count, table, rows, passes_for(cols), chunks, out, ldo,
+                       err_flag, aligned ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -1497,11 +1497,11 @@ static int embedding_impl(llmcp_q8_ctx *ctx, const llmcp_memref_i64_1d *tokens,
     return fail(LLMCP_Q8_DECLINED, "tokens must be contiguous");
   if (out.cols != w->cols || out.rows != tokens->sizes[0])
     return fail(LLMCP_Q8_DECLINED, "embedding output must be [tokens, hidden]");
-  // one thread per (token, 16 columns) on a one-dimensional grid of
-  // 256-thread workgroups; HIP bounds the grid's work-items (workgroups x
-  // 256) by 2^32 - 1
+  // one thread per (token, 4 columns) for f32 rows (8 for bf16) on a
+  // one-dimensional grid of 256-thread workgroups; HIP bounds the grid's
+  // work-items (workgroups x 256) by 2^32 - 1
   if (tokens->sizes[0] > (1ll << 40) ||
-      (tokens->sizes[0] * (w->cols / 16) + 255) / 256 * 256 > 0xFFFFFFFFll)
+      (tokens->sizes[0] * (w->cols / (out.bf16 ? 8 : 4)) + 255) / 256 * 256 > 0xFFFFFFFFll)
     return fail(LLMCP_Q8_DECLINED, "too many tokens for one launch (%lld)",
                 (long long)tokens->sizes[0]);
   if ((rc = set_device(ctx))) return rc;
