@@ -211,13 +211,15 @@ def bench_lm_head(ctx, v=248320, k=2560, iters=20):
     ms = run_graph(ctx, timer, g, iters)
     us = ms * 1e3 / iters
     nbytes = per + k * 4 + v * 4
-    # eight gathers of 1024 ids per graph (own ids and outputs), so that a
-    # graph launch's fixed cost is shared as in a real step
-    reps = 8
+    # 32 gathers of 1024 ids per graph, cycling through eight id sets and
+    # outputs, so that a graph launch's fixed cost is shared as in a real
+    # step
+    reps, sets = 32, 8
     rng = np.random.default_rng(1024)
-    tds = [ctx.to_device(rng.integers(0, v, 1024).astype(np.int64)) for _ in range(reps)]
-    ods = [ctx.alloc(1024 * k * 4) for _ in range(reps)]
-    g2 = graph_of(ctx, lambda: [ctx.embedding(tds[i], 1024, w, ods[i]) for i in range(reps)])
+    tds = [ctx.to_device(rng.integers(0, v, 1024).astype(np.int64)) for _ in range(sets)]
+    ods = [ctx.alloc(1024 * k * 4) for _ in range(sets)]
+    g2 = graph_of(ctx, lambda: [ctx.embedding(tds[i % sets], 1024, w, ods[i % sets])
+                                for i in range(reps)])
     run_graph(ctx, timer, g2, 2)
     ms2 = run_graph(ctx, timer, g2, iters)
     us2 = ms2 * 1e3 / (iters * reps)
@@ -252,8 +254,12 @@ def bench_gemm(ctx, m, n=9216, k=2560, iters=30):
         for w, _ in ws:
             ctx.linear(xd, w, yd, m, mode="prefill")
 
+    # as many quantizer launches per graph as the GEMM's smallest rotation
+    # would need, so that the graph launch's own cost is shared
+    nq = max(16, copies)
+
     def qrot():
-        for _ in ws:
+        for _ in range(nq):
             ctx.quantize(xd, m, k, qd, sd)
 
     timer = Timer(ctx)
@@ -262,7 +268,7 @@ def bench_gemm(ctx, m, n=9216, k=2560, iters=30):
     run_graph(ctx, timer, g, 1)
     us = run_graph(ctx, timer, g, rounds) * 1e3 / (rounds * copies)
     run_graph(ctx, timer, gq, 1)
-    q_us = run_graph(ctx, timer, gq, rounds) * 1e3 / (rounds * copies)
+    q_us = run_graph(ctx, timer, gq, rounds) * 1e3 / (rounds * nq)
     for w, p4d in ws:
         ctx.release(w)
         p4d.free()

@@ -221,16 +221,20 @@ __global__ void selftest_exp_kernel(uint32_t lo, uint32_t hi,
   }
 }
 
-// Grid: x covers (row, padded block) in units of 8 blocks per wave.
+// Grid: x covers (row, padded block) in units of 8 blocks per wave.  The
+// grid's threads are below 2^32 (the launch checks), so the index math is
+// 32-bit (a 64-bit division per thread took the M = 1024, K = 2560
+// quantizer from 3.3 to 4.6 us).
 __global__ void quantize_kernel(const void *__restrict__ x, int x_bf16,
                                 int64_t m, int64_t ldx, int64_t blocks,
                                 int8_t *qa, int64_t ldq, float *sa,
                                 int64_t lds, int64_t blocks_pad, int aligned) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t blk_all = t >> 3;  // global (row, block) index
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t blk_all = t >> 3;  // global (row, block) index
   const int lane = threadIdx.x & 63;
-  const int64_t row = blk_all / blocks_pad;
-  const int64_t blk = blk_all - row * blocks_pad;
+  const uint32_t row_i = blk_all / (uint32_t)blocks_pad;
+  const int64_t row = (int64_t)row_i;
+  const int64_t blk = (int64_t)(blk_all - row_i * (uint32_t)blocks_pad);
   const bool in_range = row < m;
   const bool valid = in_range && blk < blocks;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1138,9 +1142,11 @@ hipError_t launch_quantize(const void *x, bool x_bf16, int64_t m, int64_t ldx,
   const int64_t esz = x_bf16 ? 2 : 4;
   const int aligned =
       ((uintptr_t)x % (4 * esz) == 0) && (ldx % 4 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(threads, 256)), dim3(256),
-                     0, s, x, x_bf16 ? 1 : 0, m, ldx, blocks, qa, ldq, sa, lds,
-                     blocks_pad, aligned);
+  const dim3 grid(grid_for(threads, 256));
+  // HIP bounds a grid's work-items by 2^32 - 1
+  if ((int64_t)grid.x * 256 > 0xFFFFFFFFll) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(quantize_kernel, grid, dim3(256), 0, s, x, x_bf16 ? 1 : 0,
+                     m, ldx, blocks, qa, ldq, sa, lds, blocks_pad, aligned);
   return hipGetLastError();
 }
 
