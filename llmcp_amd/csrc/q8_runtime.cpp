@@ -1862,6 +1862,10 @@ int llmcp_q8_quantize_activations(llmcp_q8_ctx *ctx,
     if (rc) return rc;
     const int64_t m = input->sizes[0], k = input->sizes[1];
     if (m == 0) return LLMCP_Q8_OK;
+    // one thread per 4 values on a one-dimensional grid: HIP bounds its
+    // work-items by 2^32 - 1
+    if (m > (1ll << 40) || m * (k / 4) > 0xFFFFFF00ll)
+      return fail(LLMCP_Q8_DECLINED, "too many rows for one launch (%lld)", (long long)m);
     hipError_t e = launch_quantize(input->data + input->offset, false, m,
                                    input->strides[0], k, qa_dev, k, sa_dev,
                                    k / kBlock, k / kBlock, ctx->stream);
@@ -1882,6 +1886,8 @@ int llmcp_q8_block_dots(llmcp_q8_ctx *ctx, const llmcp_memref_f32_2d *input,
     if ((rc = set_device(ctx))) return rc;
     const int64_t m = input->sizes[0], k = input->sizes[1], b = k / kBlock;
     if (m == 0) return LLMCP_Q8_OK;
+    if (m > (1ll << 40) || m * (k / 4) > 0xFFFFFF00ll)
+      return fail(LLMCP_Q8_DECLINED, "too many rows for one launch (%lld)", (long long)m);
     if ((rc = ensure_scratch(ctx, (uint64_t)(m * k), (uint64_t)(m * b * 4))))
       return rc;
     hipError_t e = launch_quantize(input->data + input->offset, false, m,

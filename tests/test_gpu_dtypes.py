@@ -223,3 +223,45 @@ def test_matmul_benchmark_all_ones_fixture(ctx, oracle, m, k):
                         epilogue=ctx.epilogue)
     assert bits_equal(y, to_bf16(oracle, ref))
     ctx.release(t)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_embedding_strided_output(ctx, oracle, dtype):
+    # rows that start off 16 B boundaries (output offset by one element,
+    # row stride k + 3) take the per-element stores; the padding between
+    # rows is left alone
+    import ctypes
+    import llmcp_amd as q8
+    rng = np.random.default_rng(370 + len(dtype))
+    v, k, n = 256, 2560, 37
+    w = weights(rng, v, k)
+    p4 = oracle.pack_q8_0_p4(w)
+    t = ctx.upload_p4(p4, v, k)
+    tokens = rng.integers(0, v, n).astype(np.int64)
+    td = ctx.to_device(tokens)
+    el = np.float32 if dtype == "f32" else np.uint16
+    ld = k + 3
+    sentinel = np.full(n * ld + 1, 0x7FC5 if dtype == "bf16" else np.nan, el)
+    if dtype == "f32":
+        sentinel = sentinel.view(np.uint32)
+        sentinel[:] = 0x7FC00005
+        sentinel = sentinel.view(np.float32)
+    bd = ctx.to_device(sentinel)
+    esz = np.dtype(el).itemsize
+    o = q8.f32_memref(bd.ptr + esz, n, k, row_stride=ld)
+    ti = q8.i64_memref(td.ptr, n)
+    q8.check(ctx._entry("llmcp_q8_embedding", dtype)(
+        ctx.handle, ctypes.byref(ti), ctypes.byref(t.memref()), ctypes.byref(o)))
+    got = ctx.to_host(bd, (n * ld + 1,), el)
+    ref = oracle.embedding(tokens, p4, k)
+    if dtype == "bf16":
+        ref = to_bf16(oracle, ref)
+    rows = np.stack([got[1 + i * ld: 1 + i * ld + k] for i in range(n)])
+    assert bits_equal(rows, ref)
+    keep = np.ones(n * ld + 1, bool)
+    for i in range(n):
+        keep[1 + i * ld: 1 + i * ld + k] = False
+    assert np.array_equal(got[keep].view(np.uint16 if dtype == "bf16" else np.uint32),
+                          sentinel[keep].view(np.uint16 if dtype == "bf16" else np.uint32))
+    assert ctx.check_flag() == 0
+    ctx.release(t)
