@@ -310,12 +310,13 @@ __device__ __forceinline__ void argmax_fold(unsigned long long *slots,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Waves per workgroup of an IN_WG GEMV.  The workgroup quantizes the input
-// row once (pc * 16 blocks, 8 lanes per block, row_rounds float4 loads per
-// lane), so wider workgroups share that work.  Four for every shape: at
-// K = 9216 two and eight were 30 % and 13 % slower, at K = 2560 two was 3 %
-// slower (one matrix) and three 1 % slower (gate/up).
-__host__ __device__ constexpr int wg_waves(int /*pc*/) { return 4; }
+// Waves per workgroup of a one-matrix IN_WG GEMV.  The workgroup quantizes
+// the input row once (pc * 16 blocks, 8 lanes per block, row_rounds float4
+// loads per lane), so wider workgroups share that work.  Three at K = 9216
+// (the down GEMV: 6.94 us against 7.13 with four, 8.8 with six; two and
+// eight were 30 % and 13 % slower than four), four elsewhere (at K = 2560
+// three measured 3.51 us against 3.42 and two 3 % slower).
+__host__ __device__ constexpr int wg_waves(int pc) { return pc == 18 ? 3 : 4; }
 __host__ __device__ constexpr int row_rounds(int pc, int w) {
   return (2 * pc + w - 1) / w;
 }
@@ -761,12 +762,13 @@ hipError_t launch_gemv_p(const A &args, hipStream_t s) {
   return hipGetLastError();
 }
 
-// IN_WG takes its workgroup width from wg_waves (the SwiGLU: two lane groups
-// per four-wave workgroup; six and eight waves measured 10 % and 9 % slower,
-// two 2 % slower); IN_PRE (wide outputs) runs four waves per workgroup.
+// One-matrix IN_WG GEMVs take their workgroup width from wg_waves; the
+// SwiGLU runs two lane groups per four-wave workgroup (six and eight waves
+// measured 10 % and 9 % slower, two 2 % slower); IN_PRE (wide outputs) runs
+// four waves per workgroup.
 template <bool ARGMAX, int IN, int PC, int V, class A>
 hipError_t launch_gemv_w(const A &args, hipStream_t s) {
-  constexpr int W = IN == IN_WG ? wg_waves(PC) : 4;
+  constexpr int W = IN == IN_WG ? ((V & 64) != 0 ? 4 : wg_waves(PC)) : 4;
   return launch_gemv_p<ARGMAX, IN, W, PC, V>(args, s);
 }
 
