@@ -407,7 +407,11 @@ int llmcp_q8_lm_head_bf16(llmcp_q8_ctx *ctx, const llmcp_memref_bf16_2d *hidden,
  * LLMCP_Q8_STATIC_SCRATCH_BYTES that each GPU holds until the process ends,
  * set up when the first context on that GPU is created; a hidden state that
  * needs more returns LLMCP_Q8_DECLINED.  Every call on one GPU shares that
- * array: calls that overlap on one GPU (two contexts, two streams) race. */
+ * array, so one context per GPU may use it: the first context to call this
+ * entry on a GPU owns the array until it is destroyed, and calls from any
+ * other context on that GPU return LLMCP_Q8_DECLINED.  The owner's calls
+ * are ordered on its stream (also across llmcp_q8_ctx_set_stream); calls
+ * that overlap in other ways race. */
 int llmcp_q8_lm_head_noalloc(llmcp_q8_ctx *ctx,
                              const llmcp_memref_f32_2d *hidden,
                              const llmcp_memref_i8_1d *table,
@@ -628,15 +632,6 @@ int llmcp_q8_graph_launch(llmcp_q8_ctx *ctx, void *graph_exec);
 int llmcp_q8_graph_destroy(void *graph_exec);
 /* Bytes the device copy of a registered weight occupies (0 if unknown). */
 uint64_t llmcp_q8_device_bytes(llmcp_q8_ctx *ctx, const void *key);
-
-/* ------------------------------------------------------------ testing -- */
-/* No counterpart in the reference.  For tests of the RMSNorm entries: rows
- * of up to 12288 values have their serial sum of squares evaluated
- * speculatively from predicted partial sums, with exact fallbacks; this
- * offsets the predictions by `bits` f32 steps (process-wide, 0 = off) so
- * that the fallbacks decide the results.  Results do not change.  Not for
- * use while RMSNorm calls are in flight. */
-int llmcp_q8_test_rmsnorm_skew(int32_t bits);
 
 #ifdef __cplusplus
 }

@@ -84,7 +84,7 @@ EXPORTS = [
     "_mlir_ciface_llmcp_q8_linear_group3", "_mlir_ciface_llmcp_q8_linear_group4",
     "llmcp_q8_rmsnorm", "llmcp_q8_rmsnorm_bf16", "llmcp_q8_rmsnorm_linear_group",
     "llmcp_q8_rmsnorm_linear_group_bf16", "llmcp_q8_gated_rmsnorm",
-    "llmcp_q8_gated_rmsnorm_bf16", "llmcp_q8_test_rmsnorm_skew",
+    "llmcp_q8_gated_rmsnorm_bf16",
     "_mlir_ciface_llmcp_q8_linear_group3_bf16", "_mlir_ciface_llmcp_q8_linear_group4_bf16",
     "_mlir_ciface_llmcp_q8_rmsnorm", "_mlir_ciface_llmcp_q8_rmsnorm_bf16",
     "_mlir_ciface_llmcp_q8_gated_rmsnorm", "_mlir_ciface_llmcp_q8_gated_rmsnorm_bf16",
@@ -107,7 +107,7 @@ def lib():
     F = ctypes.POINTER(ctypes.c_float)
     sig = {
         "llmcp_q8_abi_version": (I32, []),
-        "llmcp_q8_test_rmsnorm_skew": (I, [I32]),
+        "llmcp_q8_test_ctx_rmsnorm_skew": (I, [P, I32]),
         "llmcp_q8_last_error": (ctypes.c_char_p, []),
         "llmcp_q8_ctx_create": (I, [I, ctypes.POINTER(P)]),
         "llmcp_q8_ctx_destroy": (I, [P]),

@@ -123,7 +123,7 @@ hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);
 // Q8_1 activations in the GEMM's tiled layout: the 32 rows x 32 values of
 // row tile t and block b are 1 KiB at (t * blocks_pad + b) * 1024 (row r at
 // r * 32), their scales 32 floats at (t * blocks_pad + b) * 32.  Rows past m
-// in the last tile are left unwritten (their results are never stored).
+// in the last tile and blocks past the row's are written as zeros.
 hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
                                  int64_t ldx, int64_t cols, int8_t *qa,
                                  float *sa, int64_t blocks_pad, hipStream_t s);
@@ -133,17 +133,15 @@ hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
 // x and y share their type (f32 or bf16); w is f32 or bf16.  qmode 1 also
 // writes y's Q8_1 in the dense layout (row r at r * blocks_pad * 32, scales
 // at r * blocks_pad), qmode 2 in the tiled layout of launch_quantize_tiled.
+// spec_skew (tests only; 0 otherwise) offsets the predicted partial sums of
+// rows of up to 12288 values, whose serial sum is evaluated speculatively,
+// by that many f32 steps, so that the exact fallbacks decide the results;
+// the results are the same either way.
 hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
                           int64_t h, const void *w, bool w_bf16, float eps,
                           bool zero_centered, void *y, bool y_bf16, int64_t ldy,
                           int8_t *qa, float *sa, int64_t blocks_pad, int qmode,
-                          hipStream_t s);
-
-// Tests only: offsets launch_rmsnorm's predicted partial sums (rows of up to
-// 12288 values, where the sum is evaluated speculatively) by `bits` f32
-// steps, so that the kernel's fallbacks decide the results; 0 restores it.
-// Results are the same either way.  Not synchronised with launches.
-void set_rmsnorm_spec_skew(int bits);
+                          hipStream_t s, int spec_skew = 0);
 
 // Gated RMSNorm of `groups` dense groups of g values (g % 32 == 0): x, gate
 // and y share their type (f32 or bf16), w [g] is f32.

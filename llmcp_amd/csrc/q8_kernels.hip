@@ -309,8 +309,11 @@ __global__ __launch_bounds__(256) void quantize_tiles_kernel(
 // buffer meanwhile.  Then all waves write y and, with QMODE, its Q8_1 (the
 // quantizer's arithmetic, quantize_block8, on the values as stored): QMODE
 // 1 the dense [m][blocks_pad * 32] layout, QMODE 2 the GEMM's tiled layout
-// (blocks past H written as zeros; rows past m in the last tile are left
-// unwritten, as by launch_quantize_tiled: their results are never stored).
+// (blocks past H written as zeros).  Rows past m in the last tile are left
+// unwritten, unlike launch_quantize_tiled, which zeroes them: they hold
+// whatever the workspace held before.  That is harmless only because every
+// consumer of the tiled layout stores results of rows below m alone (the
+// GEMM's epilogue checks m < m_rows), which never read those rows.
 // Requires h % 32 == 0.
 //
 // GATED: llmcp.gated_rms_norm, whose groups of h values are the rows here
@@ -1244,17 +1247,11 @@ hipError_t launch_argmax_reduce(unsigned long long *slots, int64_t *out,
   return hipGetLastError();
 }
 
-// Offset (in f32 bits) added to rmsnorm_spec_kernel's pass-B predictions:
-// 0 except in tests, which move the predictions away to run the fallbacks.
-static int g_spec_skew = 0;
-
-void set_rmsnorm_spec_skew(int bits) { g_spec_skew = bits; }
-
 hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
                           int64_t h, const void *w, bool w_bf16, float eps,
                           bool zero_centered, void *y, bool y_bf16, int64_t ldy,
                           int8_t *qa, float *sa, int64_t blocks_pad, int qmode,
-                          hipStream_t s) {
+                          hipStream_t s, int spec_skew) {
   if (h % kBlock != 0 || m <= 0 || (qmode != 0 && blocks_pad * kBlock < h))
     return hipErrorInvalidValue;
   if ((uintptr_t)w % (w_bf16 ? 8 : 16) != 0) return hipErrorInvalidValue;
@@ -1271,7 +1268,7 @@ hipError_t launch_rmsnorm(const void *x, bool x_bf16, int64_t m, int64_t ldx,
     if (spec)                                                                              \
       hipLaunchKernelGGL((rmsnorm_spec_kernel<XB, WB, YB, Q>), grid, dim3(kSpecThreads), lds, \
                          s, x, ldx, w, eps, zc, hh, y, ldy, qa, sa, bp, aligned | (yal << 1), \
-                         g_spec_skew);                                                     \
+                         spec_skew);                                                       \
     else                                                                                   \
       hipLaunchKernelGGL((rmsnorm_kernel<XB, WB, YB, Q, false>), grid, dim3(256), 0, s, x,  \
                          ldx, w, eps, zc, m, hh, y, ldy, qa, sa, bp, aligned, nullptr, 0, 0); \

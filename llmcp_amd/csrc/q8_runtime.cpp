@@ -114,6 +114,9 @@ struct llmcp_q8_ctx {
   uint64_t generation = 0;
   // Orders work across llmcp_q8_ctx_set_stream.
   hipEvent_t switch_event = nullptr;
+  // Tests only (llmcp_q8_test_ctx_rmsnorm_skew): offset of this context's
+  // speculative RMSNorm predictions, in f32 steps; 0 otherwise.
+  int32_t rmsnorm_skew = 0;
   bool fma() const { return platform == LLMCP_Q8_PLATFORM_AARCH64; }
 };
 
@@ -278,6 +281,11 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void *g_scratch_ptr[kMaxDevices];
 bool g_scratch_dirty[kMaxDevices];  // the slots may hold a failed call's keys
+// The one context per device whose calls may use the fixed scratch (the
+// first to call the no-allocation entry there, until it is destroyed):
+// two contexts run on different streams, and their calls would race on
+// the shared array unordered.
+llmcp_q8_ctx *g_scratch_owner[kMaxDevices];
 
 }  // namespace
 
@@ -526,11 +534,6 @@ extern "C" {
 
 int32_t llmcp_q8_abi_version(void) { return LLMCP_Q8_ABI_VERSION; }
 
-int llmcp_q8_test_rmsnorm_skew(int32_t bits) {
-  set_rmsnorm_spec_skew(bits);
-  return LLMCP_Q8_OK;
-}
-
 const char *llmcp_q8_last_error(void) { return g_last_error; }
 
 int llmcp_q8_ctx_create(int device, llmcp_q8_ctx **out) {
@@ -602,6 +605,11 @@ int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx) {
     if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     if (g_default_ctx == ctx) g_default_ctx = nullptr;
+    if (ctx->device >= 0 && ctx->device < kMaxDevices) {
+      // its calls have finished (the streams were synchronized above)
+      std::lock_guard<std::mutex> lock(g_scratch_mutex);
+      if (g_scratch_owner[ctx->device] == ctx) g_scratch_owner[ctx->device] = nullptr;
+    }
     delete ctx;
     return LLMCP_Q8_OK;
   });
@@ -653,6 +661,19 @@ int llmcp_q8_set_platform(llmcp_q8_ctx *ctx, int32_t platform) {
 
 int32_t llmcp_q8_get_platform(llmcp_q8_ctx *ctx) {
   return ctx ? ctx->platform : -1;
+}
+
+// Test hook, declared in no header of the product (the tests bind it
+// directly; no counterpart in the reference): rows of up to 12288 values
+// have their serial sum of squares evaluated speculatively from predicted
+// partial sums with exact fallbacks, and this moves the predictions of this
+// context's RMSNorm calls by `bits` f32 steps (0 = off) so that the
+// fallbacks decide the results.  Results do not change.  The setting is
+// per context: no other context's calls see it.
+int llmcp_q8_test_ctx_rmsnorm_skew(llmcp_q8_ctx *ctx, int32_t bits) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  ctx->rmsnorm_skew = bits;
+  return LLMCP_Q8_OK;
 }
 
 int llmcp_q8_set_weight_budget(llmcp_q8_ctx *ctx, uint64_t bytes) {
@@ -1258,7 +1279,7 @@ static int rmsnorm_impl(llmcp_q8_ctx *ctx, const Rows &in, const NormWeight &nw,
   if ((rc = set_device(ctx))) return rc;
   hipError_t e = launch_rmsnorm(in.data, in.bf16, in.rows, in.ld, in.cols, nw.data,
                                 nw.bf16, eps, zero_centered != 0, out.data, out.bf16,
-                                out.ld, nullptr, nullptr, 0, 0, ctx->stream);
+                                out.ld, nullptr, nullptr, 0, 0, ctx->stream, ctx->rmsnorm_skew);
   if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
   return LLMCP_Q8_OK;
 }
@@ -1316,7 +1337,8 @@ static int rmsnorm_group_impl(llmcp_q8_ctx *ctx, const Rows &in, const NormWeigh
   if (m == 1) {
     hipError_t e = launch_rmsnorm(in.data, in.bf16, 1, in.ld, in.cols, nw.data, nw.bf16,
                                   eps, zero_centered != 0, normed.data, normed.bf16,
-                                  normed.ld, nullptr, nullptr, 0, 0, ctx->stream);
+                                  normed.ld, nullptr, nullptr, 0, 0, ctx->stream,
+                                  ctx->rmsnorm_skew);
     if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
     return linear_group_run(ctx, normed, count, w, outs, acts, false);
   }
@@ -1328,7 +1350,7 @@ static int rmsnorm_group_impl(llmcp_q8_ctx *ctx, const Rows &in, const NormWeigh
     return rc;
   hipError_t e = launch_rmsnorm(in.data, in.bf16, m, in.ld, in.cols, nw.data, nw.bf16, eps,
                                 zero_centered != 0, normed.data, normed.bf16, normed.ld,
-                                ws.qa, ws.sa, nblk, 2, ctx->stream);
+                                ws.qa, ws.sa, nblk, 2, ctx->stream, ctx->rmsnorm_skew);
   if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
   return linear_group_run(ctx, normed, count, w, outs, acts, true);
 }
@@ -1788,6 +1810,16 @@ int llmcp_q8_lm_head_noalloc(llmcp_q8_ctx *ctx,
       return fail(LLMCP_Q8_DECLINED, kDenseMsg);
     if (ctx->device >= kMaxDevices || !g_scratch_ptr[ctx->device])
       return fail(LLMCP_Q8_EINVAL, "no fixed scratch on device %d", ctx->device);
+    {
+      std::lock_guard<std::mutex> lock(g_scratch_mutex);
+      llmcp_q8_ctx *&owner = g_scratch_owner[ctx->device];
+      if (!owner) owner = ctx;
+      if (owner != ctx)
+        return fail(LLMCP_Q8_DECLINED,
+                    "the fixed scratch of device %d is in use by another context "
+                    "(one context per GPU may call the no-allocation entry)",
+                    ctx->device);
+    }
     const Workspace ws = static_workspace(ctx->device);
     return lm_head_impl(ctx, in, table, out, argmax_dev, execution_mode, &ws);
   });

@@ -118,7 +118,8 @@ def test_rmsnorm_fallbacks(ctx, oracle, q8, skew, dtype, m, h):
     """Rows of width <= 12288 run the speculative sum: lanes fold each
     sixteenth of the row from 32 candidate starts around a predicted partial
     sum, and the segments are chained through the candidates whose start is
-    the true one.  llmcp_q8_test_rmsnorm_skew moves the predictions by
+    the true one.  llmcp_q8_test_ctx_rmsnorm_skew moves the context's
+    predictions by
     `skew` f32 steps, so that the true start is found among the first
     pass's candidates instead (f32 rows, whose prediction drift is small) or
     nowhere and the segment is folded again; the results are unchanged."""
@@ -128,12 +129,12 @@ def test_rmsnorm_fallbacks(ctx, oracle, q8, skew, dtype, m, h):
     xd, wd = ctx.to_device(x), ctx.to_device(w)
     yd = ctx.alloc(x.nbytes)
     L = q8.lib()
-    assert L.llmcp_q8_test_rmsnorm_skew(skew) == 0
+    assert L.llmcp_q8_test_ctx_rmsnorm_skew(ctx.handle, skew) == 0
     try:
         ctx.rmsnorm(xd, wd, yd, m, h, eps=1e-6, zero_centered=True, dtype=dtype)
         got = ctx.to_host(yd, (m, h), et)
     finally:
-        L.llmcp_q8_test_rmsnorm_skew(0)
+        L.llmcp_q8_test_ctx_rmsnorm_skew(ctx.handle, 0)
     ref = oracle.rmsnorm(x, w, 1e-6, zero_centered=True, out_bf16=dtype == "bf16")
     assert np.array_equal(bits(got), bits(ref))
 
@@ -248,6 +249,49 @@ def test_rmsnorm_linear_group(ctx, oracle, shapes, acts, m, mode, dtype):
             ctx.linear(nd, t, sep, m, activation=acts[i], mode=mode, dtype=dtype)
             assert np.array_equal(bits(got), bits(ctx.to_host(sep, (m, n), et))), i
             rows = np.arange(m) if m <= 4 else np.array([0, m // 2, m - 1])
+            ref = oracle.linear(nf[rows], p4[i], n, activation=acts[i],
+                                epilogue=ctx.epilogue, colpar=True)
+            if dtype == "bf16":
+                ref = oracle.f32_to_bf16_bits(ref)
+            assert np.array_equal(bits(got[rows]), bits(ref)), i
+        assert ctx.check_flag() == 0
+    finally:
+        for t in ts:
+            ctx.release(t)
+
+
+@pytest.mark.parametrize("m,k,dtype", [(513, 2560, "f32"), (1024, 2560, "f32"),
+                                        (1025, 2560, "bf16"), (3, 12320, "f32"),
+                                        (2, 16384, "bf16")])
+def test_rmsnorm_linear_group_four_row_kernel(ctx, oracle, m, k, dtype):
+    """Shapes past the speculative kernel's limits (more than 512 f32 or 1024
+    bf16 rows, or rows wider than 12288) take the four-rows RMSNorm kernel,
+    whose epilogue writes the tiled Q8_1 that the GEMMs read (QMODE 2, the
+    config-4 prefill with its norm): the fused call must equal the norm
+    followed by the separate linears bit for bit, and the oracle on sampled
+    rows."""
+    shapes, acts = [(256, k), (64, k)], ["silu", "none"]
+    rng = np.random.default_rng(m + k)
+    x, w = rows_and_weight(rng, m, k, dtype, oracle, scale=2.0)
+    ws = [(rng.standard_normal(s) * 0.02).astype(np.float32) for s in shapes]
+    p4 = [oracle.pack_q8_0_p4(a) for a in ws]
+    ts = [ctx.upload_p4(p, *s) for p, s in zip(p4, shapes)]
+    try:
+        esz, et = (4, np.float32) if dtype == "f32" else (2, np.uint16)
+        xd, wd = ctx.to_device(x), ctx.to_device(w)
+        nd = ctx.alloc(m * k * esz)
+        outs = [ctx.alloc(m * n * esz) for n, _ in shapes]
+        ctx.rmsnorm_linear_group(xd, wd, nd, ts, outs, m, eps=1e-6, zero_centered=True,
+                                 activations=acts, mode="prefill", dtype=dtype)
+        normed = oracle.rmsnorm(x, w, 1e-6, zero_centered=True, out_bf16=dtype == "bf16")
+        assert np.array_equal(bits(ctx.to_host(nd, (m, k), et)), bits(normed))
+        nf = normed if dtype == "f32" else oracle.bf16_bits_to_f32(normed)
+        for i, ((n, _), t, o) in enumerate(zip(shapes, ts, outs)):
+            got = ctx.to_host(o, (m, n), et)
+            sep = ctx.alloc(m * n * esz)
+            ctx.linear(nd, t, sep, m, activation=acts[i], mode="prefill", dtype=dtype)
+            assert np.array_equal(bits(got), bits(ctx.to_host(sep, (m, n), et))), i
+            rows = np.array([0, m // 2, m - 1])
             ref = oracle.linear(nf[rows], p4[i], n, activation=acts[i],
                                 epilogue=ctx.epilogue, colpar=True)
             if dtype == "bf16":

@@ -104,3 +104,34 @@ def test_noalloc_declines_oversized_input(pctx, oracle, q8):
         assert "scratch" in q8.last_error()
     finally:
         ctx.release(t)
+
+
+def test_noalloc_one_context_per_gpu(oracle, q8):
+    """The fixed scratch belongs to the first context that calls the entry
+    on a GPU: another context's call is declined (their streams would race
+    on the array) until the owner is destroyed."""
+    rng = np.random.default_rng(80)
+    v, k = 256, 1024
+    p4 = oracle.pack_q8_0_p4((rng.standard_normal((v, k)) * 0.02).astype(np.float32))
+    a, b = q8.Context(0), q8.Context(0)
+    try:
+        ta, tb = a.upload_p4(p4, v, k), b.upload_p4(p4, v, k)
+        x = rng.standard_normal((1, k)).astype(np.float32)
+        xa, la, ma = a.to_device(x), a.alloc(v * 4), a.alloc(8)
+        xb, lb, mb = b.to_device(x), b.alloc(v * 4), b.alloc(8)
+        assert call_noalloc(q8, a, xa, 1, ta, la, ma, "decode") == q8.OK, q8.last_error()
+        assert call_noalloc(q8, b, xb, 1, tb, lb, mb, "decode") == q8.DECLINED
+        assert "another context" in q8.last_error()
+        want = a.to_host(la, (1, v), np.float32)
+        a.release(ta)
+        a.close()
+        a = None
+        assert call_noalloc(q8, b, xb, 1, tb, lb, mb, "decode") == q8.OK, q8.last_error()
+        got = b.to_host(lb, (1, v), np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert int(b.to_host(mb, (1,), np.int64)[0]) == oracle.argmax(want[0])
+        b.release(tb)
+    finally:
+        if a is not None:
+            a.close()
+        b.close()
