@@ -43,10 +43,10 @@ extern "C" {
  * activations; 3: linear + residual add; 4: reference platform switch,
  * weight budget, graph staleness check, grouped linears; 5: RMSNorm, gated
  * RMSNorm and RMSNorm + grouped linears; 6: their MLIR C-interface entries
- * and the bf16 group entries).  The model ABI of
+ * and the bf16 group entries; 7: the accumulation switch).  The model ABI of
  * the AOT library (llmcp_model_abi_version() == 2,
  * include/llmcp/Support/AotAbi.h:12) is not changed by this library. */
-#define LLMCP_Q8_ABI_VERSION 6
+#define LLMCP_Q8_ABI_VERSION 7
 
 enum llmcp_q8_status {
   LLMCP_Q8_OK = 0,
@@ -88,6 +88,30 @@ enum llmcp_q8_activation {
 enum llmcp_q8_platform {
   LLMCP_Q8_PLATFORM_X86 = 0,
   LLMCP_Q8_PLATFORM_AARCH64 = 1
+};
+
+/* How a context's multi-row linears sum their blocks.  No counterpart in
+ * the reference, whose emitters always run one serial chain per output.
+ * EXACT (default)  every f32 output is the selected platform's serial
+ *                  block-order sum, bit for bit.
+ * SPLIT_K          linears of several rows (the GEMM path: linear, linear +
+ *                  add, grouped linears, SwiGLU, MLP, RMSNorm + group) whose
+ *                  tiles leave over half the GPU idle (65 to 128 rows at the
+ *                  model's widths) split K into two ranges of whole
+ *                  512-value passes (a second kernel then adds the ranges'
+ *                  partial sums: worth it only there): each range is a serial
+ *                  chain of the platform's epilogue, and the ranges' f32
+ *                  partial sums are added in range order.  The per-block
+ *                  int32 dots are still exact; f32 outputs agree with the
+ *                  reference within 1e-5 relative or 1e-4 absolute (bf16
+ *                  outputs within one bf16 step); the same inputs give the
+ *                  same bits on every call.  One-row calls, the lm_head
+ *                  (logits and argmax) and shapes that fill the GPU run as
+ *                  in EXACT.  Needs workspace for the partial sums, grown on
+ *                  first use like the prefill scratch. */
+enum llmcp_q8_accumulation {
+  LLMCP_Q8_ACCUM_EXACT = 0,
+  LLMCP_Q8_ACCUM_SPLIT_K = 1
 };
 
 /* llmcp.execution_mode (LowerToLinalg.cpp:40-52). */
@@ -166,6 +190,11 @@ int llmcp_q8_ctx_synchronize(llmcp_q8_ctx *ctx);
  * on the context; llmcp_q8_get_platform returns it (-1 for a null ctx). */
 int llmcp_q8_set_platform(llmcp_q8_ctx *ctx, int32_t platform);
 int32_t llmcp_q8_get_platform(llmcp_q8_ctx *ctx);
+/* Selects the accumulation mode (llmcp_q8_accumulation) for every later
+ * call on the context; llmcp_q8_get_accumulation returns it (-1 for a null
+ * ctx).  No counterpart in the reference. */
+int llmcp_q8_set_accumulation(llmcp_q8_ctx *ctx, int32_t mode);
+int32_t llmcp_q8_get_accumulation(llmcp_q8_ctx *ctx);
 /* Caps the device bytes of the context's registered weights (0: no cap, the
  * default); a registration past the cap fails with LLMCP_Q8_ENOMEM.  Lets a
  * serving process keep HBM for other state. */

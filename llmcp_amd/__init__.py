@@ -23,6 +23,7 @@ MODE = {"prefill": 0, "decode": 1}
 # Reference platforms (llmcp_q8_platform) and the per-block epilogue each
 # computes: fma on aarch64 (SDOT emitters), mul+add on x86 (scalar path).
 PLATFORM = {"x86": 0, "aarch64": 1}
+ACCUM = {"exact": 0, "split_k": 1}
 EPILOGUE = {"x86": "scalar", "aarch64": "fma"}
 
 _lib = None
@@ -84,7 +85,7 @@ EXPORTS = [
     "_mlir_ciface_llmcp_q8_linear_group3", "_mlir_ciface_llmcp_q8_linear_group4",
     "llmcp_q8_rmsnorm", "llmcp_q8_rmsnorm_bf16", "llmcp_q8_rmsnorm_linear_group",
     "llmcp_q8_rmsnorm_linear_group_bf16", "llmcp_q8_gated_rmsnorm",
-    "llmcp_q8_gated_rmsnorm_bf16",
+    "llmcp_q8_gated_rmsnorm_bf16", "llmcp_q8_set_accumulation", "llmcp_q8_get_accumulation",
     "_mlir_ciface_llmcp_q8_linear_group3_bf16", "_mlir_ciface_llmcp_q8_linear_group4_bf16",
     "_mlir_ciface_llmcp_q8_rmsnorm", "_mlir_ciface_llmcp_q8_rmsnorm_bf16",
     "_mlir_ciface_llmcp_q8_gated_rmsnorm", "_mlir_ciface_llmcp_q8_gated_rmsnorm_bf16",
@@ -108,6 +109,9 @@ def lib():
     sig = {
         "llmcp_q8_abi_version": (I32, []),
         "llmcp_q8_test_ctx_rmsnorm_skew": (I, [P, I32]),
+        "llmcp_q8_test_ctx_gemm_splits": (I, [P, I32]),
+        "llmcp_q8_set_accumulation": (I, [P, I32]),
+        "llmcp_q8_get_accumulation": (I32, [P]),
         "llmcp_q8_last_error": (ctypes.c_char_p, []),
         "llmcp_q8_ctx_create": (I, [I, ctypes.POINTER(P)]),
         "llmcp_q8_ctx_destroy": (I, [P]),
@@ -304,6 +308,19 @@ class Context:
         """'aarch64' (SDOT emitters: fma epilogue, the default) or 'x86'
         (scalar path: mul+add) for every later call."""
         check(lib().llmcp_q8_set_platform(self.handle, PLATFORM[platform]))
+
+    def set_accumulation(self, mode, splits=0):
+        """'exact' (the serial block order, bit for bit: the default) or
+        'split_k' (multi-row GEMMs that underfill the GPU split K, within
+        the reference's tolerance) for every later call; `splits` > 0 forces
+        that many K splits (a test hook; 0 = chosen by shape)."""
+        check(lib().llmcp_q8_set_accumulation(self.handle, ACCUM[mode]))
+        check(lib().llmcp_q8_test_ctx_gemm_splits(self.handle, int(splits)))
+
+    @property
+    def accumulation(self):
+        code = lib().llmcp_q8_get_accumulation(self.handle)
+        return {v: k for k, v in ACCUM.items()}.get(code, code)
 
     def set_platform_code(self, code):
         """llmcp_q8_set_platform with a raw code (tests of the error path)."""

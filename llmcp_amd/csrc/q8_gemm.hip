@@ -166,7 +166,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
                  int32_t row_tiles, int32_t nblk, const uint8_t *__restrict__ w,
                  int64_t n_rows, int64_t m_rows, int32_t passes, int32_t m_tiles,
                  int32_t n_tiles, void *y, int64_t ldy, const void *mul,
-                 int64_t ldg) {
+                 int64_t ldg, int32_t splits, int64_t split_stride) {
   typedef GemmStage<WM, WN, SEG> St;
   static_assert(NST == 2 || NST == 4, "stage buffers");
   constexpr int W = WM * WN;
@@ -178,38 +178,47 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   };
 
   // XCD-aware tile order: ids with the same (id % 8) share an XCD; each XCD
-  // takes whole N-tiles (all their M-tiles), so a weight tile is fetched
-  // into that XCD's L2 once.  Workgroups are persistent: workgroup g takes
-  // ids g, g + G, g + 2G, ... (G = gridDim.x, a multiple of 8, so all on one
-  // XCD); ids of the padding N-tiles (n_tile >= n_tiles) are skipped.
-  const int total = (n_tiles + 7) / 8 * 8 * m_tiles;
+  // takes whole N-tiles (all their M-tiles and K splits), so a weight tile
+  // is fetched into that XCD's L2 once.  Workgroups are persistent:
+  // workgroup g takes ids g, g + G, g + 2G, ... (G = gridDim.x, a multiple
+  // of 8, so all on one XCD); ids of the padding N-tiles (n_tile >= n_tiles)
+  // are skipped.  With splits > 1 (never persistent) each id is one tile's
+  // K split: passes [sp * passes / splits, (sp + 1) * passes / splits), its
+  // partial sums stored at y + sp * split_stride.
+  const int total = (n_tiles + 7) / 8 * 8 * m_tiles * splits;
   const int G = gridDim.x;
-  auto tile_of = [&](int id, int &mt, int &nt) __attribute__((always_inline)) {
+  auto tile_of = [&](int id, int &mt, int &nt, int &sp) __attribute__((always_inline)) {
     const int kk = id >> 3;
-    nt = (kk / m_tiles) * 8 + (id & 7);
-    mt = kk % m_tiles;
+    const int per = m_tiles * splits;
+    nt = (kk / per) * 8 + (id & 7);
+    const int r = kk - (kk / per) * per;
+    sp = r / m_tiles;
+    mt = r - sp * m_tiles;
   };
   auto next_tile = [&](int id) __attribute__((always_inline)) {
     for (; id < total; id += G) {
-      int mt, nt;
-      tile_of(id, mt, nt);
+      int mt, nt, sp;
+      tile_of(id, mt, nt, sp);
       if (nt < n_tiles) break;
     }
     return id;
   };
   int id = next_tile(blockIdx.x);
   if (id >= total) return;  // uniform per workgroup
-  int m_tile, n_tile;
-  tile_of(id, m_tile, n_tile);
+  int m_tile, n_tile, split;
+  tile_of(id, m_tile, n_tile, split);
   int64_t m0 = (int64_t)m_tile * BM;
   int64_t n0 = (int64_t)n_tile * BN;
+  // this workgroup's stages (four per pass) and the first one's index
+  const int pass0 = split * passes / splits;
+  const int sbase = pass0 * (kPassBlocks / kStageBlocks);
+  const int stages = ((split + 1) * passes / splits - pass0) * (kPassBlocks / kStageBlocks);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   __builtin_assume(wave >= 0 && wave < W);
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane & 31, lh = lane >> 5;
-  const int stages = passes * (kPassBlocks / kStageBlocks);
   const int64_t wrow = (int64_t)passes * kPassBytes;  // bytes per lane group
 
   // This wave's DMA ops.  Per op: a per-lane byte offset that depends on the
@@ -331,7 +340,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   // buffer `buf`: branch-free, the same instruction sequence in every wave.
   auto issue_op = [&](int s, St &buf, auto J, const Offsets &of) __attribute__((always_inline)) {
     constexpr int j = decltype(J)::value;
-    const int kb = s * kStageBlocks;  // first block of the stage
+    const int kb = (sbase + s) * kStageBlocks;  // first block of the stage
     const StagePos sp = stage_pos(kb);
     int8_t *lds_base = (int8_t *)&buf;
     if constexpr (j < St::S16) {
@@ -469,7 +478,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   // (into bbuf).
   auto compute = [&](int s, St &buf, St &buf1, int sa, St &abuf, const Offsets &aof, int sb,
                      St &bbuf, const Offsets &bof) __attribute__((always_inline)) {
-    const int kb = s * kStageBlocks;
+    const int kb = (sbase + s) * kStageBlocks;
     static_for<kStageBlocks>([&](auto BB) __attribute__((always_inline)) {
       constexpr int bb = decltype(BB)::value;
       const v16i c_next = dots(fr);
@@ -540,16 +549,18 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   {
     const Frag f0 = read_frag(stage(0), 0);
     fr = read_frag(stage(0), 1);
-    const ScaleRaw r0 = read_scales(0, stage(0), 0);
+    const ScaleRaw r0 = read_scales(sbase * kStageBlocks, stage(0), 0);
     c_cur = dots(f0);
-    f_cur = scale_tile(0, r0, 0);
+    f_cur = scale_tile(sbase * kStageBlocks, r0, 0);
   }
 
   for (;;) {
     const int id_next = PERSIST ? next_tile(id + G) : total;
     const bool more = PERSIST && id_next < total;
-    int m_next = m_tile, n_next = n_tile;
-    if (more) tile_of(id_next, m_next, n_next);
+    // persistent launches have one split: the next tile's is 0 as well
+    int m_next = m_tile, n_next = n_tile, split_next = 0;
+    if (more) tile_of(id_next, m_next, n_next, split_next);
+    (void)split_next;
     Offsets nxt;
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
@@ -592,6 +603,8 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     }
 
     const int64_t n = n0 + 32 * wn + li;
+    // this split's part of the output (the whole output with one split)
+    char *const ys = (char *)y + (int64_t)split * split_stride * ((EPI & 4) != 0 ? 2 : 4);
     // the activation over all 16 values (rows or columns past the end too,
     // whose results are not stored): one straight-line sequence
     activate_array(acc, EPI & 3);
@@ -613,9 +626,9 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
         // non-temporal: the output is written once and not read back here
         // (op time -3 % at M = 256 and 1024)
         if constexpr ((EPI & 4) != 0)
-          __builtin_nontemporal_store(float_to_bf16(o), (uint16_t *)y + m * ldy + n);
+          __builtin_nontemporal_store(float_to_bf16(o), (uint16_t *)ys + m * ldy + n);
         else
-          __builtin_nontemporal_store(o, (float *)y + m * ldy + n);
+          __builtin_nontemporal_store(o, (float *)ys + m * ldy + n);
       }
     }
     if (!more) break;
@@ -630,7 +643,87 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   wait_vmcnt<0>();
 }
 
+// The K splits' reduction and the epilogue: y = epi(part[0] + part[1] + ...
+// + part[splits - 1]) in that order (a fixed order, so the same inputs give
+// the same bits), part [splits][m][n] f32 from gemm_kernel's split
+// launches; the epilogue is gemm_kernel's (activation, SwiGLU multiply,
+// residual add, bf16 store).  One thread per 4 consecutive outputs of a row
+// (n % 4 == 0).
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(
+    const float *__restrict__ part, int32_t splits, int64_t split_stride, int64_t m,
+    int64_t n, void *y, int64_t ldy, const void *mul, int64_t ldg) {
+  const int64_t nq = n >> 2;
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= m * nq) return;
+  const int64_t row = q / nq, c0 = (q - row * nq) * 4;
+  const float *p = part + row * n + c0;
+  float4 a = *(const float4 *)p;
+  for (int32_t i = 1; i < splits; ++i) {
+    const float4 t = *(const float4 *)(p + (int64_t)i * split_stride);
+    a.x = a.x + t.x;
+    a.y = a.y + t.y;
+    a.z = a.z + t.z;
+    a.w = a.w + t.w;
+  }
+  float v[4] = {a.x, a.y, a.z, a.w};
+  activate_array(v, EPI & 3);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t col = c0 + j;
+    float o = v[j];
+    if constexpr ((EPI & 8) != 0) {
+      const float g = ((const float *)mul)[row * ldg + col];
+      o = (EPI & 4) != 0 ? bf16_to_float(float_to_bf16(g)) * bf16_to_float(float_to_bf16(o))
+                         : g * o;
+    }
+    if constexpr ((EPI & 16) != 0) {
+      const float r = (EPI & 4) != 0 ? bf16_to_float(((const uint16_t *)mul)[row * ldg + col])
+                                     : ((const float *)mul)[row * ldg + col];
+      o = (EPI & 4) != 0 ? bf16_to_float(float_to_bf16(o)) + r : o + r;
+    }
+    if constexpr ((EPI & 4) != 0)
+      ((uint16_t *)y)[row * ldy + col] = float_to_bf16(o);
+    else
+      ((float *)y)[row * ldy + col] = o;
+  }
+}
+
 }  // namespace
+
+template <int EPI>
+static void launch_reduce_e(const GemmLaunch &l, hipStream_t s) {
+  const void *mp = (EPI & 16) != 0 ? l.add : (const void *)l.mul;
+  const int64_t ld = (EPI & 16) != 0 ? l.ldr : l.ldg;
+  const int64_t quads = l.m * (l.rows / 4);
+  hipLaunchKernelGGL((gemm_reduce_kernel<EPI>), dim3((unsigned)((quads + 255) / 256)), dim3(256),
+                     0, s, l.part, l.splits, l.m * l.rows, l.m, l.rows, l.y, l.ldy, mp, ld);
+}
+
+// The epilogue code of a launch: activation in bits 0-1, bf16 output in bit
+// 2, the SwiGLU multiply in bit 3, the residual add in bit 4.
+static int epi_of(const GemmLaunch &l) {
+  if (l.mul) return l.y_bf16 ? 12 : 8;   // the SwiGLU up linear: no activation
+  if (l.add) return l.y_bf16 ? 20 : 16;  // linear + residual add: no activation
+  return (l.activation & 3) | (l.y_bf16 ? 4 : 0);
+}
+
+static void launch_reduce(const GemmLaunch &l, hipStream_t s) {
+  switch (epi_of(l)) {
+    case 1: return launch_reduce_e<1>(l, s);
+    case 2: return launch_reduce_e<2>(l, s);
+    case 3: return launch_reduce_e<3>(l, s);
+    case 4: return launch_reduce_e<4>(l, s);
+    case 5: return launch_reduce_e<5>(l, s);
+    case 6: return launch_reduce_e<6>(l, s);
+    case 7: return launch_reduce_e<7>(l, s);
+    case 8: return launch_reduce_e<8>(l, s);
+    case 12: return launch_reduce_e<12>(l, s);
+    case 16: return launch_reduce_e<16>(l, s);
+    case 20: return launch_reduce_e<20>(l, s);
+    default: return launch_reduce_e<0>(l, s);
+  }
+}
 
 template <int WM, int WN, int NST, bool FMA, int SEG, int EPI>
 static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
@@ -639,20 +732,26 @@ static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
   // the resident workgroups, and only for the 12-wave shape and S = 1 or 4
   // (with S = 6 the next tile's offsets spill registers)
   constexpr bool kPersist = WM * WN >= 12 && SEG != 6;
-  const unsigned total = (unsigned)((n_tiles + 7) / 8 * 8 * m_tiles);
+  // K splits (never persistent) store f32 partial sums, [splits][m][rows]
+  // at l.part, for launch_reduce (EPI 0)
+  const int32_t splits = l.splits > 1 ? l.splits : 1;
+  const unsigned total = (unsigned)((n_tiles + 7) / 8 * 8 * m_tiles * splits);
+  void *const y = splits > 1 ? (void *)l.part : l.y;
+  const int64_t ldy = splits > 1 ? l.rows : l.ldy;
+  const int64_t stride = splits > 1 ? l.m * l.rows : 0;
   // the epilogue's second operand: the SwiGLU gate or the residual
   const void *mp = (EPI & 16) != 0 ? l.add : (const void *)l.mul;
   const int64_t ld = (EPI & 16) != 0 ? l.ldr : l.ldg;
-  if (kPersist && grid < total)
+  if (kPersist && splits == 1 && grid < total)
     hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, kPersist>), dim3(grid),
                        dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
-                       l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
-                       mp, ld);
+                       l.w, l.rows, l.m, passes, m_tiles, n_tiles, y, ldy,
+                       mp, ld, splits, stride);
   else
     hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, false>), dim3(total),
                        dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
-                       l.w, l.rows, l.m, passes, m_tiles, n_tiles, l.y, l.ldy,
-                       mp, ld);
+                       l.w, l.rows, l.m, passes, m_tiles, n_tiles, y, ldy,
+                       mp, ld, splits, stride);
 }
 
 template <int WM, int WN, int NST, bool FMA, int SEG>
@@ -660,19 +759,17 @@ static void launch_gemm_e(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
                           int32_t n_tiles, unsigned grid, hipStream_t s) {
   // activation and output type are template arguments: inlined for every
   // accumulator element, runtime switches bloat the kernel and slow it
+  // K splits: plain f32 partial sums, then the reduction applies the epilogue
+  if (l.splits > 1) {
+    launch_gemm_k<WM, WN, NST, FMA, SEG, 0>(l, passes, m_tiles, n_tiles, grid, s);
+    return launch_reduce(l, s);
+  }
 #define LLMCP_GEMM_EPI(E) \
   case E: return launch_gemm_k<WM, WN, NST, FMA, SEG, E>(l, passes, m_tiles, n_tiles, grid, s);
-  if (l.mul) {  // the SwiGLU up linear: no activation of its own
-    if (l.y_bf16) return launch_gemm_k<WM, WN, NST, FMA, SEG, 12>(l, passes, m_tiles, n_tiles, grid, s);
-    return launch_gemm_k<WM, WN, NST, FMA, SEG, 8>(l, passes, m_tiles, n_tiles, grid, s);
-  }
-  if (l.add) {  // linear + residual add: no activation
-    if (l.y_bf16) return launch_gemm_k<WM, WN, NST, FMA, SEG, 20>(l, passes, m_tiles, n_tiles, grid, s);
-    return launch_gemm_k<WM, WN, NST, FMA, SEG, 16>(l, passes, m_tiles, n_tiles, grid, s);
-  }
-  switch ((l.activation & 3) | (l.y_bf16 ? 4 : 0)) {
+  switch (epi_of(l)) {
     LLMCP_GEMM_EPI(1) LLMCP_GEMM_EPI(2) LLMCP_GEMM_EPI(3) LLMCP_GEMM_EPI(4)
-    LLMCP_GEMM_EPI(5) LLMCP_GEMM_EPI(6) LLMCP_GEMM_EPI(7)
+    LLMCP_GEMM_EPI(5) LLMCP_GEMM_EPI(6) LLMCP_GEMM_EPI(7) LLMCP_GEMM_EPI(8)
+    LLMCP_GEMM_EPI(12) LLMCP_GEMM_EPI(16) LLMCP_GEMM_EPI(20)
     default: return launch_gemm_k<WM, WN, NST, FMA, SEG, 0>(l, passes, m_tiles, n_tiles, grid, s);
   }
 #undef LLMCP_GEMM_EPI
@@ -713,17 +810,39 @@ static hipError_t launch_gemm_t(const GemmLaunch &l, hipStream_t s) {
   return hipGetLastError();
 }
 
+// 128 x 96 workgroups (12 waves, one per CU by LDS): at M = 1024, N = 9216
+// that is 768 workgroups, three full rounds on 256 CUs.  Up to 64 rows:
+// 64 x 64 workgroups (4 waves, two per CU).
+static bool small_shape(int64_t m) { return m <= 64; }
+
 template <bool FMA>
 static hipError_t launch_gemm_shape(const GemmLaunch &l, hipStream_t s) {
-  // 128 x 96 workgroups (12 waves, one per CU by LDS): at M = 1024, N = 9216
-  // that is 768 workgroups, three full rounds on 256 CUs.  Up to 64 rows:
-  // 64 x 64 workgroups (4 waves, two per CU).
-  if (l.m <= 64) return launch_gemm_t<2, 2, 4, FMA>(l, s);
+  if (small_shape(l.m)) return launch_gemm_t<2, 2, 4, FMA>(l, s);
   return launch_gemm_t<4, 3, 4, FMA>(l, s);
 }
 
 hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s) {
+  if (l.splits > 1) {
+    if (!l.part || l.splits > passes_for(l.cols) || l.rows % 4 != 0) return hipErrorInvalidValue;
+  }
   return l.fma ? launch_gemm_shape<true>(l, s) : launch_gemm_shape<false>(l, s);
+}
+
+int32_t gemm_splits_for(int64_t m, int64_t rows, int64_t cols, int32_t forced) {
+  const int32_t passes = (int32_t)passes_for(cols);
+  if (m <= 1 || passes <= 1) return 1;
+  if (forced > 0) return std::min(forced, passes);
+  // Two splits where the 12-wave shape leaves more than half the CUs idle
+  // (its tiles < CUs / 2); otherwise none.  Measured at N = 9216, K = 2560
+  // (op time: the quantizer, the GEMM and, split, the reduction): M = 128
+  // 32.4 -> 28.8 us with two splits; every split count was slower at
+  // M = 16 / 64 (18.5 / 18.9 us unsplit, 20.7-27.2 split), M = 256 (34.9
+  // against 49.8-58.6) and M = 512.  The 64-row shape's waves are bound by
+  // each CU's operand delivery, which splits share, and the reduction costs
+  // a launch.
+  if (small_shape(m)) return 1;
+  const int64_t tiles = ((m + 127) / 128) * ((rows + 95) / 96);
+  return 2 * tiles < (int64_t)cu_count() && passes >= 2 ? 2 : 1;
 }
 
 }  // namespace llmcp_q8

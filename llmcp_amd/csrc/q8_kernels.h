@@ -116,9 +116,24 @@ struct GemmLaunch {
   // result rounds acc to bf16 first and adds in f32.
   const void *add = nullptr;
   int64_t ldr = 0;
+  // K splits (1: none, the reference's serial block order bit for bit).
+  // splits > 1 (at most passes_for(cols); rows % 4 == 0): each output's
+  // blocks run as `splits` serial chains over contiguous ranges of whole
+  // passes, each from 0 in the platform's epilogue, stored as f32 partial
+  // sums in `part` ([splits][m][rows] floats), which a second kernel adds
+  // in split order before the epilogue.  Deterministic; not the reference's
+  // summation order, so f32 results agree with it within rounding only.
+  int32_t splits = 1;
+  float *part = nullptr;
 };
 
 hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);
+
+// K splits for a multi-row linear of [m x cols] by [rows x cols] when
+// splitting is allowed: `forced` > 0 (clamped to the pass count), else the
+// count measured fastest for the shape class (2 where the 12-wave tiles
+// leave over half the CUs idle, otherwise 1).
+int32_t gemm_splits_for(int64_t m, int64_t rows, int64_t cols, int32_t forced);
 
 // Q8_1 activations in the GEMM's tiled layout: the 32 rows x 32 values of
 // row tile t and block b are 1 KiB at (t * blocks_pad + b) * 1024 (row r at

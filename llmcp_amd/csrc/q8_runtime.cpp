@@ -105,6 +105,14 @@ struct llmcp_q8_ctx {
   // Reference platform whose arithmetic every path reproduces
   // (llmcp_q8_platform): aarch64 = fma epilogue everywhere, x86 = mul+add.
   int32_t platform = LLMCP_Q8_PLATFORM_AARCH64;
+  // llmcp_q8_accumulation of the multi-row linears; with SPLIT_K the K
+  // splits' f32 partial sums live in `part` (grown on demand).
+  int32_t accumulation = LLMCP_Q8_ACCUM_EXACT;
+  float *part = nullptr;
+  uint64_t part_bytes = 0;
+  // Tests only (llmcp_q8_test_ctx_gemm_splits): K splits forced on every
+  // splittable GEMM of this context in SPLIT_K mode; 0 = chosen by shape.
+  int32_t test_splits = 0;
   // Cap on device bytes of registered weights (0: none).
   uint64_t weight_budget = 0;
   uint64_t weight_bytes = 0;
@@ -597,6 +605,7 @@ int llmcp_q8_ctx_destroy(llmcp_q8_ctx *ctx) {
     if (ctx->keys) (void)hipFree(ctx->keys);
     if (ctx->hf) (void)hipFree(ctx->hf);
     if (ctx->up) (void)hipFree(ctx->up);
+    if (ctx->part) (void)hipFree(ctx->part);
     {
       std::lock_guard<std::mutex> lock(g_graph_mutex);
       for (auto it = g_graphs.begin(); it != g_graphs.end();)
@@ -657,6 +666,30 @@ int llmcp_q8_set_platform(llmcp_q8_ctx *ctx, int32_t platform) {
     ctx->platform = platform;
     return LLMCP_Q8_OK;
   });
+}
+
+int llmcp_q8_set_accumulation(llmcp_q8_ctx *ctx, int32_t mode) {
+  return guarded([&]() -> int {
+    if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+    if (mode != LLMCP_Q8_ACCUM_EXACT && mode != LLMCP_Q8_ACCUM_SPLIT_K)
+      return fail(LLMCP_Q8_EINVAL, "unknown accumulation mode %d", mode);
+    ctx->accumulation = mode;
+    return LLMCP_Q8_OK;
+  });
+}
+
+int32_t llmcp_q8_get_accumulation(llmcp_q8_ctx *ctx) {
+  return ctx ? ctx->accumulation : -1;
+}
+
+// Test hook, declared in no header of the product (no counterpart in the
+// reference): forces `splits` K splits (clamped to the pass count; 0 = the
+// shape's own choice) on this context's splittable GEMMs in SPLIT_K mode.
+int llmcp_q8_test_ctx_gemm_splits(llmcp_q8_ctx *ctx, int32_t splits) {
+  if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");
+  if (splits < 0) return fail(LLMCP_Q8_EINVAL, "negative split count %d", splits);
+  ctx->test_splits = splits;
+  return LLMCP_Q8_OK;
 }
 
 int32_t llmcp_q8_get_platform(llmcp_q8_ctx *ctx) {
@@ -1056,10 +1089,13 @@ static int gemm_quantize(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
 // decode and prefill emitters of one platform share it (fma on aarch64,
 // Q8Decode.cpp:200-203 and Q8Matmul.cpp:204-223; mul+add in the x86 scalar
 // path, Q8Scalar.cpp:192-199, which serves both modes).
+// In SPLIT_K mode (and unless `exact`, as for the lm_head) a GEMM whose
+// tiles leave the GPU underfilled splits K (gemm_splits_for) and sums the
+// splits' partial sums in a second kernel.
 static int gemm_launch(llmcp_q8_ctx *ctx, const Workspace &ws, int64_t m,
                        const Tensor *w, const Rows &out, int activation,
                        const float *mul, int64_t ldg,
-                       const Rows *residual = nullptr) {
+                       const Rows *residual = nullptr, bool exact = false) {
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   GemmLaunch g;
   g.qa = ws.qa;
@@ -1081,6 +1117,17 @@ static int gemm_launch(llmcp_q8_ctx *ctx, const Workspace &ws, int64_t m,
     g.add = residual->data;
     g.ldr = residual->ld;
   }
+  if (!exact && ctx->accumulation == LLMCP_Q8_ACCUM_SPLIT_K && !ws.fixed &&
+      w->rows % 4 == 0) {
+    const int32_t splits = gemm_splits_for(m, w->rows, w->cols, ctx->test_splits);
+    if (splits > 1) {
+      const uint64_t bytes = (uint64_t)splits * (uint64_t)m * (uint64_t)w->rows * 4u;
+      int rc = grow(ctx, ctx->part, ctx->part_bytes, bytes, "split-K partial sums");
+      if (rc) return rc;
+      g.splits = splits;
+      g.part = ctx->part;
+    }
+  }
   hipError_t e = launch_gemm(g, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "gemm launch");
   return LLMCP_Q8_OK;
@@ -1088,11 +1135,11 @@ static int gemm_launch(llmcp_q8_ctx *ctx, const Workspace &ws, int64_t m,
 
 static int gemm_common(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
                        const Rows &out, int activation,
-                       const Workspace *fixed = nullptr) {
+                       const Workspace *fixed = nullptr, bool exact = false) {
   Workspace ws = fixed ? *fixed : ctx_workspace(ctx);
   int rc = gemm_quantize(ctx, in, w, ws);
   if (rc) return rc;
-  return gemm_launch(ctx, ws, in.rows, w, out, activation, nullptr, 0);
+  return gemm_launch(ctx, ws, in.rows, w, out, activation, nullptr, 0, nullptr, exact);
 }
 
 static int check_linear_shapes(const Rows &in, const Tensor *w,
@@ -1410,8 +1457,9 @@ static int lm_head_impl(llmcp_q8_ctx *ctx, const Rows &in,
     return gemv_common(ctx, in, w, nullptr, logits, LLMCP_Q8_ACT_NONE,
                        argmax_dev, nullptr, fixed);
   // Several rows: the GEMM writes every row's logits, then the first
-  // maximum of the last row is reduced from HBM.
-  if ((rc = gemm_common(ctx, in, w, logits, LLMCP_Q8_ACT_NONE, fixed)))
+  // maximum of the last row is reduced from HBM.  Always the serial block
+  // order: the argmax id must be the reference's.
+  if ((rc = gemm_common(ctx, in, w, logits, LLMCP_Q8_ACT_NONE, fixed, true)))
     return rc;
   if (!argmax_dev) return LLMCP_Q8_OK;
   Workspace ws;

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol(q8):
 
 
 def test_abi_version(q8):
-    assert q8.lib().llmcp_q8_abi_version() == 6
+    assert q8.lib().llmcp_q8_abi_version() == 7
 
 
 def test_host_packer_matches_oracle(q8, oracle):
