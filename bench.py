@@ -652,6 +652,20 @@ def cpu_baseline(res, c1, c3, seq, budget_s=18.0):
         })
 
 
+def bench_peaks(ctx, nbytes=4 << 30):
+    """The device's measured peaks (llmcp_q8_microbench_*, the role of the
+    reference's microbench/cpu_microbench.cpp for its CPU): streaming read,
+    write and copy over a 4 GiB buffer (16x the Infinity Cache; 10 launches
+    after one untimed) and the int8 MFMA issue rate of independent chains
+    without memory traffic."""
+    return {"hbm_read_GB/s": round(ctx.microbench_bandwidth("read", nbytes), 1),
+            "hbm_write_GB/s": round(ctx.microbench_bandwidth("write", nbytes), 1),
+            "hbm_copy_GB/s": round(ctx.microbench_bandwidth("copy", nbytes), 1),
+            "int8_mfma_TOPS": round(ctx.microbench_int8_mfma(), 1),
+            "buffer_bytes": nbytes,
+            "spec": {"hbm_GB/s": HBM_PEAK_GBS, "int8_TOPS": INT8_PEAK_TOPS}}
+
+
 def copy_calibration(ctx, nbytes=256 << 20, reps=10):
     """A plain device copy of known size (HIP's copy kernel), run under
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE to scale the counters."""
@@ -720,26 +734,32 @@ def main():
     if args.norm_only:
         print(json.dumps({"rmsnorm": bench_norms(ctx, q8)}), flush=True)
         return
+    peaks = bench_peaks(ctx)
     res = bench_decode_mlp(ctx, q8, args.steps, args.warmup)
-    extra = {"platform": args.platform}
+    extra = {"platform": args.platform, "peaks": peaks}
+    read_peak, int8_peak = peaks["hbm_read_GB/s"], peaks["int8_mfma_TOPS"]
     repack = dict(res["repack_ms"])
     c1 = c3 = seq = None
     if not args.no_extra:
         c1 = bench_gemv(ctx, 2560, 2560)
         extra["gemv_2560x2560"] = {"us": round(c1["us"], 3), "GB/s": round(c1["gb_s"], 1),
-                                   "frac_hbm": round(c1["gb_s"] / HBM_PEAK_GBS, 4)}
+                                   "frac_hbm": round(c1["gb_s"] / HBM_PEAK_GBS, 4),
+                                   "frac_hbm_measured": round(c1["gb_s"] / read_peak, 4)}
         repack["2560x2560"] = round(c1["repack_ms"], 3)
         c1a = bench_gemv(ctx, 2560, 2560, residual=True)
         extra["gemv_2560x2560_residual_add"] = {"us": round(c1a["us"], 3)}
         c3 = bench_lm_head(ctx)
         extra["lm_head_248320x2560_argmax"] = {
             "us": round(c3["us"], 2), "GB/s": round(c3["gb_s"], 1),
-            "frac_hbm": round(c3["gb_s"] / HBM_PEAK_GBS, 4)}
+            "frac_hbm": round(c3["gb_s"] / HBM_PEAK_GBS, 4),
+            "frac_hbm_measured": round(c3["gb_s"] / read_peak, 4)}
         repack["248320x2560"] = round(c3["repack_ms"], 3)
         extra["embedding_gather_1024"] = {"us": round(c3["gather_us"], 2),
                                           "GB/s": round(c3["gather_gb_s"], 1)}
         for m in (64, 256, 1024):
-            extra["gemm_m%d_n9216_k2560" % m] = bench_gemm(ctx, m)
+            g = bench_gemm(ctx, m)
+            g["frac_int8_measured"] = round(g["op_TOPS"] / int8_peak, 4)
+            extra["gemm_m%d_n9216_k2560" % m] = g
         seq = bench_sequence(ctx)
         repack["7680x2560"] = round(seq["_qkv_repack_ms"], 3)
         extra["sequence_32_layers"] = {k: v for k, v in seq.items() if not k.startswith("_")}
@@ -770,10 +790,13 @@ def main():
                    "step_bytes": res["step_bytes"],
                    "weight_pool_bytes": res["pool_bytes"],
                    "weight_copies": res["copies"],
-                   "frac_hbm_peak": round(res["gb_s"] / HBM_PEAK_GBS, 4)},
+                   "frac_hbm_peak": round(res["gb_s"] / HBM_PEAK_GBS, 4),
+                   "frac_hbm_measured_peak": round(res["gb_s"] / read_peak, 4)},
         "roofline": {"bound": "hbm", "achieved": round(res["gu_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(res["gu_gbs"] / HBM_PEAK_GBS, 4),
+                     "measured_peak": read_peak,
+                     "frac_measured": round(res["gu_gbs"] / read_peak, 4),
                      "traffic": (load_traffic() or {}).get("hbm_bytes_per_launch"),
                      "kernel": "gemv_kernel<false,1,4,4,5,%d> (SwiGLU: gate and up "
                                "streamed by the two waves of a pair, 4-wave workgroups, "

@@ -650,6 +650,21 @@ int llmcp_q8_event_create(void **event);
 int llmcp_q8_event_destroy(void *event);
 int llmcp_q8_event_record(llmcp_q8_ctx *ctx, void *event);
 int llmcp_q8_event_elapsed_ms(void *start, void *stop, float *ms);
+/* Peaks of the device, measured (microbench/cpu_microbench.cpp's role for
+ * the reference's CPU: bandwidth read / write / copy, :480-503; the int8
+ * dot peak from independent accumulator chains, :203-260).
+ * llmcp_q8_microbench_bandwidth: kind 0 read, 1 write, 2 copy over a
+ * device buffer of `bytes` (rounded down to a multiple of 64 MiB; copy
+ * moves bytes / 2 each way), allocated for the call and freed after;
+ * `launches` timed launches after one untimed; *gb_per_s = bytes moved
+ * (read plus written) per second / 1e9.  llmcp_q8_microbench_int8_mfma:
+ * v_mfma_i32_32x32x32_i8 chains with no memory traffic, three waves per
+ * SIMD; *tops = int8 operations (2 per multiply-add) per second / 1e12.
+ * Both synchronize the context's stream. */
+int llmcp_q8_microbench_bandwidth(llmcp_q8_ctx *ctx, int32_t kind, uint64_t bytes,
+                                  int32_t launches, double *gb_per_s);
+int llmcp_q8_microbench_int8_mfma(llmcp_q8_ctx *ctx, int32_t iterations, double *tops);
+
 /* Stream capture into a HIP graph and replay (launch-bound loops).  A graph
  * holds the device addresses of the context's workspace and weights at
  * capture: graph_launch refuses it with LLMCP_Q8_ESTALE once any of them

@@ -86,6 +86,7 @@ EXPORTS = [
     "llmcp_q8_rmsnorm", "llmcp_q8_rmsnorm_bf16", "llmcp_q8_rmsnorm_linear_group",
     "llmcp_q8_rmsnorm_linear_group_bf16", "llmcp_q8_gated_rmsnorm",
     "llmcp_q8_gated_rmsnorm_bf16", "llmcp_q8_set_accumulation", "llmcp_q8_get_accumulation",
+    "llmcp_q8_microbench_bandwidth", "llmcp_q8_microbench_int8_mfma",
     "_mlir_ciface_llmcp_q8_linear_group3_bf16", "_mlir_ciface_llmcp_q8_linear_group4_bf16",
     "_mlir_ciface_llmcp_q8_rmsnorm", "_mlir_ciface_llmcp_q8_rmsnorm_bf16",
     "_mlir_ciface_llmcp_q8_gated_rmsnorm", "_mlir_ciface_llmcp_q8_gated_rmsnorm_bf16",
@@ -111,6 +112,8 @@ def lib():
         "llmcp_q8_test_ctx_rmsnorm_skew": (I, [P, I32]),
         "llmcp_q8_test_ctx_gemm_splits": (I, [P, I32]),
         "llmcp_q8_set_accumulation": (I, [P, I32]),
+        "llmcp_q8_microbench_bandwidth": (I, [P, I32, U64, I32, ctypes.POINTER(ctypes.c_double)]),
+        "llmcp_q8_microbench_int8_mfma": (I, [P, I32, ctypes.POINTER(ctypes.c_double)]),
         "llmcp_q8_get_accumulation": (I32, [P]),
         "llmcp_q8_last_error": (ctypes.c_char_p, []),
         "llmcp_q8_ctx_create": (I, [I, ctypes.POINTER(P)]),
@@ -321,6 +324,20 @@ class Context:
     def accumulation(self):
         code = lib().llmcp_q8_get_accumulation(self.handle)
         return {v: k for k, v in ACCUM.items()}.get(code, code)
+
+    def microbench_bandwidth(self, kind, nbytes, launches=10):
+        """Measured streaming GB/s: kind 'read', 'write' or 'copy'."""
+        out = ctypes.c_double(0.0)
+        check(lib().llmcp_q8_microbench_bandwidth(
+            self.handle, {"read": 0, "write": 1, "copy": 2}[kind], int(nbytes), int(launches),
+            ctypes.byref(out)))
+        return out.value
+
+    def microbench_int8_mfma(self, iterations=20000):
+        """Measured int8 MFMA TOPS (no memory traffic)."""
+        out = ctypes.c_double(0.0)
+        check(lib().llmcp_q8_microbench_int8_mfma(self.handle, int(iterations), ctypes.byref(out)))
+        return out.value
 
     def set_platform_code(self, code):
         """llmcp_q8_set_platform with a raw code (tests of the error path)."""

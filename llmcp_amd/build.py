@@ -13,7 +13,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libllmcp_q8.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["q8_kernels.hip", "q8_gemv_fma.hip", "q8_gemm.hip", "q8_runtime.cpp"]
+SOURCES = ["q8_kernels.hip", "q8_gemv_fma.hip", "q8_gemm.hip", "q8_microbench.hip",
+           "q8_runtime.cpp"]
 
 ROOT = os.path.dirname(HERE)
 CONSUMER_SRC = os.path.join(ROOT, "tests", "c_consumer", "q8_consumer.cpp")

@@ -169,6 +169,16 @@ hipError_t launch_embedding(const int64_t *tokens, int64_t count,
                             void *out, bool out_bf16, int64_t ldo,
                             int32_t *err_flag, hipStream_t s);
 
+// Peak microbenchmarks (q8_microbench.hip).  launch_stream: kind 0 reads
+// `bytes` at src (dst: a 4 B sink, never written in practice), 1 writes
+// them at dst, 2 copies src to dst; bytes a multiple of cus * 256 KiB.
+hipError_t launch_stream(int kind, const void *src, void *dst, int64_t bytes, int cus,
+                         hipStream_t s);
+// int8 MFMA chains with no memory traffic; mfma_i8_peak_ops is the number
+// of int8 operations one launch performs.
+hipError_t launch_mfma_i8_peak(int32_t iterations, int cus, unsigned *sink, hipStream_t s);
+double mfma_i8_peak_ops(int32_t iterations, int cus);
+
 hipError_t launch_block_dots(const int8_t *qa, int64_t ldq, int64_t m,
                              const uint8_t *w, int64_t rows, int64_t cols,
                              int32_t *out, hipStream_t s);

@@ -2463,6 +2463,95 @@ int llmcp_q8_event_elapsed_ms(void *start, void *stop, float *ms) {
   });
 }
 
+// Compute units of the context's device.
+static int ctx_cus(llmcp_q8_ctx *ctx) {
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, ctx->device) !=
+          hipSuccess || n <= 0)
+    n = 256;
+  return n;
+}
+
+int llmcp_q8_microbench_bandwidth(llmcp_q8_ctx *ctx, int32_t kind, uint64_t bytes,
+                                  int32_t launches, double *gb_per_s) {
+  return guarded([&]() -> int {
+    if (!ctx || !gb_per_s) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (kind < 0 || kind > 2 || launches < 1)
+      return fail(LLMCP_Q8_EINVAL, "bandwidth kind %d, %d launches", kind, launches);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const int cus = ctx_cus(ctx);
+    const uint64_t unit = 64ull << 20;  // a multiple of cus * 256 KiB up to 256 CUs
+    const uint64_t half = (kind == 2 ? bytes / 2 : bytes) / unit * unit;
+    if (half == 0 || cus > 256)
+      return fail(LLMCP_Q8_EINVAL, "bandwidth buffer of %llu bytes on %d CUs",
+                  (unsigned long long)bytes, cus);
+    void *a = nullptr, *b = nullptr;
+    unsigned *sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    auto release = [&]() {
+      if (a) (void)hipFree(a);
+      if (b) (void)hipFree(b);
+      if (sink) (void)hipFree(sink);
+      if (e0) (void)hipEventDestroy(e0);
+      if (e1) (void)hipEventDestroy(e1);
+    };
+    if (hipMalloc(&a, half) != hipSuccess || (kind == 2 && hipMalloc(&b, half) != hipSuccess) ||
+        hipMalloc((void **)&sink, 256) != hipSuccess) {
+      release();
+      return fail(LLMCP_Q8_ENOMEM, "bandwidth buffers of %llu bytes",
+                  (unsigned long long)half);
+    }
+    hipError_t e = hipMemsetAsync(a, 1, half, ctx->stream);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    const void *src = a;
+    void *dst = kind == 0 ? (void *)sink : kind == 1 ? a : b;
+    if (e == hipSuccess) e = launch_stream(kind, src, dst, (int64_t)half, cus, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(e0, ctx->stream);
+    for (int32_t i = 0; i < launches && e == hipSuccess; ++i)
+      e = launch_stream(kind, src, dst, (int64_t)half, cus, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    release();
+    if (e != hipSuccess) return hip_fail(e, "bandwidth microbenchmark");
+    const double moved = (double)half * (kind == 2 ? 2.0 : 1.0) * launches;
+    *gb_per_s = moved / (ms * 1e-3) / 1e9;
+    return LLMCP_Q8_OK;
+  });
+}
+
+int llmcp_q8_microbench_int8_mfma(llmcp_q8_ctx *ctx, int32_t iterations, double *tops) {
+  return guarded([&]() -> int {
+    if (!ctx || !tops) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (iterations < 1) return fail(LLMCP_Q8_EINVAL, "%d iterations", iterations);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const int cus = ctx_cus(ctx);
+    unsigned *sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipMalloc((void **)&sink, 256) != hipSuccess)
+      return fail(LLMCP_Q8_ENOMEM, "microbenchmark sink");
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = launch_mfma_i8_peak(iterations / 8 + 1, cus, sink, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(e0, ctx->stream);
+    if (e == hipSuccess) e = launch_mfma_i8_peak(iterations, cus, sink, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipFree(sink);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return hip_fail(e, "int8 MFMA microbenchmark");
+    *tops = mfma_i8_peak_ops(iterations, cus) / (ms * 1e-3) / 1e12;
+    return LLMCP_Q8_OK;
+  });
+}
+
 int llmcp_q8_graph_begin(llmcp_q8_ctx *ctx) {
   return guarded([&]() -> int {
     if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");

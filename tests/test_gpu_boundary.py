@@ -137,3 +137,23 @@ def test_platform_switch_is_per_context(q8, oracle):
         with pytest.raises(q8.Q8Error) as e:
             a.set_platform_code(7)
         assert e.value.code == q8.EINVAL
+
+
+def test_microbench_peaks(q8):
+    """The peak microbenchmarks run and report plausible rates (HBM reads
+    between 1 and 8 TB/s over a buffer past every cache, int8 MFMA between
+    0.5 and 5.1 POPS), and reject bad arguments."""
+    c = q8.Context(0)
+    try:
+        rd = c.microbench_bandwidth("read", 1 << 30, launches=3)
+        cp = c.microbench_bandwidth("copy", 1 << 30, launches=3)
+        assert 1000.0 < rd < 8000.0, rd
+        assert 1000.0 < cp < 8000.0, cp
+        tops = c.microbench_int8_mfma(2000)
+        assert 500.0 < tops < 5100.0, tops
+        with pytest.raises(q8.Q8Error):
+            c.microbench_bandwidth("read", 1 << 20)  # below one 64 MiB unit
+        with pytest.raises(q8.Q8Error):
+            q8.check(q8.lib().llmcp_q8_microbench_int8_mfma(c.handle, 0, None))
+    finally:
+        c.close()
