@@ -1028,6 +1028,10 @@ static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
   if (in_loop) {
     l.x = x.data;
     l.x_bf16 = x.bf16;
+  } else if (w1) {
+    // the SwiGLU GEMV quantizes its row in each workgroup, from 16 B (8 B)
+    // aligned loads
+    return fail(LLMCP_Q8_DECLINED, "SwiGLU input row must be %d B aligned", x.bf16 ? 8 : 16);
   } else {
     const int64_t nblk = passes_for(w0->cols) * kPassBlocks;
     int rc = reserve(ctx, ws, (uint64_t)(nblk * kBlock), (uint64_t)(nblk * 4));

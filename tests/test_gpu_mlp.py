@@ -142,3 +142,15 @@ def test_mlp_several_rows(ctx, oracle, mlp_weights, mode, dtype):
     ctx.swiglu(xd, tg, tu, h2, m, mode=mode, dtype=dtype)
     ctx.linear(h2, td, y3, m, mode=mode, dtype=dtype)
     assert bits_equal(ctx.to_host(y3, (m, HIDDEN), et), y_ref)
+
+
+def test_swiglu_misaligned_row_declined(ctx, q8, mlp_weights):
+    """The one-row SwiGLU (and so the decode MLP) quantizes its row in each
+    workgroup from 16 B loads: a row that is not 16 B aligned is declined
+    with LLMCP_Q8_DECLINED (the caller falls back), not a HIP error."""
+    _, (tg, tu, td) = mlp_weights
+    xd, hd, yd = ctx.alloc(HIDDEN * 4 + 16), ctx.alloc(FFN * 4), ctx.alloc(HIDDEN * 4)
+    with pytest.raises(q8.Declined):
+        ctx.swiglu(xd.ptr + 4, tg, tu, hd, 1)
+    with pytest.raises(q8.Declined):
+        ctx.mlp(xd.ptr + 4, tg, tu, td, yd, h=hd)
