@@ -158,16 +158,20 @@ struct Seg6 {
 // EPI: activation code in bits 0-1, bf16 output in bit 2, the SwiGLU
 // multiply by `mul` (f32) in bit 3, the residual add of `mul` (y's element
 // type, no activation) in bit 4 (compile time: the epilogue is inlined for
-// every accumulator element).
-template <int WM, int WN, int NST, bool FMA, int SEG, int EPI, bool PERSIST>
+// every accumulator element).  KSPLIT: the launch splits K (`splits` > 1,
+// partial sums, never persistent); without it `splits` and `split_stride`
+// are ignored and the stage arithmetic folds as for one split.
+template <int WM, int WN, int NST, bool FMA, int SEG, int EPI, bool PERSIST, bool KSPLIT>
 __global__ __launch_bounds__(64 * WM * WN)
 __attribute__((amdgpu_waves_per_eu(WM * WN >= 12 ? 3 : 2)))
 void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
                  int32_t row_tiles, int32_t nblk, const uint8_t *__restrict__ w,
                  int64_t n_rows, int64_t m_rows, int32_t passes, int32_t m_tiles,
                  int32_t n_tiles, void *y, int64_t ldy, const void *mul,
-                 int64_t ldg, int32_t splits, int64_t split_stride) {
+                 int64_t ldg, int32_t splits_arg, int64_t split_stride) {
   typedef GemmStage<WM, WN, SEG> St;
+  static_assert(!(KSPLIT && PERSIST), "K splits run one tile per workgroup");
+  const int32_t splits = KSPLIT ? splits_arg : 1;
   static_assert(NST == 2 || NST == 4, "stage buffers");
   constexpr int W = WM * WN;
   constexpr int BM = 32 * WM, BN = 32 * WN;
@@ -189,11 +193,17 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   const int G = gridDim.x;
   auto tile_of = [&](int id, int &mt, int &nt, int &sp) __attribute__((always_inline)) {
     const int kk = id >> 3;
-    const int per = m_tiles * splits;
-    nt = (kk / per) * 8 + (id & 7);
-    const int r = kk - (kk / per) * per;
-    sp = r / m_tiles;
-    mt = r - sp * m_tiles;
+    if constexpr (KSPLIT) {
+      const int per = m_tiles * splits;
+      nt = (kk / per) * 8 + (id & 7);
+      const int r = kk - (kk / per) * per;
+      sp = r / m_tiles;
+      mt = r - sp * m_tiles;
+    } else {
+      nt = (kk / m_tiles) * 8 + (id & 7);
+      mt = kk % m_tiles;
+      sp = 0;
+    }
   };
   auto next_tile = [&](int id) __attribute__((always_inline)) {
     for (; id < total; id += G) {
@@ -210,9 +220,10 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   int64_t m0 = (int64_t)m_tile * BM;
   int64_t n0 = (int64_t)n_tile * BN;
   // this workgroup's stages (four per pass) and the first one's index
-  const int pass0 = split * passes / splits;
+  const int pass0 = KSPLIT ? split * passes / splits : 0;
   const int sbase = pass0 * (kPassBlocks / kStageBlocks);
-  const int stages = ((split + 1) * passes / splits - pass0) * (kPassBlocks / kStageBlocks);
+  const int stages = (KSPLIT ? (split + 1) * passes / splits - pass0 : passes) *
+                     (kPassBlocks / kStageBlocks);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -742,16 +753,23 @@ static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
   // the epilogue's second operand: the SwiGLU gate or the residual
   const void *mp = (EPI & 16) != 0 ? l.add : (const void *)l.mul;
   const int64_t ld = (EPI & 16) != 0 ? l.ldr : l.ldg;
-  if (kPersist && splits == 1 && grid < total)
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, kPersist>), dim3(grid),
+  if (splits > 1) {
+    if constexpr (EPI == 0)
+      hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, 0, false, true>), dim3(total),
+                         dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
+                         l.w, l.rows, l.m, passes, m_tiles, n_tiles, y, ldy,
+                         mp, ld, splits, stride);
+  } else if (kPersist && grid < total) {
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, kPersist, false>), dim3(grid),
                        dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
                        l.w, l.rows, l.m, passes, m_tiles, n_tiles, y, ldy,
-                       mp, ld, splits, stride);
-  else
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, false>), dim3(total),
+                       mp, ld, 1, 0);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, false, false>), dim3(total),
                        dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
                        l.w, l.rows, l.m, passes, m_tiles, n_tiles, y, ldy,
-                       mp, ld, splits, stride);
+                       mp, ld, 1, 0);
+  }
 }
 
 template <int WM, int WN, int NST, bool FMA, int SEG>
