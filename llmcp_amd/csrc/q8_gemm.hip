@@ -266,6 +266,22 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
       dst16[u] = (int)offsetof(St, dw16) + (o - St::CA - St::CB - St::CS) * 1024;
     }
   }
+  // The wave-uniform part of a 16 B op's source for the stage whose first
+  // block is kb at (unit, slot): base + kb * ca + (unit * kPassBytes & um) +
+  // (slot * 16 & sm), with the base and coefficients resolved from the
+  // op's kind once here, so that a stage costs a few scalar operations per
+  // op and no branch on the kind.
+  const uint8_t *obase[St::S16];
+  uint32_t oca[St::S16], oum[St::S16], osm[St::S16];
+#pragma unroll
+  for (int u = 0; u < St::S16; ++u) {
+    const bool a_ = kind[u] == K_A, b_ = kind[u] == K_B, s_ = kind[u] == K_SA;
+    obase[u] = uniform_ptr(a_ ? (const uint8_t *)qa + abb[u] * 1024
+                              : s_ ? (const uint8_t *)sa : w);
+    oca[u] = a_ ? 1024u : s_ ? 128u : 0u;
+    oum[u] = (a_ || s_) ? 0u : ~0u;
+    osm[u] = b_ ? ~0u : 0u;
+  }
 #pragma unroll
   for (int u = 0; u < St::S4; ++u) {
     int o = wave + u * W;
@@ -356,11 +372,8 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     int8_t *lds_base = (int8_t *)&buf;
     if constexpr (j < St::S16) {
       const int u = j;
-      const uint8_t *wb = w + sp.unit * kPassBytes + sp.slot * 16;
-      const uint8_t *ab = (const uint8_t *)qa + (int64_t)(kb + abb[u]) * 1024;
-      const uint8_t *sab = (const uint8_t *)sa + (int64_t)kb * 128;
-      const uint8_t *db = w + sp.unit * kPassBytes;
-      const uint8_t *base = kind[u] == K_A ? ab : kind[u] == K_B ? wb : kind[u] == K_SA ? sab : db;
+      const uint32_t off = (uint32_t)kb * oca[u] + ((uint32_t)sp.unit * kPassBytes & oum[u]) +
+                           ((uint32_t)sp.slot * 16u & osm[u]);
       uint32_t extra = 0;
       if constexpr (SEG == 6) {
         // masks, not a select between array elements (which the compiler
@@ -369,7 +382,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
         const uint32_t m0 = sp.r == 0 ? ~0u : 0u, m2 = sp.r == 2 ? ~0u : 0u;
         extra = (x16r0[u] & m0) | (x16r2[u] & m2) | (x16r4[u] & ~(m0 | m2));
       }
-      dma16(uniform_ptr(base) + of.o16[u] + extra, lds_base + dst16[u]);
+      dma16(obase[u] + off + of.o16[u] + extra, lds_base + dst16[u]);
     } else {
       const int u = j - St::S16;
       const uint8_t *db = w + sp.unit * kPassBytes + 2 * (sp.slot & ~1);
