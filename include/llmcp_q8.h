@@ -96,10 +96,11 @@ enum llmcp_q8_platform {
  *                  block-order sum, bit for bit.
  * SPLIT_K          linears of several rows (the GEMM path: linear, linear +
  *                  add, grouped linears, SwiGLU, MLP, RMSNorm + group) whose
- *                  tiles leave over half the GPU idle (65 to 128 rows at the
- *                  model's widths) split K into two ranges of whole
- *                  512-value passes (a second kernel then adds the ranges'
- *                  partial sums: worth it only there): each range is a serial
+ *                  tiles leave CUs idle split K into ranges of whole
+ *                  512-value passes, as many as keep one workgroup per CU
+ *                  (and at most max(3, passes / 3); a second kernel then
+ *                  adds the ranges' partial sums, so shapes that already
+ *                  fill the GPU stay unsplit): each range is a serial
  *                  chain of the platform's epilogue, and the ranges' f32
  *                  partial sums are added in range order.  The per-block
  *                  int32 dots are still exact; f32 outputs agree with the

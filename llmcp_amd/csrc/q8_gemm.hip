@@ -863,17 +863,27 @@ int32_t gemm_splits_for(int64_t m, int64_t rows, int64_t cols, int32_t forced) {
   const int32_t passes = (int32_t)passes_for(cols);
   if (m <= 1 || passes <= 1) return 1;
   if (forced > 0) return std::min(forced, passes);
-  // Two splits where the 12-wave shape leaves more than half the CUs idle
-  // (its tiles < CUs / 2); otherwise none.  Measured at N = 9216, K = 2560
-  // (op time: the quantizer, the GEMM and, split, the reduction): M = 128
-  // 32.4 -> 28.8 us with two splits; every split count was slower at
-  // M = 16 / 64 (18.5 / 18.9 us unsplit, 20.7-27.2 split), M = 256 (34.9
-  // against 49.8-58.6) and M = 512.  The 64-row shape's waves are bound by
-  // each CU's operand delivery, which splits share, and the reduction costs
-  // a launch.
-  if (small_shape(m)) return 1;
-  const int64_t tiles = ((m + 127) / 128) * ((rows + 95) / 96);
-  return 2 * tiles < (int64_t)cu_count() && passes >= 2 ? 2 : 1;
+  // As many splits as keep tiles x splits within one workgroup per CU, and
+  // at most max(3, passes / 3) (three passes per split where K has nine or
+  // more).  Measured op time (quantizer, GEMM, reduction) against EXACT,
+  // splits in brackets:
+  //   N = 2560, K = 9216: M = 64 65.9 -> 26.9 us (6); M = 128 109.8 -> 37.6
+  //     (6; 9 splits 50.1); M = 256 109.2 -> 48.7 (4; 6 splits 61.6);
+  //     M = 512 107.7 -> 72.8 (2; 3 splits 92.2); M = 1024 127.8, every
+  //     split slower.
+  //   N = 2560, K = 2560: M = 64 17.5 -> 14.8 (3; 5 splits 14.2);
+  //     M = 256 29.1 -> 22.9 (3; 4 splits 23.3).
+  //   N = 7680, K = 2560: M = 128 30.1 -> 24.8 (3; 4 splits 36.5);
+  //     M = 256 31.9, every split slower.
+  //   N = 9216, K = 2560: M = 128 32.4 -> 28.8 (2); M = 16 / 64 / 256
+  //     slower split.
+  // A second workgroup per CU (the 64-row tiles fit two) shares the CU's
+  // operand delivery, so the bound is one per CU for both tile shapes.
+  const int64_t tiles = small_shape(m) ? ((m + 63) / 64) * ((rows + 63) / 64)
+                                       : ((m + 127) / 128) * ((rows + 95) / 96);
+  const int64_t by_cus = (int64_t)cu_count() / tiles;
+  const int64_t by_passes = std::max<int64_t>(std::min<int64_t>(passes, 3), passes / 3);
+  return (int32_t)std::max<int64_t>(1, std::min(by_cus, by_passes));
 }
 
 }  // namespace llmcp_q8

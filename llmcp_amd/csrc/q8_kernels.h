@@ -131,8 +131,9 @@ hipError_t launch_gemm(const GemmLaunch &l, hipStream_t s);
 
 // K splits for a multi-row linear of [m x cols] by [rows x cols] when
 // splitting is allowed: `forced` > 0 (clamped to the pass count), else the
-// count measured fastest for the shape class (2 where the 12-wave tiles
-// leave over half the CUs idle, otherwise 1).
+// count measured fastest for the shape class (tiles x splits within one
+// workgroup per CU, at most max(3, passes / 3); 1 where the tiles already
+// cover the CUs).
 int32_t gemm_splits_for(int64_t m, int64_t rows, int64_t cols, int32_t forced);
 
 // Q8_1 activations in the GEMM's tiled layout: the 32 rows x 32 values of
