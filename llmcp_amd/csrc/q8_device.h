@@ -6,6 +6,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace llmcp_q8 {
 
 // Activation codes of include/llmcp_q8.h (llmcp_q8_activation).
@@ -137,6 +139,17 @@ __device__ __forceinline__ float activate(float v, int act) {
     case ACT_SOFTPLUS: return softplus_f32(v);
     default: return v;
   }
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1,
+// so that every private-array index in the body is a constant.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 }  // namespace llmcp_q8

@@ -85,17 +85,6 @@ struct GemmStage {
   __align__(16) uint32_t dw4[CD4 > 0 ? WN : 1][2][64];
 };
 
-// Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1,
-// so that every private-array index in the body is a constant.
-template <class F, int... I>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ void dma16(const void *g, void *lds_base) {
@@ -505,9 +494,15 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     const int kb = (sbase + s) * kStageBlocks;
     static_for<kStageBlocks>([&](auto BB) __attribute__((always_inline)) {
       constexpr int bb = decltype(BB)::value;
-      const v16i c_next = dots(fr);
+      v16i c_next = dots(fr);
       v32f f_next;
       if constexpr ((bb & 1) != 0) f_next = scale_tile(bb == 1 ? kb : kb + kStageBlocks, sr, bb == 1 ? 1 : 0);
+      // The MFMAs are pure operations: instruction selection would place
+      // them next to their first use (the next block's epilogue), which
+      // then waits for them.  An empty asm that takes their results keeps
+      // them here, ahead of this block's epilogue.
+      asm volatile("" ::"v"(c_next));
+      if constexpr ((bb & 1) != 0) asm volatile("" ::"v"(f_next));
       if constexpr (bb == 2) {
         wait_vmcnt<kMidOps>();
         stage_barrier();
