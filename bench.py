@@ -656,12 +656,18 @@ def bench_peaks(ctx, nbytes=4 << 30):
     """The device's measured peaks (llmcp_q8_microbench_*, the role of the
     reference's microbench/cpu_microbench.cpp for its CPU): streaming read,
     write and copy over a 4 GiB buffer (16x the Infinity Cache; 10 launches
-    after one untimed) and the int8 MFMA issue rate of independent chains
-    without memory traffic."""
+    after one untimed), the int8 MFMA issue rate of independent chains
+    without memory traffic, and the ceiling of the prefill GEMM's per-block
+    work without its memory stream: the exact epilogue (int8 MFMA, a convert
+    and an FMA per element and block), the same with convert-free f16 dots,
+    and its MFMAs alone."""
     return {"hbm_read_GB/s": round(ctx.microbench_bandwidth("read", nbytes), 1),
             "hbm_write_GB/s": round(ctx.microbench_bandwidth("write", nbytes), 1),
             "hbm_copy_GB/s": round(ctx.microbench_bandwidth("copy", nbytes), 1),
             "int8_mfma_TOPS": round(ctx.microbench_int8_mfma(), 1),
+            "gemm_exact_epilogue_TOPS": round(ctx.microbench_epilogue("exact"), 1),
+            "gemm_cvtfree_epilogue_TOPS": round(ctx.microbench_epilogue("cvtfree"), 1),
+            "gemm_mfma_only_TOPS": round(ctx.microbench_epilogue("mfma"), 1),
             "buffer_bytes": nbytes,
             "spec": {"hbm_GB/s": HBM_PEAK_GBS, "int8_TOPS": INT8_PEAK_TOPS}}
 
@@ -759,6 +765,8 @@ def main():
         for m in (64, 256, 1024):
             g = bench_gemm(ctx, m)
             g["frac_int8_measured"] = round(g["op_TOPS"] / int8_peak, 4)
+            g["frac_exact_epilogue_ceiling"] = round(
+                g["op_TOPS"] / peaks["gemm_exact_epilogue_TOPS"], 4)
             extra["gemm_m%d_n9216_k2560" % m] = g
         seq = bench_sequence(ctx)
         repack["7680x2560"] = round(seq["_qkv_repack_ms"], 3)

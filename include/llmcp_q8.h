@@ -661,10 +661,20 @@ int llmcp_q8_event_elapsed_ms(void *start, void *stop, float *ms);
  * (read plus written) per second / 1e9.  llmcp_q8_microbench_int8_mfma:
  * v_mfma_i32_32x32x32_i8 chains with no memory traffic, three waves per
  * SIMD; *tops = int8 operations (2 per multiply-add) per second / 1e12.
- * Both synchronize the context's stream. */
+ * llmcp_q8_microbench_epilogue: the prefill GEMM's per-block work on one
+ * 32x32 tile without its memory stream, three waves per SIMD, `blocks`
+ * blocks per wave (rounded down to even, at least 2): mode 0 the exact
+ * epilogue (int8 MFMA, f32 scale tile, a convert and an FMA per element
+ * and block), mode 1 the same with two f16 MFMAs per block on
+ * integer-valued operands and no convert, mode 2 the MFMAs alone; *tops =
+ * the tile's int8 operations (2 * 32^3 per block) per second / 1e12, the
+ * ceiling of the GEMM for that epilogue.  All synchronize the context's
+ * stream. */
 int llmcp_q8_microbench_bandwidth(llmcp_q8_ctx *ctx, int32_t kind, uint64_t bytes,
                                   int32_t launches, double *gb_per_s);
 int llmcp_q8_microbench_int8_mfma(llmcp_q8_ctx *ctx, int32_t iterations, double *tops);
+int llmcp_q8_microbench_epilogue(llmcp_q8_ctx *ctx, int32_t mode, int32_t blocks,
+                                 double *tops);
 
 /* Stream capture into a HIP graph and replay (launch-bound loops).  A graph
  * holds the device addresses of the context's workspace and weights at

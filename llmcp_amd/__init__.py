@@ -87,6 +87,7 @@ EXPORTS = [
     "llmcp_q8_rmsnorm_linear_group_bf16", "llmcp_q8_gated_rmsnorm",
     "llmcp_q8_gated_rmsnorm_bf16", "llmcp_q8_set_accumulation", "llmcp_q8_get_accumulation",
     "llmcp_q8_microbench_bandwidth", "llmcp_q8_microbench_int8_mfma",
+    "llmcp_q8_microbench_epilogue",
     "_mlir_ciface_llmcp_q8_linear_group3_bf16", "_mlir_ciface_llmcp_q8_linear_group4_bf16",
     "_mlir_ciface_llmcp_q8_rmsnorm", "_mlir_ciface_llmcp_q8_rmsnorm_bf16",
     "_mlir_ciface_llmcp_q8_gated_rmsnorm", "_mlir_ciface_llmcp_q8_gated_rmsnorm_bf16",
@@ -114,6 +115,7 @@ def lib():
         "llmcp_q8_set_accumulation": (I, [P, I32]),
         "llmcp_q8_microbench_bandwidth": (I, [P, I32, U64, I32, ctypes.POINTER(ctypes.c_double)]),
         "llmcp_q8_microbench_int8_mfma": (I, [P, I32, ctypes.POINTER(ctypes.c_double)]),
+        "llmcp_q8_microbench_epilogue": (I, [P, I32, I32, ctypes.POINTER(ctypes.c_double)]),
         "llmcp_q8_get_accumulation": (I32, [P]),
         "llmcp_q8_last_error": (ctypes.c_char_p, []),
         "llmcp_q8_ctx_create": (I, [I, ctypes.POINTER(P)]),
@@ -337,6 +339,16 @@ class Context:
         """Measured int8 MFMA TOPS (no memory traffic)."""
         out = ctypes.c_double(0.0)
         check(lib().llmcp_q8_microbench_int8_mfma(self.handle, int(iterations), ctypes.byref(out)))
+        return out.value
+
+    def microbench_epilogue(self, mode="exact", blocks=20000):
+        """TOPS ceiling of the prefill GEMM's per-block work without its memory
+        stream: mode 'exact' (int8 MFMA + convert + FMA), 'cvtfree' (f16
+        MFMAs on integer operands + FMA) or 'mfma' (the MFMAs alone)."""
+        out = ctypes.c_double(0.0)
+        check(lib().llmcp_q8_microbench_epilogue(
+            self.handle, {"exact": 0, "cvtfree": 1, "mfma": 2}[mode], int(blocks),
+            ctypes.byref(out)))
         return out.value
 
     def set_platform_code(self, code):

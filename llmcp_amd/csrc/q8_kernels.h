@@ -179,6 +179,13 @@ hipError_t launch_stream(int kind, const void *src, void *dst, int64_t bytes, in
 // of int8 operations one launch performs.
 hipError_t launch_mfma_i8_peak(int32_t iterations, int cus, unsigned *sink, hipStream_t s);
 double mfma_i8_peak_ops(int32_t iterations, int cus);
+// The prefill GEMM's per-block instruction mix on LDS-resident operands
+// (mode 0 the exact int8 epilogue, 1 convert-free f16 dots, 2 the MFMAs
+// alone), 2 * pairs blocks per wave; epilogue_mix_ops counts 2 * 32^3
+// operations per wave and block.
+hipError_t launch_epilogue_mix(int mode, int32_t pairs, int cus, unsigned *sink,
+                               hipStream_t s);
+double epilogue_mix_ops(int32_t pairs, int cus);
 
 hipError_t launch_block_dots(const int8_t *qa, int64_t ldq, int64_t m,
                              const uint8_t *w, int64_t rows, int64_t cols,

@@ -2556,6 +2556,38 @@ int llmcp_q8_microbench_int8_mfma(llmcp_q8_ctx *ctx, int32_t iterations, double 
   });
 }
 
+int llmcp_q8_microbench_epilogue(llmcp_q8_ctx *ctx, int32_t mode, int32_t blocks,
+                                 double *tops) {
+  return guarded([&]() -> int {
+    if (!ctx || !tops) return fail(LLMCP_Q8_EINVAL, "null argument");
+    if (mode < 0 || mode > 2 || blocks < 2)
+      return fail(LLMCP_Q8_EINVAL, "epilogue mode %d, %d blocks", mode, blocks);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const int cus = ctx_cus(ctx);
+    const int32_t pairs = blocks / 2;
+    unsigned *sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipMalloc((void **)&sink, 256) != hipSuccess)
+      return fail(LLMCP_Q8_ENOMEM, "microbenchmark sink");
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = launch_epilogue_mix(mode, pairs / 8 + 1, cus, sink, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(e0, ctx->stream);
+    if (e == hipSuccess) e = launch_epilogue_mix(mode, pairs, cus, sink, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipFree(sink);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return hip_fail(e, "epilogue microbenchmark");
+    *tops = epilogue_mix_ops(pairs, cus) / (ms * 1e-3) / 1e12;
+    return LLMCP_Q8_OK;
+  });
+}
+
 int llmcp_q8_graph_begin(llmcp_q8_ctx *ctx) {
   return guarded([&]() -> int {
     if (!ctx) return fail(LLMCP_Q8_EINVAL, "null context");

@@ -151,9 +151,20 @@ def test_microbench_peaks(q8):
         assert 1000.0 < cp < 8000.0, cp
         tops = c.microbench_int8_mfma(2000)
         assert 500.0 < tops < 5100.0, tops
+        # the GEMM's per-block work: the exact epilogue cannot beat its own
+        # MFMAs, and both stay below the MFMA issue peak
+        exact = c.microbench_epilogue("exact", 2000)
+        cvtfree = c.microbench_epilogue("cvtfree", 2000)
+        mfma = c.microbench_epilogue("mfma", 2000)
+        assert 100.0 < exact < 5100.0 and 100.0 < cvtfree < 5100.0, (exact, cvtfree)
+        assert exact < 1.05 * mfma < 1.05 * 5100.0, (exact, mfma)
         with pytest.raises(q8.Q8Error):
             c.microbench_bandwidth("read", 1 << 20)  # below one 64 MiB unit
         with pytest.raises(q8.Q8Error):
             q8.check(q8.lib().llmcp_q8_microbench_int8_mfma(c.handle, 0, None))
+        with pytest.raises(q8.Q8Error):
+            c.microbench_epilogue("exact", 1)  # below one block pair
+        with pytest.raises(q8.Q8Error):
+            q8.check(q8.lib().llmcp_q8_microbench_epilogue(c.handle, 3, 100, None))
     finally:
         c.close()
