@@ -452,9 +452,21 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
 
   // sched_barrier(0) pins the ring right after the row loads; without it
   // the scheduler sinks the loads toward their uses and only about one pass
-  // stays in flight.
+  // stays in flight.  With the row quantized in the workgroup, only the
+  // first kEarly units go out before the row is quantized and the rest
+  // right after: a wave blocks while the memory pipeline accepts its loads,
+  // so a whole ring issued first holds up the row's quantization, and with
+  // it the chain, until most of the ring has been accepted.  Measured per
+  // launch (graph replay, A/B on one box): the down GEMV (K = 9216,
+  // 13-unit ring) 7.03-7.09 us with all 13 first, 6.69-6.89 us with 6 (4
+  // to 8 alike); K = 2560 (4-unit ring) 3.43-3.44 us with all 4, 3.39 with
+  // 3.  The SwiGLU's wave pairs measured the same either way and keep the
+  // whole ring first, as do the grouped and argmax variants (not measured).
+  constexpr int kEarlyWant =
+      (!kRowFirst || PAIR || GROUP || ARGMAX) ? D : PC == 18 ? 6 : PC == 5 ? 3 : D;
+  constexpr int kEarly = kEarlyWant < D ? kEarlyWant : D;
 #pragma unroll
-  for (int d = 0; d < D; ++d) issue(d, d);
+  for (int d = 0; d < kEarly; ++d) issue(d, d);
   __builtin_amdgcn_sched_barrier(0);
 
   if (IN == IN_WG) {
@@ -519,6 +531,10 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(
     }
     __syncthreads();
   }
+  // the rest of the ring (all of it went out above unless kEarly < D)
+#pragma unroll
+  for (int d = kEarly; d < D; ++d) issue(d, d);
+  __builtin_amdgcn_sched_barrier(0);
 
   float acc = 0.0f;
 
