@@ -9,7 +9,10 @@ the 7680-wide QKV block and a residual branch r = x + o(x); two more
 2560 x 2560 blocks follow, then the MLP (gate/up 9216 x 2560 with silu * up,
 down 2560 x 9216) whose output is added to r.  Every row of every step
 depends only on the same row of the step before, so at M = 1024 the oracle
-follows a sample of rows through the whole chain.  The tied 248320 x 2560
+follows a sample of rows through the whole chain: two layers (with the
+lm_head and the gather) and all 32 layers with distinct weights, in the
+pre-norm residual form with the RMSNorms (with the grouped form of each
+layer's shared-input linears).  The tied 248320 x 2560
 table serves the last-row lm_head (ModelBuilder.cpp:492-513) and a gather of
 1024 token ids."""
 import numpy as np
@@ -123,6 +126,96 @@ def test_config5_two_layer_chain(ctx, oracle, model, m, mode):
             for w in t.values():
                 ctx.release(w)
         ctx.release(head)
+
+
+@pytest.fixture(scope="module")
+def model32(q8):
+    """All 32 layers of config 5 with distinct weights (seeds apart from the
+    two-layer fixture's), host copies of their p4 bytes for the oracle."""
+    with q8.Context(0) as c:
+        layers = []
+        for li in range(32):
+            w = {}
+            for j, (name, (n, k)) in enumerate(SHAPES.items()):
+                d, _ = c.synthesize_p4(seed=20000 + 16 * li + j, rows=n, cols=k)
+                w[name] = c.to_host(d, (d.nbytes,), np.uint8)
+                d.free()
+            layers.append(w)
+    return layers
+
+
+@pytest.mark.parametrize("m,mode", [(1, "decode"), (1024, "prefill")])
+def test_config5_32_layer_chain(ctx, oracle, model32, m, mode):
+    """All 32 layers of configs[4] as one chain, in the model builder's
+    pre-norm residual form (ModelBuilder.cpp:205-236, :271-275): xn =
+    RMSNorm(x); qkv(xn); r = x + o(xn); rn = RMSNorm(r); h = SwiGLU(b(a(rn)));
+    y = r + down(h), each layer's y the next layer's x (the norms keep the
+    residual stream finite over 32 layers; without them the SwiGLU squares
+    its magnitude every layer).  Every output on the checked rows is
+    bit-exact to the oracle (M = 1: the row; M = 1024: first, last and six
+    random rows, which depend only on themselves).  At each layer the four
+    linears of xn run as one group (the grouped form of the bench's
+    sequence) and equal the same four linears one call at a time, over all
+    M rows."""
+    layers = model32
+    regs = [{name: ctx.upload_p4(w[name], *SHAPES[name]) for name in SHAPES}
+            for w in layers]
+    try:
+        rng = np.random.default_rng(171 + m)
+        eps = 1e-6
+        norms = [(1.0 + 0.1 * rng.standard_normal((2, HIDDEN))).astype(np.float32)
+                 for _ in layers]
+        x0 = rng.standard_normal((m, HIDDEN)).astype(np.float32)
+        rows = np.arange(m) if m == 1 else np.unique(
+            np.concatenate([[0, m - 1], rng.choice(m, 6, replace=False)]))
+        sizes = {"xn": HIDDEN, "qkv": QKV, "r": HIDDEN, "rn": HIDDEN, "a": HIDDEN,
+                 "b": HIDDEN, "h": FFN, "y": HIDDEN}
+        bufs = [{k: ctx.alloc(m * n * 4) for k, n in sizes.items()} for _ in range(2)]
+        names = ("qkv", "o", "a", "b")
+        width = {"qkv": QKV, "o": HIDDEN, "a": HIDDEN, "b": HIDDEN}
+        grouped = {nm: ctx.alloc(m * width[nm] * 4) for nm in names}
+        single = {nm: ctx.alloc(m * width[nm] * 4) for nm in names}
+        x = ctx.to_device(x0)
+        xr = x0[rows]
+        lin = lambda v, w, name: oracle.linear(v, w[name], SHAPES[name][0],
+                                               epilogue=ctx.epilogue, colpar=True)
+        for li, t in enumerate(regs):
+            bf = bufs[li % 2]
+            n1, n2 = ctx.to_device(norms[li][0]), ctx.to_device(norms[li][1])
+            ctx.rmsnorm(x, n1, bf["xn"], m, HIDDEN, eps=eps)
+            # the grouped form of xn's four linears against single calls
+            ctx.linear_group(bf["xn"], [t[nm] for nm in names],
+                             [grouped[nm] for nm in names], m, mode=mode)
+            for nm in names:
+                ctx.linear(bf["xn"], t[nm], single[nm], m, mode=mode)
+                assert bits_equal(ctx.to_host(grouped[nm], (m, width[nm]), np.float32),
+                                  ctx.to_host(single[nm], (m, width[nm]), np.float32)), (li, nm)
+            ctx.linear(bf["xn"], t["qkv"], bf["qkv"], m, mode=mode)
+            ctx.linear_add(bf["xn"], t["o"], x, bf["r"], m, mode=mode)
+            ctx.rmsnorm(bf["r"], n2, bf["rn"], m, HIDDEN, eps=eps)
+            ctx.linear(bf["rn"], t["a"], bf["a"], m, mode=mode)
+            ctx.linear(bf["a"], t["b"], bf["b"], m, mode=mode)
+            ctx.swiglu(bf["b"], t["gate"], t["up"], bf["h"], m, mode=mode)
+            ctx.linear_add(bf["h"], t["down"], bf["r"], bf["y"], m, mode=mode)
+            w = layers[li]
+            xn = oracle.rmsnorm(xr, norms[li][0], eps)
+            qkv = lin(xn, w, "qkv")
+            r = (lin(xn, w, "o") + xr).astype(np.float32)
+            a = lin(oracle.rmsnorm(r, norms[li][1], eps), w, "a")
+            bb = lin(a, w, "b")
+            h = oracle.swiglu(bb, w["gate"], w["up"], FFN, epilogue=ctx.epilogue, colpar=True)
+            y = (lin(h, w, "down") + r).astype(np.float32)
+            got = lambda k, n: ctx.to_host(bf[k], (m, n), np.float32)[rows]
+            assert np.all(np.isfinite(y)), li
+            assert bits_equal(got("qkv", QKV), qkv), (li, m)
+            assert bits_equal(got("r", HIDDEN), r), (li, m)
+            assert bits_equal(got("h", FFN), h), (li, m)
+            assert bits_equal(got("y", HIDDEN), y), (li, m)
+            x, xr = bf["y"], y
+    finally:
+        for t in regs:
+            for w in t.values():
+                ctx.release(w)
 
 
 def test_real_model_arena(q8, oracle):
