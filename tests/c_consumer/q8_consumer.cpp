@@ -293,6 +293,46 @@ int main(int argc, char **argv) {
                 (double)bf16_to_f32(f32_to_bf16(1.5f)), (double)bf16_to_f32(r1[0]));
     for (void *q : {xd, wd, yd, gd, gw, o1, o2}) llmcp_q8_dev_free(ctx, q);
   }
+  // ABI 7: the accumulation switch and the peak microbenchmarks.  In
+  // SPLIT_K mode a 64-row linear of the 256 x 2560 weight (4 tiles) splits
+  // K; every output is still the same sum of K/32 equal terms, and its
+  // bf16 rounding is K.
+  {
+    const int64_t n = rows[1], k = cols[1], m = 64;
+    MemRef<int8_t, 1> w{(int8_t *)(file + off[1]), (int8_t *)(file + off[1]), 0,
+                        {n * (k + k / 16)}, {1}};
+    if (llmcp_q8_set_accumulation(ctx, LLMCP_Q8_ACCUM_SPLIT_K) ||
+        llmcp_q8_get_accumulation(ctx) != LLMCP_Q8_ACCUM_SPLIT_K)
+      return fail("set_accumulation");
+    void *xd = nullptr, *yd = nullptr;
+    if (llmcp_q8_dev_alloc(ctx, (uint64_t)(m * k * 4), &xd) ||
+        llmcp_q8_dev_alloc(ctx, (uint64_t)(m * n * 4), &yd))
+      return fail("alloc");
+    std::vector<float> xf(m * k, 1.0f), yf(m * n, 0.0f);
+    llmcp_q8_memcpy_h2d(ctx, xd, xf.data(), xf.size() * 4);
+    MemRef<float, 2> xm{(float *)xd, (float *)xd, 0, {m, k}, {k, 1}};
+    MemRef<float, 2> ym{(float *)yd, (float *)yd, 0, {m, n}, {n, 1}};
+    if (_mlir_ciface_llmcp_q8_linear((llmcp_memref_f32_2d *)&xm, (llmcp_memref_i8_1d *)&w,
+                                     (llmcp_memref_f32_2d *)&ym, LLMCP_Q8_ACT_NONE,
+                                     LLMCP_Q8_PREFILL))
+      return fail("split-K linear");
+    llmcp_q8_memcpy_d2h(ctx, yf.data(), yd, yf.size() * 4);
+    for (int64_t i = 0; i < m * n; ++i)
+      bad += yf[i] != yf[0] || bf16_to_f32(f32_to_bf16(yf[i])) != (float)k;
+    if (llmcp_q8_set_accumulation(ctx, LLMCP_Q8_ACCUM_EXACT)) return fail("set_accumulation");
+    llmcp_q8_dev_free(ctx, xd);
+    llmcp_q8_dev_free(ctx, yd);
+    double gbs = 0.0, tops = 0.0, ceiling = 0.0;
+    if (llmcp_q8_microbench_bandwidth(ctx, 0, 64ull << 20, 2, &gbs) || !(gbs > 0.0))
+      return fail("bandwidth microbenchmark");
+    if (llmcp_q8_microbench_int8_mfma(ctx, 200, &tops) || !(tops > 0.0))
+      return fail("int8 MFMA microbenchmark");
+    if (llmcp_q8_microbench_epilogue(ctx, 0, 200, &ceiling) || !(ceiling > 0.0))
+      return fail("epilogue microbenchmark");
+    std::printf("q8_consumer: split-K linear %.6g; read %.0f GB/s (64 MiB), int8 MFMA %.0f TOPS, "
+                "exact-epilogue ceiling %.0f TOPS (short runs)\n",
+                (double)yf[0], gbs, tops, ceiling);
+  }
   llmcp_q8_ctx_destroy(ctx);
   munmap(map, fsize);
   if (bad) {
