@@ -281,6 +281,23 @@ def bench_gemm(ctx, m, n=9216, k=2560, iters=30):
             "bytes": per + m * k * 4 + m * n * 4}
 
 
+def bench_split_k(ctx, n=2560, k=9216, ms=(64, 256)):
+    """The SPLIT_K accumulation mode (opt-in, within the north-star
+    tolerance) against EXACT on the down projection's shape at few rows,
+    where K = 9216 runs 72 serial stages per tile: op times of the same
+    calls in both modes (the count of splits is the library's choice)."""
+    out = {}
+    for m in ms:
+        fig = {}
+        for mode in ("exact", "split_k"):
+            ctx.set_accumulation(mode)
+            fig[mode + "_op_us"] = bench_gemm(ctx, m, n=n, k=k, iters=20)["op_us"]
+        ctx.set_accumulation("exact")
+        fig["speedup"] = round(fig["exact_op_us"] / fig["split_k_op_us"], 2)
+        out["m%d" % m] = fig
+    return out
+
+
 def bench_sequence(ctx, hidden=2560, ffn=9216, qkv=7680, layers=32, vocab=248320):
     """Config 5: every Q8_0 linear of a 32-layer 4B-class model plus the tied
     lm_head, all resident in HBM, at M=1 (decode) and M=1024 (prefill)."""
@@ -768,6 +785,7 @@ def main():
             g["frac_exact_epilogue_ceiling"] = round(
                 g["op_TOPS"] / peaks["gemm_exact_epilogue_TOPS"], 4)
             extra["gemm_m%d_n9216_k2560" % m] = g
+        extra["split_k_n2560_k9216"] = bench_split_k(ctx)
         seq = bench_sequence(ctx)
         repack["7680x2560"] = round(seq["_qkv_repack_ms"], 3)
         extra["sequence_32_layers"] = {k: v for k, v in seq.items() if not k.startswith("_")}
