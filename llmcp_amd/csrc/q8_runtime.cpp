@@ -2494,6 +2494,8 @@ int llmcp_q8_microbench_bandwidth(llmcp_q8_ctx *ctx, int32_t kind, uint64_t byte
     unsigned *sink = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     auto release = [&]() {
+      // launches queued before a failure may still use the buffers
+      (void)hipStreamSynchronize(ctx->stream);
       if (a) (void)hipFree(a);
       if (b) (void)hipFree(b);
       if (sink) (void)hipFree(sink);
@@ -2547,6 +2549,7 @@ int llmcp_q8_microbench_int8_mfma(llmcp_q8_ctx *ctx, int32_t iterations, double 
     if (e == hipSuccess) e = hipEventSynchronize(e1);
     float ms = 0.0f;
     if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipStreamSynchronize(ctx->stream);  // (after a failure: queued launches)
     (void)hipFree(sink);
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
@@ -2579,6 +2582,7 @@ int llmcp_q8_microbench_epilogue(llmcp_q8_ctx *ctx, int32_t mode, int32_t blocks
     if (e == hipSuccess) e = hipEventSynchronize(e1);
     float ms = 0.0f;
     if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipStreamSynchronize(ctx->stream);  // (after a failure: queued launches)
     (void)hipFree(sink);
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
