@@ -1071,11 +1071,26 @@ static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
   return LLMCP_Q8_OK;
 }
 
+// The prefill GEMM reads its operands at 32-bit offsets from their bases
+// (buffer-addressed loads): the weight and the tiled Q8_1 rows must each be
+// below 4 GiB, else the call is declined (the caller's CPU path runs).
+static int gemm_operands_fit(const Tensor *w, int64_t m) {
+  const uint64_t nblk = (uint64_t)passes_for(w->cols) * kPassBlocks;
+  const uint64_t rows = (uint64_t)((m + 31) / 32) * 32;
+  if (w->dev_bytes > 0xFFFFFFFFull || rows * nblk * kBlock > 0xFFFFFFFFull)
+    return fail(LLMCP_Q8_DECLINED,
+                "prefill GEMM operands must each be below 4 GiB (weight %llu bytes, "
+                "%lld rows of %lld blocks)",
+                (unsigned long long)w->dev_bytes, (long long)m, (long long)nblk);
+  return LLMCP_Q8_OK;
+}
+
 // Q8_1 of the input rows into the workspace (the GEMM's tiled layout; the
 // context's scratch grows on first use for a larger M).
 static int gemm_quantize(llmcp_q8_ctx *ctx, const Rows &in, const Tensor *w,
                          Workspace &ws) {
   const int64_t m = in.rows;
+  if (int rc = gemm_operands_fit(w, m)) return rc;
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   const int64_t row_tiles = (m + 31) / 32;  // the tiled layout pads M to 32
   int rc = reserve(ctx, ws, (uint64_t)(row_tiles * 32 * nblk * kBlock),
@@ -1100,6 +1115,7 @@ static int gemm_launch(llmcp_q8_ctx *ctx, const Workspace &ws, int64_t m,
                        const Tensor *w, const Rows &out, int activation,
                        const float *mul, int64_t ldg,
                        const Rows *residual = nullptr, bool exact = false) {
+  if (int rc = gemm_operands_fit(w, m)) return rc;
   const int64_t nblk = passes_for(w->cols) * kPassBlocks;
   GemmLaunch g;
   g.qa = ws.qa;
@@ -1242,7 +1258,10 @@ static int linear_group_run(llmcp_q8_ctx *ctx, const Rows &in, int32_t count,
   int rc = LLMCP_Q8_OK;
   auto act_of = [&](int32_t i) { return acts ? acts[i] : LLMCP_Q8_ACT_NONE; };
   if (m > 1) {
-    // one quantization of the input rows, then each weight's GEMM
+    // one quantization of the input rows, then each weight's GEMM (every
+    // weight checked before anything is launched)
+    for (int32_t i = 0; i < count; ++i)
+      if ((rc = gemm_operands_fit(w[i], m))) return rc;
     Workspace ws = ctx_workspace(ctx);
     if (!prequantized && (rc = gemm_quantize(ctx, in, w[0], ws))) return rc;
     for (int32_t i = 0; i < count; ++i)
@@ -1393,6 +1412,8 @@ static int rmsnorm_group_impl(llmcp_q8_ctx *ctx, const Rows &in, const NormWeigh
     if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
     return linear_group_run(ctx, normed, count, w, outs, acts, false);
   }
+  for (int32_t i = 0; i < count; ++i)
+    if ((rc = gemm_operands_fit(w[i], m))) return rc;
   const int64_t nblk = passes_for(in.cols) * kPassBlocks;
   const int64_t row_tiles = (m + 31) / 32;
   Workspace ws = ctx_workspace(ctx);
@@ -1514,6 +1535,7 @@ static int mlp_impl(llmcp_q8_ctx *ctx, const Rows &in,
     // Several rows: the SwiGLU GEMMs of llmcp_q8_swiglu (gate with SiLU,
     // then up with the multiply in its epilogue) into h, then the GEMM of h,
     // with the platform's epilogue as for llmcp_q8_linear.
+    if ((rc = gemm_operands_fit(wg, m)) || (rc = gemm_operands_fit(wd, m))) return rc;
     const int64_t f = wg->rows;
     Rows h;
     if (hidden) {

@@ -168,3 +168,37 @@ def test_microbench_peaks(q8):
             q8.check(q8.lib().llmcp_q8_microbench_epilogue(c.handle, 3, 100, None))
     finally:
         c.close()
+
+
+def test_prefill_operands_over_4gib_declined(q8, oracle):
+    """The prefill GEMM reads its operands at 32-bit offsets (buffer-addressed
+    loads), so a multi-row linear over a weight of 4 GiB or more is declined
+    (LLMCP_Q8_DECLINED: the caller's own path runs) before anything is
+    launched, also for the lm_head, the grouped linears and the MLP; the
+    context stays usable.  The 4.56 GB weight is registered from an
+    uninitialised device buffer: no call computes with it."""
+    rows, cols = 262144, 16384
+    nbytes = rows * cols // 32 * 34
+    assert unit_bytes(rows, cols) >= 1 << 32
+    rng = np.random.default_rng(47)
+    with q8.Context(0) as ctx:
+        big = ctx.register_device_p4(ctx.alloc(nbytes), rows, cols)
+        x = rng.standard_normal((2, cols)).astype(np.float32)
+        xd, yd = ctx.to_device(x), ctx.alloc(2 * rows * 4)
+        with pytest.raises(q8.Declined):
+            ctx.linear(xd, big, yd, 2, mode="prefill")
+        with pytest.raises(q8.Declined):
+            ctx.lm_head(xd, big, yd, 2)
+        with pytest.raises(q8.Declined):
+            ctx.linear_group(xd, [big], [yd], 2)
+        ctx.release(big)
+        # an ordinary prefill linear on the same context afterwards
+        n, k = 64, 512
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        p4 = oracle.pack_q8_0_p4(w)
+        t = ctx.upload_p4(p4, n, k)
+        xs = rng.standard_normal((3, k)).astype(np.float32)
+        xsd, ysd = ctx.to_device(xs), ctx.alloc(3 * n * 4)
+        ctx.linear(xsd, t, ysd, 3, mode="prefill")
+        assert bits_equal(ctx.to_host(ysd, (3, n), np.float32),
+                          oracle.linear(xs, p4, n, epilogue=ctx.epilogue))
