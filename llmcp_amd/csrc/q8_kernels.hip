@@ -1177,8 +1177,8 @@ hipError_t launch_quantize_tiled(const void *x, bool x_bf16, int64_t m,
   return hipGetLastError();
 }
 
-bool gemv_quantizes_input(int64_t rows, int nmat) {
-  return nmat == 2 || rows / kLanes <= kInLoopQuantMaxGroups;
+bool gemv_quantizes_input(int64_t rows, int64_t cols, int nmat) {
+  return nmat == 2 || rows / kLanes <= kInLoopQuantMaxGroups || cols <= kInLoopQuantMaxCols;
 }
 
 

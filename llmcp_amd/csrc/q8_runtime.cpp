@@ -1023,7 +1023,7 @@ static int gemv_common(llmcp_q8_ctx *ctx, const Rows &x, const Tensor *w0,
     ws = ctx_workspace(ctx);
   }
   GemvLaunch l;
-  const bool in_loop = gemv_quantizes_input(w0->rows, w1 ? 2 : 1) &&
+  const bool in_loop = gemv_quantizes_input(w0->rows, w0->cols, w1 ? 2 : 1) &&
                        (uintptr_t)x.data % (x.bf16 ? 8 : 16) == 0;
   if (in_loop) {
     l.x = x.data;
