@@ -1,5 +1,5 @@
-// A C++17 host of the C ABI, written the way llmcp's AOT runtime would use it
-// (INTEGRATION.md's wiring): the library is linked like any C library, the
+// A C++17 host of the C ABI, written the way llmcp's AOT runtime would use it:
+// the library is linked like any C library, the
 // weights come from a mapped single-file arena that llmcp_q8_upload_arena
 // registers, and the MLIR C-interface entries are called with the runtime's
 // own MemRef<T, N> descriptors (include/llmcp/Runtime/AotRuntime.h:52-58),

@@ -338,7 +338,7 @@ def test_column_parallel_variant_is_bit_identical(oracle):
 
 def test_golden_small_case_regression(oracle):
     # Fixture written by tests/golden/make_golden.py from this oracle; keeps the
-    # oracle's outputs fixed across rounds and feeds the GPU parity tests.
+    # oracle's outputs fixed across changes and feeds the GPU parity tests.
     z = np.load(os.path.join(GOLDEN, "q8_small_case.npz"))
     assert np.array_equal(oracle.pack_q8_0_p4(z["w"]), z["p4"])
     qa, sa = oracle.quantize_act_q8_1(z["x"])
