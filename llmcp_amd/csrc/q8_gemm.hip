@@ -19,6 +19,7 @@
 #include <stddef.h>
 
 #include <algorithm>
+#include <atomic>
 #include <utility>
 
 #include "q8_device.h"
@@ -815,19 +816,18 @@ static void launch_gemm_e(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
 #undef LLMCP_GEMM_EPI
 }
 
-// Compute units of the current device (cached per device).
-static int cu_count() {
-  static int cached[64] = {0};
+int cu_count() {
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] <= 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
             hipSuccess || n <= 0)
       n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 template <int WM, int WN, int NST, bool FMA>

@@ -34,6 +34,10 @@ hipError_t launch_selftest_quantizer(unsigned long long *bad, hipStream_t s);
 hipError_t launch_selftest_exp(unsigned long long *out, float *inputs,
                                uint32_t *results, uint32_t cap, hipStream_t s);
 
+// Compute units of the current device (cached per device; 256 if the
+// query fails).
+int cu_count();
+
 // Most weights one grouped GEMV serves (llmcp_q8_linear_group).
 constexpr int kMaxGroup = 8;
 

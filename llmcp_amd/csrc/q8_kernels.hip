@@ -980,81 +980,88 @@ __global__ __launch_bounds__(1024) void argmax_reduce_kernel(
 
 // ---------------------------------------------------------- embedding -- //
 
-// One thread per (token, V columns), a flat grid over tokens x chunks so
-// that every lane has work -- LowerToLinalg.cpp:435-531 gathered from the
-// unit layout.  out = f32(q) * f32(d), exact.  V = 4 for f32 rows (one 4 B
-// word of quants) and 8 for bf16 rows (two words), so that every lane
-// stores 16 B and a wave's stores form one contiguous run; the rows are
-// written once, so the stores are non-temporal.  (One thread per 16
+// One thread per (token, V columns) -- LowerToLinalg.cpp:435-531 gathered
+// from the unit layout.  out = f32(q) * f32(d), exact.  V = 4 for f32 rows
+// (one 4 B word of quants) and 8 for bf16 rows (two words), so that every
+// lane stores 16 B and a wave's stores form one contiguous run; the rows
+// are written once, so the stores are non-temporal.  (One thread per 16
 // columns, 64 B of plain stores per lane, took 6.4 us for 1024 ids of the
-// 248320 x 2560 table against 3.8 us for this form.)
+// 248320 x 2560 table against 3.8 us for this form.)  Workgroups are
+// 256 lanes in two dimensions: x over a row's chunks (64, 128 or 256
+// lanes, chosen by the host so that few lanes idle), y over 256 / x
+// tokens; the grid's y strides over the tokens past what one resident
+// round of workgroups holds.  A
+// thread's column offsets are computed once, and no 64-bit division splits
+// a flat index.
 template <bool BF16>
-__global__ void embedding_kernel(const int64_t *__restrict__ tokens,
-                                 int64_t count, const uint8_t *__restrict__ t,
-                                 int64_t rows, int64_t passes, int64_t chunks,
-                                 void *__restrict__ out, int64_t ldo,
-                                 int32_t *err, int aligned) {
+__global__ __launch_bounds__(256) void embedding_kernel(
+    const int64_t *__restrict__ tokens, int64_t count, const uint8_t *__restrict__ t,
+    int64_t rows, int64_t passes, int32_t chunks, void *__restrict__ out, int64_t ldo,
+    int32_t *err, int aligned) {
   constexpr int V = BF16 ? 8 : 4;
-  const int64_t th = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t ti = th / chunks;
-  const int64_t c = th - ti * chunks;
-  if (ti >= count) return;
-  const int64_t tok = tokens[ti];
-  float v[V];
-  if (tok < 0 || tok >= rows) {
-#pragma unroll
-    for (int e = 0; e < V; ++e) v[e] = 0.0f;
-    if (c == 0) atomicOr(err, 1);
-  } else {
-    const int64_t g = tok >> 2;
-    const int r = (int)(tok & 3);
-    const int64_t col = c * V;
-    const int64_t b = col >> 5;             // block
-    const int h = (int)((col >> 4) & 1);    // its 16-value half
-    const int off = (int)(col & 15);        // first value within the half
-    int64_t u;
-    int j;
-    locate_seg(b, seg_for(passes), u, j);
-    const uint8_t *pass = t + (g * passes + u) * kPassBytes;
-    const uint8_t *qp = pass + h * 1024 + r * 256 + j * 16 + off;
-    uint32_t w[V / 4];
-    if constexpr (BF16) {
-      const uint2 q = *(const uint2 *)qp;
-      w[0] = q.x;
-      w[1] = q.y;
-    } else {
-      w[0] = *(const uint32_t *)qp;
-    }
-    const float d = half_bits_to_float(
-        *(const uint16_t *)(pass + kPassQs + 2 * (16 * r + j)));
-#pragma unroll
-    for (int e = 0; e < V; ++e)
-      v[e] = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * d;
-  }
+  const int c = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  const int64_t t0 = (int64_t)blockIdx.y * blockDim.y + threadIdx.y;
+  const int64_t tstep = (int64_t)gridDim.y * blockDim.y;
+  if (c >= chunks) return;
+  const int64_t col = (int64_t)c * V;
+  const int64_t b = col >> 5;             // block
+  const int h = (int)((col >> 4) & 1);    // its 16-value half
+  const int off = (int)(col & 15);        // first value within the half
+  int64_t u;
+  int j;
+  locate_seg(b, seg_for(passes), u, j);
+  // byte offsets inside a lane group's passes (row r adds r * 256 / 32)
+  const int64_t q_off = u * kPassBytes + h * 1024 + j * 16 + off;
+  const int64_t d_off = u * kPassBytes + kPassQs + 2 * j;
   typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-  if constexpr (BF16) {
-    // truncf to a bf16 result (LowerToLinalg.cpp:435-531)
-    uint16_t *o = (uint16_t *)out + ti * ldo + c * V;
-    if (aligned) {
-      v4u p;
+  for (int64_t ti = t0; ti < count; ti += tstep) {
+    const int64_t tok = tokens[ti];
+    float v[V];
+    if (tok < 0 || tok >= rows) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        p[e] = (uint32_t)float_to_bf16(v[2 * e]) |
-               ((uint32_t)float_to_bf16(v[2 * e + 1]) << 16);
-      __builtin_nontemporal_store(p, (v4u *)o);
+      for (int e = 0; e < V; ++e) v[e] = 0.0f;
+      if (c == 0) atomicOr(err, 1);
     } else {
+      const uint8_t *grp = t + (tok >> 2) * passes * kPassBytes;
+      const int r = (int)(tok & 3);
+      const uint8_t *qp = grp + q_off + r * 256;
+      uint32_t w[V / 4];
+      if constexpr (BF16) {
+        const uint2 q = *(const uint2 *)qp;
+        w[0] = q.x;
+        w[1] = q.y;
+      } else {
+        w[0] = *(const uint32_t *)qp;
+      }
+      const float d = half_bits_to_float(*(const uint16_t *)(grp + d_off + 32 * r));
 #pragma unroll
-      for (int e = 0; e < V; ++e) o[e] = float_to_bf16(v[e]);
+      for (int e = 0; e < V; ++e)
+        v[e] = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * d;
     }
-  } else {
-    float *o = (float *)out + ti * ldo + c * V;
-    if (aligned) {
-      const v4u p = {__float_as_uint(v[0]), __float_as_uint(v[1]),
-                     __float_as_uint(v[2]), __float_as_uint(v[3])};
-      __builtin_nontemporal_store(p, (v4u *)o);
-    } else {
+    if constexpr (BF16) {
+      // truncf to a bf16 result (LowerToLinalg.cpp:435-531)
+      uint16_t *o = (uint16_t *)out + ti * ldo + col;
+      if (aligned) {
+        v4u p;
 #pragma unroll
-      for (int e = 0; e < V; ++e) o[e] = v[e];
+        for (int e = 0; e < 4; ++e)
+          p[e] = (uint32_t)float_to_bf16(v[2 * e]) |
+                 ((uint32_t)float_to_bf16(v[2 * e + 1]) << 16);
+        __builtin_nontemporal_store(p, (v4u *)o);
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[e] = float_to_bf16(v[e]);
+      }
+    } else {
+      float *o = (float *)out + ti * ldo + col;
+      if (aligned) {
+        const v4u p = {__float_as_uint(v[0]), __float_as_uint(v[1]),
+                       __float_as_uint(v[2]), __float_as_uint(v[3])};
+        __builtin_nontemporal_store(p, (v4u *)o);
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[e] = v[e];
+      }
     }
   }
 }
@@ -1323,14 +1330,31 @@ hipError_t launch_embedding(const int64_t *tokens, int64_t count,
   const int aligned = out_bf16
       ? ((uintptr_t)out % 16 == 0) && (ldo % 8 == 0)
       : ((uintptr_t)out % 16 == 0) && (ldo % 4 == 0);
-  const dim3 grid(grid_for(chunks * count, 256));
+  // a row's chunks over the widest x (256, 128 or 64 lanes) that leaves
+  // the fewest lanes idle, 256 / x tokens per workgroup
+  int bs = 256;
+  for (int cand : {128, 64}) {
+    const int64_t waste = (chunks + cand - 1) / cand * cand - chunks;
+    if (waste < (chunks + bs - 1) / bs * bs - chunks) bs = cand;
+  }
+  // At most eight workgroups per CU (32 waves, all resident at once; the
+  // y stride hands a thread further tokens): 1024 f32 rows of 2560 values,
+  // 2560 workgroups of one token pair each, took 4.51 us against 4.26 with
+  // 2045 (and 4.66 with 1020).
+  const int by = 256 / bs;
+  const int64_t gx = (chunks + bs - 1) / bs;
+  const int64_t ty = (count + by - 1) / by;
+  int64_t ycap = std::max<int64_t>(1, 8 * (int64_t)cu_count() / gx);
+  ycap = std::min<int64_t>(ycap, 65535);
+  const dim3 grid((unsigned)gx, (unsigned)std::min(ty, ycap));
+  const dim3 block(bs, by);
   if (out_bf16)
-    hipLaunchKernelGGL((embedding_kernel<true>), grid, dim3(256), 0, s, tokens,
-                       count, table, rows, passes_for(cols), chunks, out, ldo,
+    hipLaunchKernelGGL((embedding_kernel<true>), grid, block, 0, s, tokens,
+                       count, table, rows, passes_for(cols), (int32_t)chunks, out, ldo,
                        err_flag, aligned ? 1 : 0);
   else
-    hipLaunchKernelGGL((embedding_kernel<false>), grid, dim3(256), 0, s, tokens,
-                       count, table, rows, passes_for(cols), chunks, out, ldo,
+    hipLaunchKernelGGL((embedding_kernel<false>), grid, block, 0, s, tokens,
+                       count, table, rows, passes_for(cols), (int32_t)chunks, out, ldo,
                        err_flag, aligned ? 1 : 0);
   return hipGetLastError();
 }
