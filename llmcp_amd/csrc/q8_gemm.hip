@@ -53,13 +53,14 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // cross-wave hand-off is an explicit vmcnt wait plus s_barrier.
 // When the tiles outnumber the resident workgroups, workgroups are
 // persistent and the ring runs on from one tile into the next (PERSIST).
-// PROD (the four-wave 64 x 64 shape for up to 64 rows, when its workgroups
-// fit one per CU): four more waves per workgroup issue all the DMA ops, so
-// the compute waves, alone on their SIMDs, spend no issue slots on them
-// (M = 64, N = 9216, K = 2560: op 18.4 -> 16.5 us).
+// PROD (when the workgroups fit one per CU, not persistent): four more
+// waves per workgroup issue all the DMA ops, so the compute waves spend no
+// issue slots on them (N = 9216, K = 2560: op 18.4 -> 16.5 us at M = 64 on
+// the four-wave 64 x 64 shape, 32.3 -> 31.4 at M = 256 on the twelve-wave
+// 128 x 96 one, whose compute waves then fit 128 VGPRs).
 constexpr int kStageBlocks = 4;
 
-template <int WM, int WN, int SEG>
+template <int WM, int WN, int SEG, int NI = WM * WN>
 struct GemmStage {
   static constexpr int W = WM * WN;
   // DMA ops of a stage.  16 B per lane (1 KiB per op): the A tiles (row
@@ -80,8 +81,9 @@ struct GemmStage {
   // divide evenly, waves repeat another wave's op (same bytes, same place).
   static constexpr int T16 = CA + CB + CS + CD16;
   static constexpr int T4 = CD4;
-  static constexpr int S16 = (T16 + W - 1) / W;
-  static constexpr int S4 = (T4 + W - 1) / W;
+  // NI waves issue the ops: the W compute waves, or the producer waves
+  static constexpr int S16 = (T16 + NI - 1) / NI;
+  static constexpr int S4 = (T4 + NI - 1) / NI;
   static constexpr int OPS = S16 + S4;  // DMA instructions per wave and stage
   __align__(16) int8_t a[WM][kStageBlocks][1024];
   __align__(16) int8_t b[WN][4 * 1024];
@@ -171,19 +173,22 @@ struct Seg6 {
 // are ignored and the stage arithmetic folds as for one split.
 template <int WM, int WN, int NST, bool FMA, int SEG, int EPI, bool PERSIST, bool KSPLIT,
           bool PROD>
-__global__ __launch_bounds__(64 * WM * WN * (PROD ? 2 : 1))
-__attribute__((amdgpu_waves_per_eu(WM * WN >= 12 ? 3 : 2)))
+__global__ __launch_bounds__(64 * (WM * WN + (PROD ? 4 : 0)))
+__attribute__((amdgpu_waves_per_eu((WM * WN + (PROD ? 4 : 0) + 3) / 4 > 2
+                                       ? (WM * WN + (PROD ? 4 : 0) + 3) / 4 : 2)))
 void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
                  int32_t row_tiles, int32_t nblk, const uint8_t *__restrict__ w,
                  int64_t n_rows, int64_t m_rows, int32_t passes, int32_t m_tiles,
                  int32_t n_tiles, void *y, int64_t ldy, const void *mul,
                  int64_t ldg, int32_t splits_arg, int64_t split_stride) {
-  typedef GemmStage<WM, WN, SEG> St;
+  constexpr int W = WM * WN;
+  constexpr int P = PROD ? 4 : 0;      // producer waves
+  constexpr int NI = PROD ? P : W;     // waves that issue the DMA ops
+  typedef GemmStage<WM, WN, SEG, NI> St;
   static_assert(!(KSPLIT && PERSIST), "K splits run one tile per workgroup");
   static_assert(!(PROD && PERSIST), "producer waves serve one tile per workgroup");
   const int32_t splits = KSPLIT ? splits_arg : 1;
   static_assert(NST == 2 || NST == 4, "stage buffers");
-  constexpr int W = WM * WN;
   constexpr int BM = 32 * WM, BN = 32 * WN;
   // one LDS object per stage buffer (see above)
   __shared__ St st0, st1, st2, st3, st4;
@@ -236,12 +241,14 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
                      (kPassBlocks / kStageBlocks);
 
   const int lane = threadIdx.x & 63;
-  // PROD: waves W..2W-1 are producers; producer p issues the DMA ops that
-  // compute wave p would issue without them (the same op list).
+  // PROD: waves W..W+3 are producers and issue every DMA op (op lists
+  // strided over the four of them); the compute waves issue none.
   const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool producer = PROD && wave_all >= W;
-  const int wave = producer ? wave_all - W : wave_all;
+  const int wave = producer ? 0 : wave_all;               // compute wave
+  const int iw = PROD ? (producer ? wave_all - W : 0) : wave_all;  // issuer
   __builtin_assume(wave >= 0 && wave < W);
+  __builtin_assume(iw >= 0 && iw < NI);
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane & 31, lh = lane >> 5;
   const int64_t wrow = (int64_t)passes * kPassBytes;  // bytes per lane group
@@ -260,7 +267,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   const int q4 = lane >> 2;
 #pragma unroll
   for (int u = 0; u < St::S16; ++u) {
-    int o = wave + u * W;
+    int o = iw + u * NI;
     if (o >= St::T16) o -= St::T16;
     abb[u] = o % kStageBlocks;
     piece16[u] = 0;
@@ -298,7 +305,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
   }
 #pragma unroll
   for (int u = 0; u < St::S4; ++u) {
-    int o = wave + u * W;
+    int o = iw + u * NI;
     if (o >= St::T4) o -= St::T4;
     // S > 1, column tile o/2, block 2(o%2) + lh of the stage, one f16 per
     // dword
@@ -322,7 +329,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     Offsets of;
 #pragma unroll
     for (int u = 0; u < St::S16; ++u) {
-      int o = wave + u * W;
+      int o = iw + u * NI;
       if (o >= St::T16) o -= St::T16;
       if (kind[u] == K_A) {
         const int64_t rt = min((int64_t)mt * WM + o / kStageBlocks, (int64_t)row_tiles - 1);
@@ -348,7 +355,7 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
     }
 #pragma unroll
     for (int u = 0; u < St::S4; ++u) {
-      int o = wave + u * W;
+      int o = iw + u * NI;
       if (o >= St::T4) o -= St::T4;
       const int64_t n = min(nn0 + 32 * (o / 2) + li, n_rows - 1);
       of.o4[u] = (uint32_t)((n >> 2) * wrow + kPassQs + 32 * (n & 3) +
@@ -596,18 +603,24 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
       // buffer of the stage just consumed is free.  Stage s: the second
       // half of stage s+3 (into the buffer freed at stage s-1's barrier),
       // the wait for stage s+1, the barrier, the first half of stage s+4
-      // (into stage s's buffer).
+      // (into stage s's buffer); past the tile's last stage, the last stage
+      // again (into buffers nobody reads).
+      // the ring's four buffers by a runtime index (stage() would also
+      // reference the unused fifth)
+      auto ring = [&](int i) __attribute__((always_inline)) -> St & {
+        return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3;
+      };
       prologue_dma();
       stage_barrier();
       for (int s = 0; s < stages; ++s) {
         const int i = s & (NST - 1);
-        St &abuf = stage((i + NST - 1) & (NST - 1));
+        St &abuf = ring((i + NST - 1) & (NST - 1));
         static_for<St::OPS>([&](auto J) __attribute__((always_inline)) {
           if constexpr (decltype(J)::value >= kHalf) issue_op(min(s + NST - 1, last), abuf, J, cur);
         });
         wait_vmcnt<kMidOps>();
         stage_barrier();
-        St &bbuf = stage(i);
+        St &bbuf = ring(i);
         static_for<St::OPS>([&](auto J) __attribute__((always_inline)) {
           if constexpr (decltype(J)::value < kHalf) issue_op(min(s + NST, last), bbuf, J, cur);
         });
@@ -817,14 +830,21 @@ static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
   // the epilogue's second operand: the SwiGLU gate or the residual
   const void *mp = (EPI & 16) != 0 ? l.add : (const void *)l.mul;
   const int64_t ld = (EPI & 16) != 0 ? l.ldr : l.ldg;
-  // producer waves: the four-wave shape when its workgroups fit one per CU
-  constexpr bool kProd = WM * WN == 4;
+  // producer waves: when the workgroups fit one per CU (not persistent).
+  // With the twelve-wave shape the compute waves are held to 128 VGPRs,
+  // which spills inside the stage loop except for the fma epilogue with
+  // S = 1 and no SwiGLU multiply or residual (M = 1024, N = 2560,
+  // K = 9216, S = 6, measured 2 % slower with them), so only that form
+  // takes them there.
+  constexpr bool kProd =
+      WM * WN == 4 || (WM * WN == 12 && FMA && SEG == 1 && (EPI & 24) == 0);
   const bool prod = kProd && total <= (unsigned)cu_count();
+  constexpr int kThreads = 64 * WM * WN, kThreadsP = 64 * (WM * WN + 4);
   if (splits > 1) {
     if constexpr (EPI == 0) {
       if (prod)
         hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, 0, false, true, kProd>), dim3(total),
-                           dim3(128 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
+                           dim3(kThreadsP), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
                            l.w, l.rows, l.m, passes, m_tiles, n_tiles, y, ldy,
                            mp, ld, splits, stride);
       else
@@ -835,12 +855,12 @@ static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
     }
   } else if (kPersist && grid < total) {
     hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, kPersist, false, false>), dim3(grid),
-                       dim3(64 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
+                       dim3(kThreads), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
                        l.w, l.rows, l.m, passes, m_tiles, n_tiles, y, ldy,
                        mp, ld, 1, 0);
   } else if (prod) {
     hipLaunchKernelGGL((gemm_kernel<WM, WN, NST, FMA, SEG, EPI, false, false, kProd>), dim3(total),
-                       dim3(128 * WM * WN), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
+                       dim3(kThreadsP), 0, s, l.qa, l.sa, l.row_tiles, l.nblk,
                        l.w, l.rows, l.m, passes, m_tiles, n_tiles, y, ldy,
                        mp, ld, 1, 0);
   } else {
