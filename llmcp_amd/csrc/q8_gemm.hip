@@ -604,9 +604,9 @@ void gemm_kernel(const int8_t *__restrict__ qa, const float *__restrict__ sa,
       // half of stage s+3 (into the buffer freed at stage s-1's barrier),
       // the wait for stage s+1, the barrier, the first half of stage s+4
       // (into stage s's buffer); past the tile's last stage, the last stage
-      // again (into buffers nobody reads).
-      // the ring's four buffers by a runtime index (stage() would also
-      // reference the unused fifth)
+      // again (into buffers nobody reads).  ring() selects the four ring
+      // buffers by a runtime index (stage() would also reference the
+      // unused fifth, and allocate it).
       auto ring = [&](int i) __attribute__((always_inline)) -> St & {
         return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3;
       };
