@@ -52,9 +52,11 @@ def sample_rows(m):
 
 
 # (m, n, k): configs[3] at M = 64 and 256, the model's other K classes
-# (K = 9216: segmented layout; K = 4096), odd row counts and N tails.
+# (K = 9216: segmented layout; K = 4096), odd row counts and N tails;
+# (200, 2560, 2560) puts the 128 x 96 workgroups' K splits on one
+# workgroup per CU, with the producer waves.
 SHAPES = [(64, 9216, 2560), (256, 9216, 2560), (2, 136, 1024), (33, 520, 2560),
-          (97, 2560, 9216), (40, 264, 4096), (130, 7680, 2560)]
+          (97, 2560, 9216), (40, 264, 4096), (130, 7680, 2560), (200, 2560, 2560)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
