@@ -832,12 +832,11 @@ static void launch_gemm_k(const GemmLaunch &l, int32_t passes, int32_t m_tiles,
   const int64_t ld = (EPI & 16) != 0 ? l.ldr : l.ldg;
   // producer waves: when the workgroups fit one per CU (not persistent).
   // With the twelve-wave shape the compute waves are held to 128 VGPRs,
-  // which spills inside the stage loop except for the fma epilogue with
-  // S = 1 and no SwiGLU multiply or residual (M = 1024, N = 2560,
-  // K = 9216, S = 6, measured 2 % slower with them), so only that form
-  // takes them there.
+  // which spills inside the stage loop except with S = 1 and no SwiGLU
+  // multiply or residual (M = 1024, N = 2560, K = 9216, S = 6, measured 2 %
+  // slower with them), so only that form takes them there.
   constexpr bool kProd =
-      WM * WN == 4 || (WM * WN == 12 && FMA && SEG == 1 && (EPI & 24) == 0);
+      WM * WN == 4 || (WM * WN == 12 && SEG == 1 && (EPI & 24) == 0);
   const bool prod = kProd && total <= (unsigned)cu_count();
   constexpr int kThreads = 64 * WM * WN, kThreadsP = 64 * (WM * WN + 4);
   if (splits > 1) {
